@@ -1,0 +1,186 @@
+/*
+ * llrs.h -- C ABI of the MI355X (gfx950) HIP backend for llama.rs's batch-1
+ * decode path.
+ *
+ * Conventions: every function returning int returns LLRS_OK (0) on success or
+ * a negative LLRS_E_* code; llrs_last_error() then holds a message for the
+ * calling thread.  No C++ exception or unwinding crosses this boundary (the
+ * reference builds with panic = "abort", Cargo.toml:20).  All pointers are
+ * plain host pointers unless a name ends in _dev.  Handles are not
+ * thread-safe: one thread drives a backend at a time, as the reference's
+ * engine drives its model (src/engine.rs:36-50).
+ */
+#ifndef LLRS_H
+#define LLRS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLRS_OK 0
+#define LLRS_E_INVALID -1   /* bad argument, shape or length (anyhow::ensure! in the reference) */
+#define LLRS_E_UNSUPPORTED -2 /* unknown GGML type, architecture or option */
+#define LLRS_E_HIP -3       /* HIP runtime failure */
+#define LLRS_E_OOM -4       /* device or host allocation failure */
+#define LLRS_E_IO -5        /* file open / read / write failure */
+#define LLRS_E_FORMAT -6    /* malformed GGUF file */
+
+/* GGML tensor type ids: QuantType::from_ggml_type (src/quant.rs:27-44). */
+enum llrs_ggml_type {
+  LLRS_F32 = 0, LLRS_F16 = 1, LLRS_Q4_0 = 2, LLRS_Q4_1 = 3, LLRS_Q5_0 = 6, LLRS_Q5_1 = 7,
+  LLRS_Q8_0 = 8, LLRS_Q4_K = 12, LLRS_Q5_K = 13, LLRS_Q6_K = 14, LLRS_BF16 = 30
+};
+
+/* LogitsMode (src/architecture.rs:35-39). */
+enum llrs_logits_mode { LLRS_LOGITS_SKIP = 0, LLRS_LOGITS_COMPUTE = 1 };
+
+/* LoadQuantization (src/loader.rs:16-25). */
+enum llrs_quantization { LLRS_QUANT_NONE = 0, LLRS_QUANT_Q4K = 1, LLRS_QUANT_Q4KM = 2 };
+
+typedef struct llrs_backend llrs_backend;
+typedef struct llrs_tensor llrs_tensor;
+typedef struct llrs_model llrs_model;
+typedef struct llrs_kv llrs_kv;
+
+/* Thread-local message for the last failed call on this thread ("" if none). */
+const char *llrs_last_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* Backend: replaces CpuBackend::new / KernelBackend::{name, threads}        */
+/* (src/backend.rs:48-65, 67-73, 97-121, 134-141).                           */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+  int device;      /* HIP device ordinal */
+  uint32_t flags;  /* reserved, must be 0 */
+} llrs_backend_config;
+
+int llrs_backend_create(const llrs_backend_config *cfg, llrs_backend **out);
+void llrs_backend_destroy(llrs_backend *b);
+/* KernelBackend::name (src/backend.rs:70): "hip-gfx950". */
+const char *llrs_backend_name(const llrs_backend *b);
+/* KernelBackend::threads (src/backend.rs:71): the device's compute-unit count. */
+size_t llrs_backend_threads(const llrs_backend *b);
+/* Blocks the host until all work queued by this backend has finished. */
+int llrs_backend_synchronize(llrs_backend *b);
+
+/* ------------------------------------------------------------------------ */
+/* Tensors: QuantTensor::from_owned / from_mmap (src/quant.rs:114-157).      */
+/* The native GGUF block bytes are copied once to HBM, block layout intact.  */
+/* ------------------------------------------------------------------------ */
+/* Validates the byte length exactly as QuantTensor::from_data
+ * (src/quant.rs:132-157): cols % block_size == 0 and
+ * nbytes == rows*cols/block_size*type_size.  rows == 0 is allowed (empty). */
+int llrs_tensor_upload(llrs_backend *b, const void *bytes, size_t nbytes, uint32_t ggml_type,
+                       size_t rows, size_t cols, llrs_tensor **out);
+void llrs_tensor_free(llrs_tensor *t);
+int llrs_tensor_info(const llrs_tensor *t, uint32_t *ggml_type, size_t *rows, size_t *cols,
+                     size_t *nbytes);
+/* Copies the tensor's native bytes back to the host (nbytes must match). */
+int llrs_tensor_download(const llrs_tensor *t, void *out, size_t nbytes);
+
+/* KernelBackend::matvec (src/backend.rs:72, 143-162) with validate_matvec's
+ * checks (src/quant.rs:303-318): nx == cols, ny == rows, tensor is 2-D.
+ * Host input and output; synchronous; y is fully overwritten. */
+int llrs_matvec(llrs_backend *b, const llrs_tensor *w, const float *x, size_t nx, float *y,
+                size_t ny);
+/* The same on device pointers, enqueued on the backend's stream (asynchronous). */
+int llrs_matvec_dev(llrs_backend *b, const llrs_tensor *w, const float *x_dev, float *y_dev);
+/* QuantTensor::row_into (src/quant.rs:261-272): dequantize row `row` into out[n]
+ * (n must equal cols); the bit-exact test hook for value_at. */
+int llrs_dequant_row(llrs_backend *b, const llrs_tensor *w, size_t row, float *out, size_t n);
+
+/* Device scratch helpers for the _dev entry points and benchmarks. */
+int llrs_device_alloc(llrs_backend *b, size_t nbytes, void **out_dev);
+int llrs_device_free(llrs_backend *b, void *dev);
+int llrs_copy_h2d(llrs_backend *b, void *dst_dev, const void *src, size_t nbytes);
+int llrs_copy_d2h(llrs_backend *b, void *dst, const void *src_dev, size_t nbytes);
+
+/* Host-side quantizers, QuantTensor::quantize_* (src/quant.rs:187-259,
+ * 650-967) including their fallbacks (Q4_K -> Q5_0 -> F32, Q6_K -> Q8_0).
+ * ggml_type selects the entry point (LLRS_Q4_K, LLRS_Q5_0, LLRS_Q8_0,
+ * LLRS_Q6_K); *out_type receives the type actually produced.  If out is NULL
+ * the required size is returned in *out_nbytes. */
+int llrs_quantize(uint32_t ggml_type, const float *values, size_t rows, size_t cols, void *out,
+                  size_t out_capacity, size_t *out_nbytes, uint32_t *out_type);
+
+/* GgufFile::open + GgufFile::tensor (src/gguf.rs:78-215): reads one tensor of
+ * a GGUF v2/v3 file with every header/range check of the reader.  Shape is
+ * reported as the reference does ([rows, cols] = [dims[1], dims[0]]; rows = 1
+ * for a 1-D tensor).  If out is NULL only the metadata is returned. */
+int llrs_gguf_read_tensor(const char *path, const char *name, uint32_t *version,
+                          uint32_t *ggml_type, size_t *rows, size_t *cols, void *out,
+                          size_t out_capacity, size_t *nbytes);
+
+/* ------------------------------------------------------------------------ */
+/* Model: ModelLoader::load_dynamic -> GgufLoader::load (src/loader.rs:37-42, */
+/* 233-399), CausalModel (src/architecture.rs:42-78).                        */
+/* ------------------------------------------------------------------------ */
+/* LlamaConfig (src/config.rs:18-55) as loaded. */
+typedef struct {
+  size_t hidden_size, intermediate_size, num_attention_heads, num_key_value_heads,
+      num_hidden_layers, vocab_size, max_position_embeddings, head_dim, kv_width;
+  float rms_norm_eps, rope_theta;
+  int tie_word_embeddings;
+} llrs_model_config;
+
+/* Loads a GGUF v2/v3 Qwen2 file: metadata -> config, tensors uploaded to HBM
+ * verbatim (quantization = LLRS_QUANT_NONE) or quantized at load time with
+ * the reference's q4k / q4km recipe when the file holds F32/F16/BF16
+ * matrices (src/loader.rs:406-447). */
+int llrs_model_load_gguf(llrs_backend *b, const char *path, int quantization, llrs_model **out);
+void llrs_model_free(llrs_model *m);
+int llrs_model_config_get(const llrs_model *m, llrs_model_config *out);
+/* Bytes of weights the decode step streams per token (all matrices incl.
+ * the LM head, plus one embedding row, norms and biases). */
+size_t llrs_model_weight_bytes(const llrs_model *m);
+
+/* Synthetic Qwen2 models (random-init from a seed, quantized with a recipe). */
+typedef struct {
+  size_t hidden_size, intermediate_size, num_attention_heads, num_key_value_heads,
+      num_hidden_layers, vocab_size, max_position_embeddings;
+  float rms_norm_eps, rope_theta;
+  int tie_word_embeddings;
+  int recipe;       /* LLRS_QUANT_Q4KM, LLRS_QUANT_Q4K, or LLRS_QUANT_NONE (F32) */
+  uint64_t seed;
+  float weight_std; /* N(0, weight_std) weights and biases; norm gains 1 + N(0, weight_std) */
+  int threads;      /* host threads for generation; 0 = all */
+} llrs_synth_config;
+/* Writes a GGUF v3 file with the synthetic model (pre-quantized tensors). */
+int llrs_synth_write_gguf(const llrs_synth_config *cfg, const char *path);
+/* Builds the same model directly in HBM without a file. */
+int llrs_model_synthetic(llrs_backend *b, const llrs_synth_config *cfg, llrs_model **out);
+
+/* KVCache::new + InferenceBuffers::new (src/cache.rs:13-36, 80-101): a
+ * device-resident f32 KV cache, layout [layer][pos][kv_width] as the
+ * reference's, plus device activation buffers.  Fails if max_seq_len is 0 or
+ * exceeds max_position_embeddings (src/cache.rs:14-19). */
+int llrs_kv_create(llrs_model *m, size_t max_seq_len, llrs_kv **out);
+void llrs_kv_free(llrs_kv *kv);
+/* KVCache::reset (src/cache.rs:55-57): a no-op, positions are overwritten before read. */
+int llrs_kv_reset(llrs_kv *kv);
+
+/* CausalModel::forward_token (src/architecture.rs:47-54; src/model.rs:135-271).
+ * Fails if token >= vocab or pos >= max_seq_len (src/model.rs:145-153). */
+int llrs_forward_token(llrs_model *m, llrs_kv *kv, uint32_t token, size_t pos, int logits_mode);
+/* CausalModel::prefill (src/architecture.rs:60-77): logits only for the last token. */
+int llrs_prefill(llrs_model *m, llrs_kv *kv, const uint32_t *tokens, size_t n, size_t start_pos);
+/* The decode loop of InferenceEngine::benchmark_tokens (src/engine.rs:205-216):
+ * n_steps x { token = argmax(current logits); forward_token(token, start_pos+i) },
+ * replayed from one captured hipGraph with token and position kept on the
+ * device.  out_tokens[i] receives the token fed at start_pos + i. */
+int llrs_decode_greedy(llrs_model *m, llrs_kv *kv, size_t start_pos, size_t n_steps,
+                       uint32_t *out_tokens);
+/* argmax_current_logits (src/engine.rs:233-241) of the current device logits. */
+int llrs_argmax(llrs_kv *kv, uint32_t *out_token);
+/* Readback for tests: InferenceBuffers::logits (src/cache.rs:76) and
+ * KVCache::{k,v}_cache[layer][0 .. n) (src/cache.rs:5-7). */
+int llrs_read_logits(llrs_kv *kv, float *out, size_t n);
+int llrs_read_kv(llrs_kv *kv, size_t layer, int which /*0 = K, 1 = V*/, float *out, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

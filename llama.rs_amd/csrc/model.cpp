@@ -1,0 +1,664 @@
+// Qwen2 model on the GPU: loader, device KV cache, per-token step, hipGraph
+// decode loop (the C ABI model half of include/llrs.h).
+//
+//   llrs_model_load_gguf   GgufLoader::load (src/loader.rs:233-399) incl.
+//                          maybe_quantize (406-447) and load_gguf_* (497-534)
+//   llrs_kv_create         KVCache::new + InferenceBuffers::new (src/cache.rs:13-101)
+//   llrs_forward_token     Qwen2Model::forward_impl (src/model.rs:135-271)
+//   llrs_prefill           CausalModel::prefill (src/architecture.rs:60-77)
+//   llrs_decode_greedy     InferenceEngine::benchmark_tokens' decode loop
+//                          (src/engine.rs:205-216) + argmax (233-241)
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "decode.h"
+#include "gemv.h"
+#include "gguf.h"
+#include "quantize.h"
+#include "synth.h"
+
+namespace llrs {
+
+struct DevLayer {
+  llrs_tensor *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr, *gate = nullptr,
+              *up = nullptr, *down = nullptr;
+  float *attn_norm = nullptr, *ffn_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+};
+
+}  // namespace llrs
+
+struct llrs_model {
+  llrs_backend *b = nullptr;
+  llrs_model_config cfg{};
+  llrs_tensor *embed = nullptr, *lm_head = nullptr;
+  float *norm = nullptr;
+  std::vector<llrs::DevLayer> layers;
+  std::vector<llrs_tensor *> tensors;
+  std::vector<void *> vecs;
+  size_t weight_bytes = 0;
+};
+
+struct llrs_kv {
+  llrs_model *m = nullptr;
+  size_t max_seq_len = 0;
+  float *k_cache = nullptr, *v_cache = nullptr;  // [layer][pos][kv_width]
+  float *hidden = nullptr, *residual = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
+        *attn = nullptr, *gate = nullptr, *up = nullptr, *act = nullptr, *logits = nullptr,
+        *scores = nullptr, *rope = nullptr;
+  int *pos = nullptr;
+  uint32_t *tok_by_pos = nullptr, *next_token = nullptr;
+  uint32_t *pinned = nullptr;  // host staging, max_seq_len + 2 words
+  hipGraph_t graph[2] = {nullptr, nullptr};
+  hipGraphExec_t exec[2] = {nullptr, nullptr};
+  std::vector<void *> allocs;
+};
+
+namespace llrs {
+
+using Fetch = std::function<int(const std::string &name, bool &present, uint32_t &type,
+                                std::vector<uint64_t> &dims, const uint8_t *&data, size_t &nbytes,
+                                std::vector<uint8_t> &storage)>;
+
+static int dev_alloc(std::vector<void *> &list, void **p, size_t bytes) {
+  LLRS_HIP(hipMalloc(p, bytes ? bytes : 4));
+  list.push_back(*p);
+  return LLRS_OK;
+}
+
+// LlamaConfig::validate (src/config.rs:57-89), with head_dim = hidden / heads.
+static int validate_config(llrs_model_config &c) {
+  if (!c.hidden_size || !c.intermediate_size || !c.num_attention_heads || !c.num_key_value_heads ||
+      !c.num_hidden_layers || !c.vocab_size)
+    return set_error(LLRS_E_INVALID, "invalid Qwen2 config: dimensions must be non-zero");
+  if (c.hidden_size % c.num_attention_heads)
+    return set_error(LLRS_E_INVALID, "hidden_size must be divisible by num_attention_heads");
+  if (c.num_attention_heads % c.num_key_value_heads)
+    return set_error(LLRS_E_INVALID,
+                     "num_attention_heads must be divisible by num_key_value_heads");
+  c.head_dim = c.hidden_size / c.num_attention_heads;
+  c.kv_width = c.num_key_value_heads * c.head_dim;
+  if (c.head_dim % 2) return set_error(LLRS_E_INVALID, "Qwen2 RoPE requires an even head_dim");
+  if (!std::isfinite(c.rms_norm_eps) || c.rms_norm_eps <= 0)
+    return set_error(LLRS_E_INVALID, "rms_norm_eps must be finite and positive");
+  if (!std::isfinite(c.rope_theta) || c.rope_theta <= 0)
+    return set_error(LLRS_E_INVALID, "rope_theta must be finite and positive");
+  return LLRS_OK;
+}
+
+static void host_to_f32(uint32_t ty, const uint8_t *src, size_t n, float *dst) {
+  for (size_t i = 0; i < n; i++) {
+    if (ty == LLRS_F32) memcpy(&dst[i], src + 4 * i, 4);
+    else if (ty == LLRS_F16) dst[i] = f16_bits_to_f32_host((uint16_t)(src[2 * i] | (src[2 * i + 1] << 8)));
+    else {
+      uint32_t b = (uint32_t)(src[2 * i] | (src[2 * i + 1] << 8)) << 16;
+      if (((b >> 16) & 0x7fffu) > 0x7f80u) b |= 0x00400000u;
+      memcpy(&dst[i], &b, 4);
+    }
+  }
+}
+
+// load_gguf_matrix + check_matrix + maybe_quantize (src/loader.rs:406-456, 497-507).
+static int load_matrix(llrs_model *m, const Fetch &fetch, const std::string &name, size_t rows,
+                       size_t cols, int quantization, llrs_tensor **out) {
+  bool present = false;
+  uint32_t ty = 0;
+  std::vector<uint64_t> dims;
+  const uint8_t *data = nullptr;
+  size_t nbytes = 0;
+  std::vector<uint8_t> storage;
+  LLRS_TRY(fetch(name, present, ty, dims, data, nbytes, storage));
+  if (!present) return set_error(LLRS_E_INVALID, "missing GGUF tensor %s", name.c_str());
+  if (dims.size() > 2)
+    return set_error(LLRS_E_INVALID, "tensor %s has %zu dimensions; Qwen2 loader supports 1D/2D weights",
+                     name.c_str(), dims.size());
+  size_t r = dims.size() == 2 ? dims[1] : 0, c = dims[0];
+  if (dims.size() != 2 || r != rows || c != cols)
+    return set_error(LLRS_E_INVALID, "tensor %s has shape [%zu, %zu], expected [%zu, %zu]",
+                     name.c_str(), dims.size() == 2 ? r : c, dims.size() == 2 ? c : (size_t)0,
+                     rows, cols);
+  std::vector<uint8_t> qbuf;
+  if (quantization != LLRS_QUANT_NONE &&
+      (ty == LLRS_F32 || ty == LLRS_F16 || ty == LLRS_BF16)) {
+    std::vector<float> vals(rows * cols);
+    host_to_f32(ty, data, rows * cols, vals.data());
+    uint32_t want = recipe_type(quantization, name, cols);
+    if (want == LLRS_F32) {
+      qbuf.resize(vals.size() * 4);
+      memcpy(qbuf.data(), vals.data(), qbuf.size());
+      ty = LLRS_F32;
+    } else {
+      ty = quantize_rows(want, vals.data(), rows, cols, qbuf);
+    }
+    data = qbuf.data();
+    nbytes = qbuf.size();
+  }
+  llrs_tensor *t = nullptr;
+  LLRS_TRY(llrs_tensor_upload(m->b, data, nbytes, ty, rows, cols, &t));
+  m->tensors.push_back(t);
+  *out = t;
+  return LLRS_OK;
+}
+
+// load_gguf_vector (src/loader.rs:509-517): any type, dequantized bit-exactly
+// (value_at) on the device into an f32 vector.
+static int load_vector(llrs_model *m, const Fetch &fetch, const std::string &name, size_t len,
+                       bool zeros_if_missing, float **out) {
+  bool present = false;
+  uint32_t ty = 0;
+  std::vector<uint64_t> dims;
+  const uint8_t *data = nullptr;
+  size_t nbytes = 0;
+  std::vector<uint8_t> storage;
+  LLRS_TRY(fetch(name, present, ty, dims, data, nbytes, storage));
+  LLRS_TRY(dev_alloc(m->vecs, (void **)out, len * 4));
+  if (!present) {
+    if (!zeros_if_missing) return set_error(LLRS_E_INVALID, "missing GGUF tensor %s", name.c_str());
+    LLRS_HIP(hipMemsetAsync(*out, 0, len * 4, m->b->stream));  // missing Q/K/V bias -> zeros
+    LLRS_HIP(hipStreamSynchronize(m->b->stream));
+    return LLRS_OK;
+  }
+  if (dims.size() != 1 || dims[0] != len)
+    return set_error(LLRS_E_INVALID, "tensor %s has the wrong shape, expected [%zu]", name.c_str(), len);
+  llrs_tensor *t = nullptr;
+  LLRS_TRY(llrs_tensor_upload(m->b, data, nbytes, ty, 1, len, &t));
+  int rc = launch_dequant_row(t, 0, *out, m->b->stream);
+  hipError_t e = hipStreamSynchronize(m->b->stream);
+  llrs_tensor_free(t);
+  LLRS_TRY(rc);
+  if (e != hipSuccess) return set_error(LLRS_E_HIP, "vector dequant failed: %s", hipGetErrorString(e));
+  return LLRS_OK;
+}
+
+static int build_model(llrs_model *m, const Fetch &fetch, int quantization) {
+  const llrs_model_config &c = m->cfg;
+  size_t H = c.hidden_size, F = c.intermediate_size, KV = c.kv_width;
+  LLRS_TRY(load_matrix(m, fetch, "token_embd.weight", c.vocab_size, H, quantization, &m->embed));
+  LLRS_TRY(load_vector(m, fetch, "output_norm.weight", H, false, &m->norm));
+  m->layers.resize(c.num_hidden_layers);
+  for (size_t i = 0; i < c.num_hidden_layers; i++) {
+    DevLayer &L = m->layers[i];
+    std::string p = "blk." + std::to_string(i) + ".";
+    LLRS_TRY(load_vector(m, fetch, p + "attn_norm.weight", H, false, &L.attn_norm));
+    LLRS_TRY(load_matrix(m, fetch, p + "attn_q.weight", H, H, quantization, &L.q));
+    LLRS_TRY(load_vector(m, fetch, p + "attn_q.bias", H, true, &L.bq));
+    LLRS_TRY(load_matrix(m, fetch, p + "attn_k.weight", KV, H, quantization, &L.k));
+    LLRS_TRY(load_vector(m, fetch, p + "attn_k.bias", KV, true, &L.bk));
+    LLRS_TRY(load_matrix(m, fetch, p + "attn_v.weight", KV, H, quantization, &L.v));
+    LLRS_TRY(load_vector(m, fetch, p + "attn_v.bias", KV, true, &L.bv));
+    LLRS_TRY(load_matrix(m, fetch, p + "attn_output.weight", H, H, quantization, &L.o));
+    LLRS_TRY(load_vector(m, fetch, p + "ffn_norm.weight", H, false, &L.ffn_norm));
+    LLRS_TRY(load_matrix(m, fetch, p + "ffn_gate.weight", F, H, quantization, &L.gate));
+    LLRS_TRY(load_matrix(m, fetch, p + "ffn_up.weight", F, H, quantization, &L.up));
+    LLRS_TRY(load_matrix(m, fetch, p + "ffn_down.weight", H, F, quantization, &L.down));
+  }
+  if (c.tie_word_embeddings) m->lm_head = m->embed;
+  else LLRS_TRY(load_matrix(m, fetch, "output.weight", c.vocab_size, H, quantization, &m->lm_head));
+  // Bytes one decode step streams from HBM for weights.
+  size_t wb = m->lm_head->nbytes + m->embed->row_bytes + H * 4;
+  for (auto &L : m->layers)
+    wb += L.q->nbytes + L.k->nbytes + L.v->nbytes + L.o->nbytes + L.gate->nbytes + L.up->nbytes +
+          L.down->nbytes + (2 * H + H + 2 * KV) * 4;
+  m->weight_bytes = wb;
+  return LLRS_OK;
+}
+
+static void free_model(llrs_model *m) {
+  if (!m) return;
+  (void)hipSetDevice(m->b->device);
+  (void)hipStreamSynchronize(m->b->stream);
+  for (auto *t : m->tensors) llrs_tensor_free(t);
+  for (void *p : m->vecs) (void)hipFree(p);
+  delete m;
+}
+
+static int load_gguf_impl(llrs_backend *b, const char *path, int quantization, llrs_model **out) {
+  GgufFile g;
+  LLRS_TRY(g.open(path));
+  const GgufValue *arch = g.meta("general.architecture");
+  if (!arch || arch->kind != GgufValue::STR)
+    return set_error(LLRS_E_FORMAT, "missing or non-string GGUF metadata general.architecture");
+  if (arch->s != "qwen2")
+    return set_error(LLRS_E_UNSUPPORTED, "unsupported GGUF architecture \"%s\"", arch->s.c_str());
+  const GgufTensorInfo *te = g.tensor("token_embd.weight");
+  if (!te) return set_error(LLRS_E_INVALID, "missing GGUF tensor token_embd.weight");
+  if (te->dims.size() != 2) return set_error(LLRS_E_INVALID, "token_embd.weight must be 2D");
+  llrs_model_config c{};
+  auto u64 = [&](const char *key, size_t &dst) -> int {
+    const GgufValue *v = g.meta(key);
+    uint64_t x;
+    if (!v || !v->as_u64(x))
+      return set_error(LLRS_E_FORMAT, "missing or non-integer GGUF metadata %s", key);
+    dst = (size_t)x;
+    return LLRS_OK;
+  };
+  LLRS_TRY(u64("qwen2.embedding_length", c.hidden_size));
+  LLRS_TRY(u64("qwen2.feed_forward_length", c.intermediate_size));
+  LLRS_TRY(u64("qwen2.attention.head_count", c.num_attention_heads));
+  LLRS_TRY(u64("qwen2.attention.head_count_kv", c.num_key_value_heads));
+  LLRS_TRY(u64("qwen2.block_count", c.num_hidden_layers));
+  c.vocab_size = (size_t)te->dims[1];
+  const GgufValue *eps = g.meta("qwen2.attention.layer_norm_rms_epsilon");
+  if (!eps || !eps->as_f32(c.rms_norm_eps))
+    return set_error(LLRS_E_FORMAT,
+                     "missing or non-numeric GGUF metadata qwen2.attention.layer_norm_rms_epsilon");
+  const GgufValue *th = g.meta("qwen2.rope.freq_base");
+  if (!th || !th->as_f32(c.rope_theta)) c.rope_theta = 10000.0f;
+  LLRS_TRY(u64("qwen2.context_length", c.max_position_embeddings));
+  c.tie_word_embeddings = g.tensor("output.weight") == nullptr;
+  LLRS_TRY(validate_config(c));
+  if (te->dims[0] != c.hidden_size)
+    return set_error(LLRS_E_INVALID, "GGUF embedding width/config mismatch");
+  llrs_model *m = new (std::nothrow) llrs_model();
+  if (!m) return set_error(LLRS_E_OOM, "out of host memory");
+  m->b = b;
+  m->cfg = c;
+  Fetch fetch = [&](const std::string &name, bool &present, uint32_t &type,
+                    std::vector<uint64_t> &dims, const uint8_t *&data, size_t &nbytes,
+                    std::vector<uint8_t> &) -> int {
+    const GgufTensorInfo *t = g.tensor(name);
+    present = t != nullptr;
+    if (!t) return LLRS_OK;
+    type = t->type;
+    dims = t->dims;
+    data = g.data(*t);
+    nbytes = t->nbytes;
+    return LLRS_OK;
+  };
+  int rc = build_model(m, fetch, quantization);
+  if (rc != LLRS_OK) {
+    free_model(m);
+    return rc;
+  }
+  *out = m;
+  return LLRS_OK;
+}
+
+static int synth_config_to_model(const llrs_synth_config &s, llrs_model_config &c) {
+  c = llrs_model_config{};
+  c.hidden_size = s.hidden_size;
+  c.intermediate_size = s.intermediate_size;
+  c.num_attention_heads = s.num_attention_heads;
+  c.num_key_value_heads = s.num_key_value_heads;
+  c.num_hidden_layers = s.num_hidden_layers;
+  c.vocab_size = s.vocab_size;
+  c.max_position_embeddings = s.max_position_embeddings;
+  c.rms_norm_eps = s.rms_norm_eps;
+  c.rope_theta = s.rope_theta;
+  c.tie_word_embeddings = s.tie_word_embeddings;
+  if (s.recipe != LLRS_QUANT_NONE && s.recipe != LLRS_QUANT_Q4K && s.recipe != LLRS_QUANT_Q4KM)
+    return set_error(LLRS_E_INVALID, "unknown recipe %d", s.recipe);
+  return validate_config(c);
+}
+
+// ------------------------------------------------------------------ decode step
+
+static int enqueue_step(llrs_model *m, llrs_kv *kv, int mode) {
+  const llrs_model_config &c = m->cfg;
+  hipStream_t s = m->b->stream;
+  int H = (int)c.hidden_size, F = (int)c.intermediate_size, KVW = (int)c.kv_width;
+  int nh = (int)c.num_attention_heads, nkv = (int)c.num_key_value_heads, hd = (int)c.head_dim;
+  size_t layer_stride = kv->max_seq_len * c.kv_width;
+  LLRS_TRY(launch_embed(m->embed, kv->tok_by_pos, kv->pos, kv->residual, s));
+  for (size_t l = 0; l < c.num_hidden_layers; l++) {
+    DevLayer &L = m->layers[l];
+    float *kc = kv->k_cache + l * layer_stride, *vc = kv->v_cache + l * layer_stride;
+    LLRS_TRY(launch_rmsnorm(kv->residual, L.attn_norm, kv->hidden, H, c.rms_norm_eps, s));
+    LLRS_TRY(launch_gemv_generic(L.q, kv->hidden, kv->q, L.bq, false, s));
+    LLRS_TRY(launch_gemv_generic(L.k, kv->hidden, kv->k, L.bk, false, s));
+    LLRS_TRY(launch_gemv_generic(L.v, kv->hidden, kv->v, L.bv, false, s));
+    LLRS_TRY(launch_rope_kv(kv->q, kv->k, kv->v, kv->rope, kv->pos, kc, vc, nh, nkv, hd, s));
+    LLRS_TRY(launch_attention(kv->q, kc, vc, kv->pos, kv->scores, kv->attn, nh, nkv, hd,
+                              (int)kv->max_seq_len, s));
+    LLRS_TRY(launch_gemv_generic(L.o, kv->attn, kv->residual, nullptr, true, s));
+    LLRS_TRY(launch_rmsnorm(kv->residual, L.ffn_norm, kv->hidden, H, c.rms_norm_eps, s));
+    LLRS_TRY(launch_gemv_generic(L.gate, kv->hidden, kv->gate, nullptr, false, s));
+    LLRS_TRY(launch_gemv_generic(L.up, kv->hidden, kv->up, nullptr, false, s));
+    LLRS_TRY(launch_silu_mul(kv->gate, kv->up, kv->act, F, s));
+    LLRS_TRY(launch_gemv_generic(L.down, kv->act, kv->residual, nullptr, true, s));
+  }
+  (void)KVW;
+  if (mode == LLRS_LOGITS_COMPUTE) {
+    LLRS_TRY(launch_rmsnorm(kv->residual, m->norm, kv->hidden, H, c.rms_norm_eps, s));
+    LLRS_TRY(launch_gemv_generic(m->lm_head, kv->hidden, kv->logits, nullptr, false, s));
+    LLRS_TRY(launch_argmax(kv->logits, (int)c.vocab_size, kv->pos, kv->tok_by_pos, kv->next_token,
+                           1, s));
+  } else {
+    LLRS_TRY(launch_advance(kv->pos, s));
+  }
+  return LLRS_OK;
+}
+
+static bool use_graphs() {
+  const char *e = getenv("LLRS_NO_GRAPH");
+  return !(e && *e && *e != '0');
+}
+
+// One step, replayed from a captured hipGraph (captured on first use).
+static int run_step(llrs_model *m, llrs_kv *kv, int mode) {
+  if (!use_graphs()) return enqueue_step(m, kv, mode);
+  hipStream_t s = m->b->stream;
+  if (!kv->exec[mode]) {
+    LLRS_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(m, kv, mode);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc != LLRS_OK) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    if (e != hipSuccess) return set_error(LLRS_E_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    kv->graph[mode] = g;
+    LLRS_HIP(hipGraphInstantiate(&kv->exec[mode], g, nullptr, nullptr, 0));
+  }
+  LLRS_HIP(hipGraphLaunch(kv->exec[mode], s));
+  return LLRS_OK;
+}
+
+// Host precompute of every position's RoPE row exactly as prepare_rope
+// (src/model.rs:76-84): inv = 1/theta^(2i/hd), angle = pos*inv, glibc sinf/cosf.
+static void rope_table(float *dst, size_t max_seq, size_t hd, float theta) {
+#pragma clang fp contract(off)
+  size_t half = hd / 2;
+  std::vector<float> inv(half);
+  for (size_t i = 0; i < half; i++) inv[i] = 1.0f / powf(theta, 2.0f * (float)i / (float)hd);
+  for (size_t p = 0; p < max_seq; p++)
+    for (size_t i = 0; i < half; i++) {
+      float a = (float)p * inv[i];
+      dst[p * hd + i] = cosf(a);
+      dst[p * hd + half + i] = sinf(a);
+    }
+}
+
+static void free_kv(llrs_kv *kv) {
+  if (!kv) return;
+  (void)hipSetDevice(kv->m->b->device);
+  (void)hipStreamSynchronize(kv->m->b->stream);
+  for (int i = 0; i < 2; i++) {
+    if (kv->exec[i]) (void)hipGraphExecDestroy(kv->exec[i]);
+    if (kv->graph[i]) (void)hipGraphDestroy(kv->graph[i]);
+  }
+  for (void *p : kv->allocs) (void)hipFree(p);
+  if (kv->pinned) (void)hipHostFree(kv->pinned);
+  delete kv;
+}
+
+static int kv_create_impl(llrs_model *m, size_t max_seq, llrs_kv **out) {
+  const llrs_model_config &c = m->cfg;
+  if (max_seq == 0) return set_error(LLRS_E_INVALID, "max_seq_len must be positive");
+  if (max_seq > c.max_position_embeddings)
+    return set_error(LLRS_E_INVALID, "requested context %zu exceeds model limit %zu", max_seq,
+                     c.max_position_embeddings);
+  if (max_seq > (1u << 24)) return set_error(LLRS_E_INVALID, "context %zu is too large", max_seq);
+  llrs_kv *kv = new (std::nothrow) llrs_kv();
+  if (!kv) return set_error(LLRS_E_OOM, "out of host memory");
+  kv->m = m;
+  kv->max_seq_len = max_seq;
+  size_t L = c.num_hidden_layers, KV = c.kv_width, H = c.hidden_size, F = c.intermediate_size;
+  auto A = [&](void **p, size_t bytes) { return dev_alloc(kv->allocs, p, bytes); };
+  int rc = LLRS_OK;
+  if ((rc = A((void **)&kv->k_cache, L * max_seq * KV * 4)) || (rc = A((void **)&kv->v_cache, L * max_seq * KV * 4)) ||
+      (rc = A((void **)&kv->hidden, H * 4)) || (rc = A((void **)&kv->residual, H * 4)) ||
+      (rc = A((void **)&kv->q, H * 4)) || (rc = A((void **)&kv->k, KV * 4)) ||
+      (rc = A((void **)&kv->v, KV * 4)) || (rc = A((void **)&kv->attn, H * 4)) ||
+      (rc = A((void **)&kv->gate, F * 4)) || (rc = A((void **)&kv->up, F * 4)) ||
+      (rc = A((void **)&kv->act, F * 4)) || (rc = A((void **)&kv->logits, c.vocab_size * 4)) ||
+      (rc = A((void **)&kv->scores, c.num_attention_heads * max_seq * 4)) ||
+      (rc = A((void **)&kv->rope, max_seq * c.head_dim * 4)) || (rc = A((void **)&kv->pos, 64)) ||
+      (rc = A((void **)&kv->tok_by_pos, (max_seq + 1) * 4)) || (rc = A((void **)&kv->next_token, 64))) {
+    free_kv(kv);
+    return rc;
+  }
+  hipError_t e = hipHostMalloc((void **)&kv->pinned, (max_seq + 2) * 4, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    kv->pinned = nullptr;
+    free_kv(kv);
+    return set_error(LLRS_E_OOM, "hipHostMalloc failed: %s", hipGetErrorString(e));
+  }
+  std::vector<float> rope(max_seq * c.head_dim);
+  rope_table(rope.data(), max_seq, c.head_dim, c.rope_theta);
+  hipStream_t s = m->b->stream;
+  e = hipMemcpyAsync(kv->rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice, s);
+  // Zero-fill the state (the reference's vec![0.0; ...]); fill kernels via memset
+  // outside any graph capture.
+  if (e == hipSuccess) e = hipMemsetAsync(kv->k_cache, 0, L * max_seq * KV * 4, s);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->v_cache, 0, L * max_seq * KV * 4, s);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->logits, 0, c.vocab_size * 4, s);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->tok_by_pos, 0, (max_seq + 1) * 4, s);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->pos, 0, 64, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    free_kv(kv);
+    return set_error(LLRS_E_HIP, "KV cache init failed: %s", hipGetErrorString(e));
+  }
+  *out = kv;
+  return LLRS_OK;
+}
+
+// Stages tok_by_pos[pos .. pos+n) = tokens and *pos = pos on the device.
+static int stage_tokens(llrs_kv *kv, const uint32_t *tokens, size_t n, size_t pos) {
+  hipStream_t s = kv->m->b->stream;
+  LLRS_HIP(hipStreamSynchronize(s));  // the pinned staging buffer is free again
+  memcpy(kv->pinned, tokens, n * 4);
+  kv->pinned[n] = (uint32_t)pos;
+  if (n) LLRS_HIP(hipMemcpyAsync(kv->tok_by_pos + pos, kv->pinned, n * 4, hipMemcpyHostToDevice, s));
+  LLRS_HIP(hipMemcpyAsync(kv->pos, kv->pinned + n, 4, hipMemcpyHostToDevice, s));
+  return LLRS_OK;
+}
+
+}  // namespace llrs
+
+using namespace llrs;
+
+extern "C" {
+
+int llrs_model_load_gguf(llrs_backend *b, const char *path, int quantization, llrs_model **out) {
+  clear_error();
+  if (!b || !path || !out) return set_error(LLRS_E_INVALID, "backend/path/out is NULL");
+  *out = nullptr;
+  if (quantization < LLRS_QUANT_NONE || quantization > LLRS_QUANT_Q4KM)
+    return set_error(LLRS_E_INVALID, "unknown quantization %d", quantization);
+  LLRS_HIP(hipSetDevice(b->device));
+  return load_gguf_impl(b, path, quantization, out);
+}
+
+void llrs_model_free(llrs_model *m) { free_model(m); }
+
+int llrs_model_config_get(const llrs_model *m, llrs_model_config *out) {
+  clear_error();
+  if (!m || !out) return set_error(LLRS_E_INVALID, "model/out is NULL");
+  *out = m->cfg;
+  return LLRS_OK;
+}
+
+size_t llrs_model_weight_bytes(const llrs_model *m) { return m ? m->weight_bytes : 0; }
+
+int llrs_synth_write_gguf(const llrs_synth_config *cfg, const char *path) {
+  clear_error();
+  if (!cfg || !path) return set_error(LLRS_E_INVALID, "cfg/path is NULL");
+  llrs_model_config c;
+  LLRS_TRY(synth_config_to_model(*cfg, c));
+  auto specs = synth_specs(*cfg);
+  std::vector<GgufOutTensor> tensors(specs.size());
+  for (size_t i = 0; i < specs.size(); i++) LLRS_TRY(synth_tensor(*cfg, i, specs[i], tensors[i]));
+  GgufWriter w;
+  w.add_str("general.architecture", "qwen2");
+  w.add_u32("general.alignment", 32);
+  w.add_u32("qwen2.embedding_length", (uint32_t)c.hidden_size);
+  w.add_u32("qwen2.feed_forward_length", (uint32_t)c.intermediate_size);
+  w.add_u32("qwen2.attention.head_count", (uint32_t)c.num_attention_heads);
+  w.add_u32("qwen2.attention.head_count_kv", (uint32_t)c.num_key_value_heads);
+  w.add_u32("qwen2.block_count", (uint32_t)c.num_hidden_layers);
+  w.add_u32("qwen2.context_length", (uint32_t)c.max_position_embeddings);
+  w.add_f32("qwen2.attention.layer_norm_rms_epsilon", c.rms_norm_eps);
+  w.add_f32("qwen2.rope.freq_base", c.rope_theta);
+  return w.write(path, tensors);
+}
+
+int llrs_model_synthetic(llrs_backend *b, const llrs_synth_config *cfg, llrs_model **out) {
+  clear_error();
+  if (!b || !cfg || !out) return set_error(LLRS_E_INVALID, "backend/cfg/out is NULL");
+  *out = nullptr;
+  LLRS_HIP(hipSetDevice(b->device));
+  llrs_model_config c;
+  LLRS_TRY(synth_config_to_model(*cfg, c));
+  auto specs = synth_specs(*cfg);
+  llrs_model *m = new (std::nothrow) llrs_model();
+  if (!m) return set_error(LLRS_E_OOM, "out of host memory");
+  m->b = b;
+  m->cfg = c;
+  Fetch fetch = [&](const std::string &name, bool &present, uint32_t &type,
+                    std::vector<uint64_t> &dims, const uint8_t *&data, size_t &nbytes,
+                    std::vector<uint8_t> &storage) -> int {
+    present = false;
+    for (size_t i = 0; i < specs.size(); i++) {
+      if (specs[i].name != name) continue;
+      GgufOutTensor t;
+      LLRS_TRY(synth_tensor(*cfg, i, specs[i], t));
+      present = true;
+      type = t.type;
+      dims = t.dims;
+      storage.swap(t.bytes);
+      data = storage.data();
+      nbytes = storage.size();
+      break;
+    }
+    return LLRS_OK;
+  };
+  int rc = build_model(m, fetch, LLRS_QUANT_NONE);
+  if (rc != LLRS_OK) {
+    free_model(m);
+    return rc;
+  }
+  *out = m;
+  return LLRS_OK;
+}
+
+int llrs_kv_create(llrs_model *m, size_t max_seq_len, llrs_kv **out) {
+  clear_error();
+  if (!m || !out) return set_error(LLRS_E_INVALID, "model/out is NULL");
+  *out = nullptr;
+  LLRS_HIP(hipSetDevice(m->b->device));
+  return kv_create_impl(m, max_seq_len, out);
+}
+
+void llrs_kv_free(llrs_kv *kv) { free_kv(kv); }
+
+int llrs_kv_reset(llrs_kv *kv) {
+  clear_error();
+  return kv ? LLRS_OK : set_error(LLRS_E_INVALID, "kv is NULL");
+}
+
+int llrs_forward_token(llrs_model *m, llrs_kv *kv, uint32_t token, size_t pos, int logits_mode) {
+  clear_error();
+  if (!m || !kv || kv->m != m) return set_error(LLRS_E_INVALID, "model/kv mismatch");
+  if (token >= m->cfg.vocab_size)
+    return set_error(LLRS_E_INVALID, "token id %u is outside vocabulary", token);
+  if (pos >= kv->max_seq_len)
+    return set_error(LLRS_E_INVALID, "position %zu exceeds configured context %zu", pos,
+                     kv->max_seq_len);
+  if (logits_mode != LLRS_LOGITS_SKIP && logits_mode != LLRS_LOGITS_COMPUTE)
+    return set_error(LLRS_E_INVALID, "unknown logits mode %d", logits_mode);
+  LLRS_HIP(hipSetDevice(m->b->device));
+  LLRS_TRY(stage_tokens(kv, &token, 1, pos));
+  LLRS_TRY(run_step(m, kv, logits_mode));
+  LLRS_HIP(hipStreamSynchronize(m->b->stream));
+  return LLRS_OK;
+}
+
+int llrs_prefill(llrs_model *m, llrs_kv *kv, const uint32_t *tokens, size_t n, size_t start_pos) {
+  clear_error();
+  if (!m || !kv || kv->m != m) return set_error(LLRS_E_INVALID, "model/kv mismatch");
+  if (n == 0) return set_error(LLRS_E_INVALID, "prefill requires at least one token");
+  if (!tokens) return set_error(LLRS_E_INVALID, "tokens is NULL");
+  for (size_t i = 0; i < n; i++) {
+    if (tokens[i] >= m->cfg.vocab_size)
+      return set_error(LLRS_E_INVALID, "token id %u is outside vocabulary", tokens[i]);
+    if (start_pos + i >= kv->max_seq_len)
+      return set_error(LLRS_E_INVALID, "position %zu exceeds configured context %zu",
+                       start_pos + i, kv->max_seq_len);
+  }
+  LLRS_HIP(hipSetDevice(m->b->device));
+  LLRS_TRY(stage_tokens(kv, tokens, n, start_pos));
+  for (size_t i = 0; i < n; i++)
+    LLRS_TRY(run_step(m, kv, i + 1 == n ? LLRS_LOGITS_COMPUTE : LLRS_LOGITS_SKIP));
+  LLRS_HIP(hipStreamSynchronize(m->b->stream));
+  return LLRS_OK;
+}
+
+int llrs_decode_greedy(llrs_model *m, llrs_kv *kv, size_t start_pos, size_t n_steps,
+                       uint32_t *out_tokens) {
+  clear_error();
+  if (!m || !kv || kv->m != m) return set_error(LLRS_E_INVALID, "model/kv mismatch");
+  if (n_steps == 0) return LLRS_OK;
+  if (!out_tokens) return set_error(LLRS_E_INVALID, "out_tokens is NULL");
+  if (start_pos + n_steps > kv->max_seq_len)
+    return set_error(LLRS_E_INVALID, "benchmark token counts exceed context");
+  LLRS_HIP(hipSetDevice(m->b->device));
+  hipStream_t s = m->b->stream;
+  LLRS_TRY(stage_tokens(kv, nullptr, 0, start_pos));
+  // token = argmax(current logits) for position start_pos; nothing advances.
+  LLRS_TRY(launch_argmax(kv->logits, (int)m->cfg.vocab_size, kv->pos, kv->tok_by_pos,
+                         kv->next_token, 0, s));
+  for (size_t i = 0; i < n_steps; i++) LLRS_TRY(run_step(m, kv, LLRS_LOGITS_COMPUTE));
+  LLRS_HIP(hipMemcpyAsync(kv->pinned, kv->tok_by_pos + start_pos, n_steps * 4,
+                          hipMemcpyDeviceToHost, s));
+  LLRS_HIP(hipStreamSynchronize(s));
+  memcpy(out_tokens, kv->pinned, n_steps * 4);
+  return LLRS_OK;
+}
+
+int llrs_argmax(llrs_kv *kv, uint32_t *out_token) {
+  clear_error();
+  if (!kv || !out_token) return set_error(LLRS_E_INVALID, "kv/out is NULL");
+  llrs_model *m = kv->m;
+  LLRS_HIP(hipSetDevice(m->b->device));
+  hipStream_t s = m->b->stream;
+  // Evaluate into the spare slot after the context so no state changes.
+  LLRS_HIP(hipStreamSynchronize(s));
+  uint32_t saved = 0;
+  LLRS_HIP(hipMemcpy(&saved, kv->pos, 4, hipMemcpyDeviceToHost));
+  LLRS_TRY(stage_tokens(kv, nullptr, 0, kv->max_seq_len));
+  LLRS_TRY(launch_argmax(kv->logits, (int)m->cfg.vocab_size, kv->pos, kv->tok_by_pos,
+                         kv->next_token, 0, s));
+  LLRS_HIP(hipMemcpyAsync(kv->pinned, kv->next_token, 4, hipMemcpyDeviceToHost, s));
+  LLRS_HIP(hipStreamSynchronize(s));
+  *out_token = kv->pinned[0];
+  LLRS_TRY(stage_tokens(kv, nullptr, 0, saved));
+  LLRS_HIP(hipStreamSynchronize(s));
+  return LLRS_OK;
+}
+
+int llrs_read_logits(llrs_kv *kv, float *out, size_t n) {
+  clear_error();
+  if (!kv || !out) return set_error(LLRS_E_INVALID, "kv/out is NULL");
+  if (n != kv->m->cfg.vocab_size)
+    return set_error(LLRS_E_INVALID, "logits length %zu != vocab %zu", n, kv->m->cfg.vocab_size);
+  LLRS_HIP(hipSetDevice(kv->m->b->device));
+  LLRS_HIP(hipMemcpyAsync(out, kv->logits, n * 4, hipMemcpyDeviceToHost, kv->m->b->stream));
+  LLRS_HIP(hipStreamSynchronize(kv->m->b->stream));
+  return LLRS_OK;
+}
+
+int llrs_read_kv(llrs_kv *kv, size_t layer, int which, float *out, size_t n) {
+  clear_error();
+  if (!kv || !out) return set_error(LLRS_E_INVALID, "kv/out is NULL");
+  const llrs_model_config &c = kv->m->cfg;
+  if (layer >= c.num_hidden_layers) return set_error(LLRS_E_INVALID, "KV layer out of bounds");
+  size_t per = kv->max_seq_len * c.kv_width;
+  if (n > per) return set_error(LLRS_E_INVALID, "read of %zu floats exceeds the layer (%zu)", n, per);
+  const float *src = (which ? kv->v_cache : kv->k_cache) + layer * per;
+  LLRS_HIP(hipSetDevice(kv->m->b->device));
+  LLRS_HIP(hipMemcpyAsync(out, src, n * 4, hipMemcpyDeviceToHost, kv->m->b->stream));
+  LLRS_HIP(hipStreamSynchronize(kv->m->b->stream));
+  return LLRS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,108 @@
+// Device-side decoders for the GGML block formats (gfx950).
+//
+// value_dev() restates value_at (src/quant.rs:349-456) element by element and
+// is bit-exact with it: every product in a dequantized value (f16 scale x
+// <= 8-bit scale x <= 6-bit code) is exact in f32, so only the final add or
+// subtract rounds, in the same order as the reference.  Contraction is
+// switched off in these functions anyway so the compiler cannot reassociate.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llrs {
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  // v_cvt_f32_f16: exact widening, f16 subnormals preserved (gfx9 default mode).
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+  uint32_t bits = (uint32_t)h << 16;
+  if ((h & 0x7fffu) > 0x7f80u) bits |= 0x00400000u;  // quiet NaN, as the `half` crate does
+  return __builtin_bit_cast(float, bits);
+}
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t *p) {
+  // All GGML block sizes are even, so every 2-byte field is 2-byte aligned.
+  return *reinterpret_cast<const uint16_t *>(p);
+}
+__device__ __forceinline__ float ld_f16(const uint8_t *p) { return f16_bits_to_f32(ld_u16(p)); }
+
+// scale_min_k4 (src/quant.rs:338-347).
+__device__ __forceinline__ void scale_min_k4(int i, const uint8_t *s, int &sc, int &mn) {
+  if (i < 4) {
+    sc = s[i] & 63;
+    mn = s[i + 4] & 63;
+  } else {
+    sc = (s[i + 4] & 0x0f) | ((s[i - 4] >> 6) << 4);
+    mn = (s[i + 4] >> 4) | ((s[i] >> 6) << 4);
+  }
+}
+
+__device__ inline float value_dev(const uint8_t *row, uint32_t ty, uint32_t col) {
+#pragma clang fp contract(off)
+  switch (ty) {
+    case 0: return *reinterpret_cast<const float *>(row + (size_t)col * 4);
+    case 1: return ld_f16(row + (size_t)col * 2);
+    case 30: return bf16_bits_to_f32(ld_u16(row + (size_t)col * 2));
+    case 2: {  // Q4_0
+      const uint8_t *b = row + (size_t)(col / 32) * 18;
+      uint32_t j = col % 32;
+      int q = j < 16 ? (b[2 + j] & 0x0f) : (b[2 + j - 16] >> 4);
+      return ld_f16(b) * ((float)q - 8.0f);
+    }
+    case 3: {  // Q4_1
+      const uint8_t *b = row + (size_t)(col / 32) * 20;
+      uint32_t j = col % 32;
+      int q = j < 16 ? (b[4 + j] & 0x0f) : (b[4 + j - 16] >> 4);
+      return ld_f16(b) * (float)q + ld_f16(b + 2);
+    }
+    case 6:
+    case 7: {  // Q5_0 / Q5_1
+      uint32_t bsz = ty == 6 ? 22 : 24, qh_off = ty == 6 ? 2 : 4, qs_off = ty == 6 ? 6 : 8;
+      const uint8_t *b = row + (size_t)(col / 32) * bsz;
+      uint32_t j = col % 32;
+      int lo = j < 16 ? (b[qs_off + j] & 0x0f) : (b[qs_off + j - 16] >> 4);
+      int hi = (b[qh_off + j / 8] >> (j % 8)) & 1;
+      int q = lo | (hi << 4);
+      if (ty == 6) return ld_f16(b) * ((float)q - 16.0f);
+      return ld_f16(b) * (float)q + ld_f16(b + 2);
+    }
+    case 8: {  // Q8_0
+      const uint8_t *b = row + (size_t)(col / 32) * 34;
+      return ld_f16(b) * (float)(int8_t)b[2 + col % 32];
+    }
+    case 12: {  // Q4_K
+      const uint8_t *b = row + (size_t)(col / 256) * 144;
+      uint32_t j = col % 256;
+      int g = (int)(j / 32), sc, mn;
+      scale_min_k4(g, b + 4, sc, mn);
+      uint8_t p = b[16 + (g / 2) * 32 + j % 32];
+      int q = (g % 2 == 0) ? (p & 0x0f) : (p >> 4);
+      return ld_f16(b) * (float)sc * (float)q - ld_f16(b + 2) * (float)mn;
+    }
+    case 13: {  // Q5_K
+      const uint8_t *b = row + (size_t)(col / 256) * 176;
+      uint32_t j = col % 256;
+      int g = (int)(j / 32), sc, mn;
+      scale_min_k4(g, b + 4, sc, mn);
+      uint8_t p = b[48 + (g / 2) * 32 + j % 32];
+      int lo = (g % 2 == 0) ? (p & 0x0f) : (p >> 4);
+      int hi = (b[16 + j % 32] & (1 << g)) ? 16 : 0;
+      return ld_f16(b) * (float)sc * (float)(lo + hi) - ld_f16(b + 2) * (float)mn;
+    }
+    case 14: {  // Q6_K
+      const uint8_t *b = row + (size_t)(col / 256) * 210;
+      uint32_t j = col % 256;
+      uint32_t half = j / 128, within = j % 128, lane = within % 32, quarter = within / 32;
+      uint8_t lb = b[half * 64 + (quarter & 1) * 32 + lane];
+      int ql = quarter < 2 ? (lb & 0x0f) : (lb >> 4);
+      int qh = (b[128 + half * 32 + lane] >> (quarter * 2)) & 3;
+      float q = (float)((ql | (qh << 4)) - 32);
+      float scale = (float)(int8_t)b[192 + half * 8 + quarter * 2 + lane / 16];
+      return ld_f16(b + 208) * scale * q;
+    }
+    default: return 0.0f;
+  }
+}
+
+}  // namespace llrs

@@ -1,0 +1,207 @@
+"""Model-level mirror of the reference's CausalModel boundary over the C ABI.
+
+    ModelLoader.load_dynamic(path, LoadOptions)   src/loader.rs:37-42
+    HipQwen2Model.forward_token / prefill         src/architecture.rs:47-77
+    KVCache (device-resident, + InferenceBuffers) src/cache.rs:4-101
+    InferenceEngine.benchmark_tokens              src/engine.rs:189-223
+"""
+from __future__ import annotations
+
+import ctypes as C
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import (HipBackend, LlrsError, LoadQuantization, LogitsMode, _check, _f32, _ModelConfig,
+               _SynthConfig, lib, P, SZ, U32P)
+
+
+@dataclass
+class LlamaConfig:
+    """config::LlamaConfig (src/config.rs:18-55) as loaded onto the device."""
+    hidden_size: int
+    intermediate_size: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    num_hidden_layers: int
+    vocab_size: int
+    max_position_embeddings: int
+    head_dim: int
+    kv_width: int
+    rms_norm_eps: float
+    rope_theta: float
+    tie_word_embeddings: bool
+
+
+@dataclass
+class SynthConfig:
+    """A synthetic Qwen2 model: shape, recipe and seed (llrs_synth_config)."""
+    hidden_size: int
+    intermediate_size: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    num_hidden_layers: int
+    vocab_size: int
+    max_position_embeddings: int = 32768
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+    tie_word_embeddings: bool = True
+    recipe: LoadQuantization = LoadQuantization.Q4KM
+    seed: int = 0
+    weight_std: float = 0.02
+    threads: int = 0
+
+    def _c(self) -> _SynthConfig:
+        return _SynthConfig(self.hidden_size, self.intermediate_size, self.num_attention_heads,
+                            self.num_key_value_heads, self.num_hidden_layers, self.vocab_size,
+                            self.max_position_embeddings, self.rms_norm_eps, self.rope_theta,
+                            int(self.tie_word_embeddings), int(self.recipe), self.seed,
+                            self.weight_std, self.threads)
+
+    def write_gguf(self, path: str) -> None:
+        """Writes the model as a pre-quantized GGUF v3 file."""
+        _check(lib().llrs_synth_write_gguf(C.byref(self._c()), str(path).encode()))
+
+
+class HipQwen2Model:
+    """architecture::CausalModel for Qwen2 on the GPU."""
+
+    def __init__(self, backend: HipBackend, handle):
+        self._backend = backend
+        self.handle = handle
+        c = _ModelConfig()
+        _check(lib().llrs_model_config_get(handle, C.byref(c)))
+        self._config = LlamaConfig(c.hidden_size, c.intermediate_size, c.num_attention_heads,
+                                   c.num_key_value_heads, c.num_hidden_layers, c.vocab_size,
+                                   c.max_position_embeddings, c.head_dim, c.kv_width,
+                                   c.rms_norm_eps, c.rope_theta, bool(c.tie_word_embeddings))
+
+    @classmethod
+    def synthetic(cls, backend: HipBackend, cfg: SynthConfig) -> "HipQwen2Model":
+        h = P()
+        _check(lib().llrs_model_synthetic(backend.handle, C.byref(cfg._c()), C.byref(h)))
+        return cls(backend, h)
+
+    def architecture(self) -> str:
+        return "qwen2"
+
+    def config(self) -> LlamaConfig:
+        return self._config
+
+    def backend(self) -> HipBackend:
+        return self._backend
+
+    def weight_bytes(self) -> int:
+        return int(lib().llrs_model_weight_bytes(self.handle))
+
+    def forward_token(self, token_id: int, pos: int, kv_cache: "KVCache",
+                      logits: LogitsMode = LogitsMode.COMPUTE) -> None:
+        _check(lib().llrs_forward_token(self.handle, kv_cache.handle, token_id, pos, int(logits)))
+
+    def prefill(self, tokens, start_pos: int, kv_cache: "KVCache") -> None:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        _check(lib().llrs_prefill(self.handle, kv_cache.handle, t.ctypes.data_as(U32P), t.size,
+                                  start_pos))
+
+    def decode_greedy(self, start_pos: int, n_steps: int, kv_cache: "KVCache") -> np.ndarray:
+        out = np.zeros(max(n_steps, 1), dtype=np.uint32)
+        _check(lib().llrs_decode_greedy(self.handle, kv_cache.handle, start_pos, n_steps,
+                                        out.ctypes.data_as(U32P)))
+        return out[:n_steps]
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h and lib is not None:
+            lib().llrs_model_free(h)
+            self.handle = None
+
+
+class KVCache:
+    """cache::KVCache + InferenceBuffers, resident in HBM."""
+
+    def __init__(self, model: HipQwen2Model, max_seq_len: int):
+        h = P()
+        _check(lib().llrs_kv_create(model.handle, max_seq_len, C.byref(h)))
+        self.handle = h
+        self.model = model
+        self.max_seq_len = max_seq_len
+
+    def reset(self) -> None:
+        _check(lib().llrs_kv_reset(self.handle))
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.model.config().vocab_size, dtype=np.float32)
+        _check(lib().llrs_read_logits(self.handle, _f32(out), out.size))
+        return out
+
+    def argmax(self) -> int:
+        t = C.c_uint32()
+        _check(lib().llrs_argmax(self.handle, C.byref(t)))
+        return int(t.value)
+
+    def layer(self, layer: int, which: str, n_pos: int) -> np.ndarray:
+        cfg = self.model.config()
+        out = np.empty(n_pos * cfg.kv_width, dtype=np.float32)
+        _check(lib().llrs_read_kv(self.handle, layer, 0 if which == "k" else 1, _f32(out),
+                                  out.size))
+        return out.reshape(n_pos, cfg.kv_width)
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h:
+            lib().llrs_kv_free(h)
+            self.handle = None
+
+
+class ModelLoader:
+    """loader::ModelLoader (src/loader.rs:33-78), GGUF files only."""
+
+    @staticmethod
+    def load_dynamic(path, backend: HipBackend,
+                     quantization: LoadQuantization = LoadQuantization.NONE) -> HipQwen2Model:
+        h = P()
+        _check(lib().llrs_model_load_gguf(backend.handle, str(path).encode(), int(quantization),
+                                          C.byref(h)))
+        return HipQwen2Model(backend, h)
+
+
+@dataclass
+class InferenceMetrics:
+    """benchmark::InferenceMetrics (src/benchmark.rs:3-34)."""
+    prompt_tokens: int = 0
+    generated_tokens: int = 0
+    prefill_s: float = 0.0
+    decode_s: float = 0.0
+    tokens: list = field(default_factory=list)
+
+    def prefill_tokens_per_second(self) -> float:
+        return self.prompt_tokens / self.prefill_s if self.prefill_s > 0 else 0.0
+
+    def decode_tokens_per_second(self) -> float:
+        return self.generated_tokens / self.decode_s if self.decode_s > 0 else 0.0
+
+
+class InferenceEngine:
+    """The benchmark half of engine::InferenceEngine (src/engine.rs:189-241)."""
+
+    def __init__(self, model: HipQwen2Model, context_length: int = 4096):
+        ctx = min(context_length, model.config().max_position_embeddings)
+        if ctx <= 0:
+            raise LlrsError(-1, "context length must be positive")
+        self.model = model
+        self.kv_cache = KVCache(model, ctx)
+
+    def benchmark_tokens(self, prompt_tokens, decode_tokens: int) -> InferenceMetrics:
+        prompt = np.ascontiguousarray(prompt_tokens, dtype=np.uint32)
+        if prompt.size == 0:
+            raise LlrsError(-1, "benchmark prompt is empty")
+        if prompt.size + decode_tokens > self.kv_cache.max_seq_len:
+            raise LlrsError(-1, "benchmark token counts exceed context")
+        self.kv_cache.reset()
+        t0 = time.perf_counter()
+        self.model.prefill(prompt, 0, self.kv_cache)
+        t1 = time.perf_counter()
+        toks = self.model.decode_greedy(prompt.size, decode_tokens, self.kv_cache)
+        t2 = time.perf_counter()
+        return InferenceMetrics(prompt.size, decode_tokens, t1 - t0, t2 - t1, list(toks))

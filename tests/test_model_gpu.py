@@ -1,0 +1,124 @@
+"""GPU decode path vs the CPU oracle on synthetic Qwen2 models (MI355X).
+
+Bar (north star): final logits within 2e-2 max-abs of the oracle's, and the
+same greedy token ids over 32 decode steps (src/engine.rs:205-216, 233-241).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 2e-2
+
+
+def tiny_cfg(llrs, **kw):
+    base = dict(hidden_size=256, intermediate_size=768, num_attention_heads=4,
+                num_key_value_heads=2, num_hidden_layers=2, vocab_size=1000,
+                max_position_embeddings=512, recipe=llrs.LoadQuantization.Q4KM, seed=7,
+                tie_word_embeddings=False)
+    base.update(kw)
+    return llrs.SynthConfig(**base)
+
+
+def make_pair(llrs, backend, oracle, cfg, path, ctx):
+    cfg.write_gguf(path)
+    model = llrs.ModelLoader.load_dynamic(path, backend)
+    om = oracle.load(path)
+    om.new_state(ctx)
+    return model, llrs.KVCache(model, ctx), om
+
+
+def compare_run(llrs, backend, oracle, cfg, path, prompt, n_decode, ctx):
+    model, kv, om = make_pair(llrs, backend, oracle, cfg, path, ctx)
+    print(f"[model] H={cfg.hidden_size} L={cfg.num_hidden_layers} V={cfg.vocab_size} "
+          f"prompt={len(prompt)} decode={n_decode}", flush=True)
+    model.prefill(prompt, 0, kv)
+    om.prefill(prompt, 0)
+    lg, lo = kv.logits(), om.logits()
+    err = float(np.abs(lg - lo).max())
+    print(f"[model] prefill logits max-abs err {err:.3e}", flush=True)
+    assert err <= LOGIT_TOL
+    assert kv.argmax() == om.argmax()
+    got = model.decode_greedy(len(prompt), n_decode, kv)
+    want = om.decode_greedy(len(prompt), n_decode)
+    print(f"[model] tokens gpu={got[:8].tolist()}... oracle={want[:8].tolist()}...", flush=True)
+    np.testing.assert_array_equal(got, want)
+    err = float(np.abs(kv.logits() - om.logits()).max())
+    print(f"[model] final logits max-abs err {err:.3e}", flush=True)
+    assert err <= LOGIT_TOL
+    n = len(prompt) + n_decode
+    for layer in (0, cfg.num_hidden_layers - 1):
+        for which in ("k", "v"):
+            a, b = kv.layer(layer, which, n), om.kv(layer, which, n)
+            assert float(np.abs(a - b).max()) <= 1e-3 * max(1.0, float(np.abs(b).max()))
+    return model, kv, om
+
+
+def test_tiny_q4km_greedy_parity(llrs, backend, oracle, tmp_path):
+    cfg = tiny_cfg(llrs)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, 24).astype(np.uint32)
+    compare_run(llrs, backend, oracle, cfg, tmp_path / "t.gguf", prompt, 32, 128)
+
+
+@pytest.mark.parametrize("recipe", ["Q4K", "NONE"])
+def test_tiny_other_recipes(llrs, backend, oracle, tmp_path, recipe):
+    cfg = tiny_cfg(llrs, recipe=getattr(llrs.LoadQuantization, recipe), tie_word_embeddings=True,
+                   num_key_value_heads=1, seed=11)
+    prompt = np.random.default_rng(2).integers(0, cfg.vocab_size, 9).astype(np.uint32)
+    compare_run(llrs, backend, oracle, cfg, tmp_path / "r.gguf", prompt, 32, 64)
+
+
+def test_head_dim_64_and_gqa_7(llrs, backend, oracle, tmp_path):
+    """0.5B-like head geometry: 14 query heads over 2 KV heads, head_dim 64."""
+    cfg = tiny_cfg(llrs, hidden_size=896, num_attention_heads=14, num_key_value_heads=2,
+                   intermediate_size=1024, num_hidden_layers=1, vocab_size=800, seed=3)
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab_size, 40).astype(np.uint32)
+    compare_run(llrs, backend, oracle, cfg, tmp_path / "h.gguf", prompt, 32, 96)
+
+
+def test_forward_token_matches_prefill(llrs, backend, oracle, tmp_path):
+    cfg = tiny_cfg(llrs, seed=13)
+    cfg.write_gguf(tmp_path / "f.gguf")
+    model = llrs.ModelLoader.load_dynamic(tmp_path / "f.gguf", backend)
+    prompt = np.array([5, 17, 999, 0, 42], np.uint32)
+    kv1, kv2 = llrs.KVCache(model, 32), llrs.KVCache(model, 32)
+    model.prefill(prompt, 0, kv1)
+    for i, t in enumerate(prompt):
+        model.forward_token(int(t), i, kv2,
+                            llrs.LogitsMode.COMPUTE if i + 1 == len(prompt) else llrs.LogitsMode.SKIP)
+    np.testing.assert_array_equal(kv1.logits(), kv2.logits())
+
+
+def test_model_error_paths(llrs, backend, tmp_path):
+    cfg = tiny_cfg(llrs, seed=17)
+    cfg.write_gguf(tmp_path / "e.gguf")
+    model = llrs.ModelLoader.load_dynamic(tmp_path / "e.gguf", backend)
+    kv = llrs.KVCache(model, 16)
+    with pytest.raises(llrs.LlrsError, match="outside vocabulary"):
+        model.forward_token(cfg.vocab_size, 0, kv)
+    with pytest.raises(llrs.LlrsError, match="exceeds configured context"):
+        model.forward_token(1, 16, kv)
+    with pytest.raises(llrs.LlrsError, match="exceeds model limit"):
+        llrs.KVCache(model, cfg.max_position_embeddings + 1)
+    with pytest.raises(llrs.LlrsError, match="at least one token"):
+        model.prefill(np.zeros(0, np.uint32), 0, kv)
+    with pytest.raises(llrs.LlrsError, match="exceed context"):
+        model.decode_greedy(10, 7, kv)
+
+
+def test_config3_qwen05b_shape_greedy_parity(llrs, backend, oracle, tmp_path):
+    """Qwen2.5-0.5B shape, q4km, 128-token random prompt, 32 greedy steps."""
+    cfg = llrs.SynthConfig(hidden_size=896, intermediate_size=4864, num_attention_heads=14,
+                           num_key_value_heads=2, num_hidden_layers=24, vocab_size=151936,
+                           max_position_embeddings=32768, rope_theta=1e6, rms_norm_eps=1e-6,
+                           tie_word_embeddings=True, recipe=llrs.LoadQuantization.Q4KM, seed=3)
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab_size, 128).astype(np.uint32)
+    model, kv, om = compare_run(llrs, backend, oracle, cfg, tmp_path / "c3.gguf", prompt, 32, 4096)
+    QT = llrs.QuantType
+    # The q4km recipe at this shape: Q5_0 fallback (896 % 256 != 0), Q8_0 V/embeddings, Q6_K down.
+    for name, qt in (("blk.0.attn_q.weight", QT.Q5_0), ("blk.0.ffn_gate.weight", QT.Q5_0),
+                     ("blk.0.attn_v.weight", QT.Q8_0), ("token_embd.weight", QT.Q8_0),
+                     ("blk.0.ffn_down.weight", QT.Q6K)):
+        assert llrs.gguf_read_tensor(tmp_path / "c3.gguf", name)[1].quant_type == qt, name
