@@ -1,0 +1,197 @@
+#!/usr/bin/env python3
+"""Batch-1 greedy decode of the Qwen2.5-7B-shaped Q4_K_M model on one MI355X.
+
+Workload: a synthetic Qwen2.5-7B-shaped model (hidden
+3584, 28 layers, 28 Q / 4 KV heads, head_dim 128, FFN 18944, vocab 152064,
+untied LM head, rope_theta 1e6), random-init N(0, 0.02) weights quantized
+with the reference's q4km recipe (Q4_K q/k/o/gate/up, Q8_0 v/embeddings/LM
+head, Q6_K ffn_down), generated in HBM.  A 512-token random prompt is
+prefilled, then `--warmup` untimed and `--steps` timed greedy decode steps
+run; one step = one token through the whole model (the decode loop of
+InferenceEngine::benchmark_tokens, src/engine.rs:205-216), replayed from a
+captured hipGraph with the token and position kept on the device.
+
+Prints ONE JSON line: decode tok/s as `value`, the whole-step HBM rate, the
+dominant kernel's roofline (HIP-event timing of its own launches) and the
+CPU baseline (the oracle's restated AVX2 path on this host's cores, on a
+bounded sample of the same model).
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import pathlib
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PEAK_HBM_GBS = 8000.0
+METRIC = "batch-1 decode tok/s + achieved HBM GB/s (% of peak), Qwen2.5-7B-shape Q4_K_M"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def package():
+    pkg = ROOT / "llama.rs_amd"
+    spec = importlib.util.spec_from_file_location(
+        "llama_rs_amd", pkg / "__init__.py", submodule_search_locations=[str(pkg)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["llama_rs_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def host_threads() -> int:
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return n
+
+
+def kv_bytes_per_token(cfg, pos: int) -> int:
+    """K and V of positions 0..pos read once per KV head, plus the new row written."""
+    row = cfg.kv_width * 4
+    return cfg.num_hidden_layers * 2 * ((pos + 1) * row + row)
+
+
+def cpu_baseline(llrs, model, seconds: float, log_prefix="cpu") -> dict:
+    """The oracle's restated AVX2 path (src/simd.rs) on all host threads, on the same
+    model bytes (exported from HBM), decoding from position 0 for ~`seconds`."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_ffi import AVX2, Oracle
+
+    threads = host_threads()
+    shm = pathlib.Path("/dev/shm") if os.path.isdir("/dev/shm") else pathlib.Path("/tmp")
+    path = shm / f"llrs_bench_{os.getpid()}.gguf"
+    try:
+        t0 = time.perf_counter()
+        model.export_gguf(path)
+        log(f"{log_prefix}: exported model to {path} in {time.perf_counter() - t0:.1f}s")
+        om = Oracle().load(path, kernel=AVX2, threads=threads)
+        om.new_state(64)
+        t0 = time.perf_counter()
+        om.forward_token(1, 0, True)
+        first = time.perf_counter() - t0
+        n = int(max(2, min(32, seconds / max(first, 1e-3))))
+        log(f"{log_prefix}: first token {first:.2f}s; timing {n} tokens on {threads} threads")
+        tok = om.argmax()
+        t0 = time.perf_counter()
+        for p in range(1, n + 1):
+            om.forward_token(tok, p, True)
+            tok = om.argmax()
+        dt = time.perf_counter() - t0
+        del om
+    finally:
+        if path.exists():
+            path.unlink()
+    return {"value": round(n / dt, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} greedy decode steps at positions 1-{n} of the same 7B q4km model "
+                      f"(after 1 warm-up token at position 0), oracle's restated AVX2 path "
+                      f"(src/simd.rs) with the reference's row-parallel policy on {threads} "
+                      f"threads; the Rust reference itself cannot be built here"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--context", type=int, default=4096)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-iters", type=int, default=5)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path; see DESIGN.md on sharding)", file=sys.stderr)
+        return 2
+    if args.prompt + args.warmup + args.steps > args.context:
+        print("prompt + warmup + steps exceed the context", file=sys.stderr)
+        return 2
+
+    llrs = package()
+    be = llrs.HipBackend(0)
+    log(f"backend {be.name()} with {be.threads()} CUs")
+    cfg = llrs.SynthConfig(hidden_size=3584, intermediate_size=18944, num_attention_heads=28,
+                           num_key_value_heads=4, num_hidden_layers=28, vocab_size=152064,
+                           max_position_embeddings=32768, rope_theta=1e6, rms_norm_eps=1e-6,
+                           tie_word_embeddings=False, recipe=llrs.LoadQuantization.Q4KM, seed=5)
+    t0 = time.perf_counter()
+    model = llrs.HipQwen2Model.synthetic(be, cfg)
+    gen_s = time.perf_counter() - t0
+    mc = model.config()
+    wbytes = model.weight_bytes()
+    log(f"generated 7B q4km model in HBM in {gen_s:.1f}s: {wbytes / 1e9:.3f} GB of weights/token")
+
+    kv = llrs.KVCache(model, args.context)
+    prompt = np.random.default_rng(5).integers(0, mc.vocab_size, args.prompt).astype(np.uint32)
+    be.synchronize()
+    t0 = time.perf_counter()
+    model.prefill(prompt, 0, kv)
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill {args.prompt} tokens in {prefill_s:.2f}s ({args.prompt / prefill_s:.1f} tok/s)")
+
+    start = args.prompt
+    if args.warmup:
+        model.decode_greedy(start, args.warmup, kv)
+    be.synchronize()
+    t0 = time.perf_counter()
+    toks = model.decode_greedy(start + args.warmup, args.steps, kv)
+    be.synchronize()
+    dt = time.perf_counter() - t0
+    tps = args.steps / dt
+    pos0 = start + args.warmup
+    bytes_tok = wbytes + sum(kv_bytes_per_token(mc, p) for p in range(pos0, pos0 + args.steps)) / args.steps
+    hbm_gbs = bytes_tok * tps / 1e9
+    log(f"decode {args.steps} steps in {dt * 1e3:.1f} ms: {tps:.1f} tok/s, "
+        f"{hbm_gbs:.0f} GB/s ({100 * hbm_gbs / PEAK_HBM_GBS:.1f}% of peak); "
+        f"first tokens {toks[:6].tolist()}")
+
+    # Per-projection launch timing (HIP events, the backend's stream), rotating
+    # over all layers so every launch streams weights from HBM.
+    per = {}
+    for which in model.PROJECTIONS:
+        us, nb = model.profile_projection(kv, which, args.profile_iters)
+        launches = 1 if which == "lm_head" else mc.num_hidden_layers
+        per[which] = {"avg_us": round(us, 2), "bytes": nb, "gbs": round(nb / us / 1e3, 1),
+                      "us_per_token": round(us * launches, 1)}
+        log(f"  {which:8s} {us:8.2f} us/launch  {nb / 1e6:8.2f} MB  {nb / us / 1e3:7.1f} GB/s")
+    dom = max(per, key=lambda k: per[k]["us_per_token"])
+    d = per[dom]
+    achieved = d["bytes"] / d["avg_us"] / 1e3
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": f"{dom} projection GEMV ({d['bytes']} algorithmic weight bytes/launch)"}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(llrs, model, args.cpu_seconds)
+        log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
+
+    out = {
+        "metric": METRIC, "value": round(tps, 3), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * dt / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random-init N(0,0.02) weights, q4km-quantized in HBM; random prompt ids)",
+        "config": {"workload": "cfg5: Qwen2.5-7B-shape q4km, 512-token prefill then batch-1 greedy "
+                               "decode", "prompt_tokens": args.prompt, "decode_start_pos": pos0,
+                   "context": args.context, "global_batch": 1, "parallelism": "none"},
+        "hbm_gbps": round(hbm_gbs, 1), "hbm_pct_peak": round(100 * hbm_gbs / PEAK_HBM_GBS, 2),
+        "bytes_per_token": int(bytes_tok), "prefill_tps": round(args.prompt / prefill_s, 2),
+        "model_gen_s": round(gen_s, 2), "roofline": roofline, "cpu_baseline": cpu,
+        "projections": per,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

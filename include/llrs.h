@@ -150,8 +150,13 @@ typedef struct {
 } llrs_synth_config;
 /* Writes a GGUF v3 file with the synthetic model (pre-quantized tensors). */
 int llrs_synth_write_gguf(const llrs_synth_config *cfg, const char *path);
-/* Builds the same model directly in HBM without a file. */
+/* Builds the same model directly in HBM without a file: generated and
+ * quantized on the GPU with the same functions, so its tensors hold exactly
+ * the bytes llrs_synth_write_gguf writes for the same config. */
 int llrs_model_synthetic(llrs_backend *b, const llrs_synth_config *cfg, llrs_model **out);
+/* Writes a loaded model back to a GGUF v3 file: matrices in their native
+ * block bytes, norms and biases as F32 (as loaded). */
+int llrs_model_export_gguf(const llrs_model *m, const char *path);
 
 /* KVCache::new + InferenceBuffers::new (src/cache.rs:13-36, 80-101): a
  * device-resident f32 KV cache, layout [layer][pos][kv_width] as the
@@ -179,6 +184,16 @@ int llrs_argmax(llrs_kv *kv, uint32_t *out_token);
  * KVCache::{k,v}_cache[layer][0 .. n) (src/cache.rs:5-7). */
 int llrs_read_logits(llrs_kv *kv, float *out, size_t n);
 int llrs_read_kv(llrs_kv *kv, size_t layer, int which /*0 = K, 1 = V*/, float *out, size_t n);
+
+/* Measurement hook (no reference counterpart; llama-bench times whole steps,
+ * src/bin/llama-bench.rs:117-126): times the decode step's launch for one
+ * projection with HIP events on the backend's stream.  `which`: 0 q, 1 k,
+ * 2 v, 3 o, 4 gate, 5 up, 6 down, 7 LM head (LM head: one matrix; the others
+ * rotate over every layer so each launch streams fresh weights).  Runs
+ * `iters` rounds; returns the mean launch time in microseconds and the
+ * matrix bytes one launch reads. */
+int llrs_profile_projection(llrs_model *m, llrs_kv *kv, int which, int iters, double *avg_us,
+                            size_t *bytes_per_launch);
 
 #ifdef __cplusplus
 }

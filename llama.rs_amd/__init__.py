@@ -108,6 +108,7 @@ SIGNATURES = [
     ("llrs_model_weight_bytes", SZ, [P]),
     ("llrs_synth_write_gguf", C.c_int, [C.POINTER(_SynthConfig), C.c_char_p]),
     ("llrs_model_synthetic", C.c_int, [P, C.POINTER(_SynthConfig), C.POINTER(P)]),
+    ("llrs_model_export_gguf", C.c_int, [P, C.c_char_p]),
     ("llrs_kv_create", C.c_int, [P, SZ, C.POINTER(P)]),
     ("llrs_kv_free", None, [P]),
     ("llrs_kv_reset", C.c_int, [P]),
@@ -117,6 +118,8 @@ SIGNATURES = [
     ("llrs_argmax", C.c_int, [P, U32P]),
     ("llrs_read_logits", C.c_int, [P, F32P, SZ]),
     ("llrs_read_kv", C.c_int, [P, SZ, C.c_int, F32P, SZ]),
+    ("llrs_profile_projection", C.c_int, [P, P, C.c_int, C.c_int, C.POINTER(C.c_double),
+                                          C.POINTER(SZ)]),
 ]
 
 

@@ -26,7 +26,9 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-I", s
           "-I", str(PKG.parent / "include")]
 HIP_FLAGS = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-munsafe-fp-atomics"]
-HOST_ONLY = {"quantize.cpp": ["-ffp-contract=off"], "synth.cpp": ["-ffp-contract=off"]}
+# The shared host/device encoders must evaluate f32 exactly as written.
+PER_FILE = {"quantize.hip": ["-ffp-contract=off"], "synth.cpp": ["-ffp-contract=off"],
+            "model.cpp": ["-ffp-contract=off"]}
 
 
 def sources():
@@ -38,8 +40,7 @@ def compile_one(src: pathlib.Path) -> pathlib.Path:
     cmd = [HIPCC] + COMMON
     if src.suffix == ".hip":
         cmd += HIP_FLAGS + ["-x", "hip"]
-    else:
-        cmd += HOST_ONLY.get(src.name, [])
+    cmd += PER_FILE.get(src.name, [])
     cmd += ["-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(l for l in (res.stdout + res.stderr).splitlines()

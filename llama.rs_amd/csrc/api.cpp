@@ -53,6 +53,33 @@ static int validate_matvec(const llrs_tensor *w, size_t nx, size_t ny) {
   return LLRS_OK;
 }
 
+int tensor_alloc(llrs_backend *b, uint32_t ty, size_t rows, size_t cols, llrs_tensor **out) {
+  *out = nullptr;
+  llrs_tensor *t = new (std::nothrow) llrs_tensor();
+  if (!t) return set_error(LLRS_E_OOM, "out of host memory");
+  t->b = b;
+  t->type = ty;
+  t->rows = rows;
+  t->cols = cols;
+  t->row_bytes = row_bytes(ty, cols);
+  t->nbytes = t->row_bytes * rows;
+  hipError_t e = hipMalloc(&t->dev, t->nbytes + kTensorTailPad);
+  if (e != hipSuccess) {
+    delete t;
+    return set_error(e == hipErrorOutOfMemory ? LLRS_E_OOM : LLRS_E_HIP,
+                     "hipMalloc(%zu) failed: %s", rows * row_bytes(ty, cols) + kTensorTailPad,
+                     hipGetErrorString(e));
+  }
+  e = hipMemsetAsync(t->dev + t->nbytes, 0, kTensorTailPad, b->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(t->dev);
+    delete t;
+    return set_error(LLRS_E_HIP, "hipMemsetAsync failed: %s", hipGetErrorString(e));
+  }
+  *out = t;
+  return LLRS_OK;
+}
+
 }  // namespace llrs
 
 using namespace llrs;
@@ -133,22 +160,10 @@ int llrs_tensor_upload(llrs_backend *b, const void *bytes, size_t nbytes, uint32
                      type_name(ty), nbytes, expected);
   if (nbytes && !bytes) return set_error(LLRS_E_INVALID, "bytes is NULL");
   LLRS_HIP(hipSetDevice(b->device));
-  llrs_tensor *t = new (std::nothrow) llrs_tensor();
-  if (!t) return set_error(LLRS_E_OOM, "out of host memory");
-  t->b = b;
-  t->type = ty;
-  t->rows = rows;
-  t->cols = cols;
-  t->row_bytes = row_bytes(ty, cols);
-  t->nbytes = nbytes;
-  hipError_t e = hipMalloc(&t->dev, nbytes + kTensorTailPad);
-  if (e != hipSuccess) {
-    delete t;
-    return set_error(e == hipErrorOutOfMemory ? LLRS_E_OOM : LLRS_E_HIP,
-                     "hipMalloc(%zu) failed: %s", nbytes + kTensorTailPad, hipGetErrorString(e));
-  }
-  e = hipMemsetAsync(t->dev + nbytes, 0, kTensorTailPad, b->stream);
-  if (e == hipSuccess && nbytes)
+  llrs_tensor *t = nullptr;
+  LLRS_TRY(tensor_alloc(b, ty, rows, cols, &t));
+  hipError_t e = hipSuccess;
+  if (nbytes)
     e = hipMemcpyAsync(t->dev, bytes, nbytes, hipMemcpyHostToDevice, b->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(b->stream);
   if (e != hipSuccess) {

@@ -79,7 +79,13 @@ void clear_error();
 // vectorised loads that round a row span outward never leave the allocation.
 constexpr size_t kTensorTailPad = 256;
 
+// Allocates an uninitialised device tensor of native layout (tail pad zeroed).
+int tensor_alloc(llrs_backend *b, uint32_t ty, size_t rows, size_t cols, llrs_tensor **out);
+
 }  // namespace llrs
+
+struct llrs_backend;
+struct llrs_tensor;
 
 struct llrs_backend {
   int device = 0;

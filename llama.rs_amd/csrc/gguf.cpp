@@ -260,6 +260,17 @@ void GgufWriter::add_str(const std::string &k, const std::string &v) {
 }
 
 int GgufWriter::write(const std::string &path, const std::vector<GgufOutTensor> &tensors) const {
+  std::vector<size_t> sizes;
+  for (const auto &t : tensors) sizes.push_back(t.bytes.size());
+  return write_streamed(path, tensors, sizes, [&](size_t i, std::vector<uint8_t> &buf) {
+    buf = tensors[i].bytes;
+    return (int)LLRS_OK;
+  });
+}
+
+int GgufWriter::write_streamed(const std::string &path, const std::vector<GgufOutTensor> &tensors,
+                               const std::vector<size_t> &nbytes,
+                               const std::function<int(size_t, std::vector<uint8_t> &)> &fetch) const {
   const size_t align = 32;
   std::vector<uint8_t> head;
   head.insert(head.end(), {'G', 'G', 'U', 'F'});
@@ -268,26 +279,34 @@ int GgufWriter::write(const std::string &path, const std::vector<GgufOutTensor> 
   put_le(head, n_meta_, 8);
   head.insert(head.end(), meta_.begin(), meta_.end());
   uint64_t off = 0;
-  for (const auto &t : tensors) {
+  for (size_t i = 0; i < tensors.size(); i++) {
+    const auto &t = tensors[i];
     put_str(head, t.name);
     put_le(head, t.dims.size(), 4);
     for (uint64_t d : t.dims) put_le(head, d, 8);
     put_le(head, t.type, 4);
     put_le(head, off, 8);
-    off += (t.bytes.size() + align - 1) / align * align;
+    off += (nbytes[i] + align - 1) / align * align;
   }
   while (head.size() % align) head.push_back(0);
   FILE *f = fopen(path.c_str(), "wb");
   if (!f) return set_error(LLRS_E_IO, "failed to create %s", path.c_str());
   bool ok = fwrite(head.data(), 1, head.size(), f) == head.size();
   static const uint8_t zeros[32] = {0};
-  for (const auto &t : tensors) {
-    if (!ok) break;
-    ok = fwrite(t.bytes.data(), 1, t.bytes.size(), f) == t.bytes.size();
-    size_t pad = (align - t.bytes.size() % align) % align;
+  std::vector<uint8_t> buf;
+  int rc = LLRS_OK;
+  for (size_t i = 0; i < tensors.size() && ok; i++) {
+    rc = fetch(i, buf);
+    if (rc != LLRS_OK || buf.size() != nbytes[i]) {
+      ok = false;
+      break;
+    }
+    ok = fwrite(buf.data(), 1, buf.size(), f) == buf.size();
+    size_t pad = (align - buf.size() % align) % align;
     if (ok && pad) ok = fwrite(zeros, 1, pad, f) == pad;
   }
   if (fclose(f) != 0) ok = false;
+  if (rc != LLRS_OK) return rc;
   if (!ok) return set_error(LLRS_E_IO, "failed to write %s", path.c_str());
   return LLRS_OK;
 }

@@ -3,6 +3,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <string>
 #include <vector>
@@ -62,6 +63,11 @@ class GgufWriter {
   void add_str(const std::string &k, const std::string &v);
   // Writes header, metadata, tensor table and 32-byte aligned data.
   int write(const std::string &path, const std::vector<GgufOutTensor> &tensors) const;
+  // Streaming form: `tensors` carry name/dims/type only; `nbytes[i]` is the
+  // size of tensor i and fetch(i, buf) fills its bytes just before writing.
+  int write_streamed(const std::string &path, const std::vector<GgufOutTensor> &tensors,
+                     const std::vector<size_t> &nbytes,
+                     const std::function<int(size_t, std::vector<uint8_t> &)> &fetch) const;
 
  private:
   std::vector<uint8_t> meta_;

@@ -23,6 +23,7 @@
 #include "gemv.h"
 #include "gguf.h"
 #include "quantize.h"
+#include "quant_encode.h"
 #include "synth.h"
 
 namespace llrs {
@@ -31,6 +32,14 @@ struct DevLayer {
   llrs_tensor *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr, *gate = nullptr,
               *up = nullptr, *down = nullptr;
   float *attn_norm = nullptr, *ffn_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+};
+
+// A named model tensor in load order: a matrix, or an f32 vector.
+struct TensorRef {
+  std::string name;
+  llrs_tensor *mat;
+  float *vec;
+  size_t len;
 };
 
 }  // namespace llrs
@@ -43,6 +52,7 @@ struct llrs_model {
   std::vector<llrs::DevLayer> layers;
   std::vector<llrs_tensor *> tensors;
   std::vector<void *> vecs;
+  std::vector<llrs::TensorRef> refs;
   size_t weight_bytes = 0;
 };
 
@@ -63,9 +73,10 @@ struct llrs_kv {
 
 namespace llrs {
 
-using Fetch = std::function<int(const std::string &name, bool &present, uint32_t &type,
-                                std::vector<uint64_t> &dims, const uint8_t *&data, size_t &nbytes,
-                                std::vector<uint8_t> &storage)>;
+// Materialises matrix `name` ([rows, cols]) as a device tensor.
+using MatFn = std::function<int(const std::string &name, size_t rows, size_t cols, llrs_tensor **out)>;
+// Writes vector `name` (length len) as f32 into dst (device); zeros if absent and allowed.
+using VecFn = std::function<int(const std::string &name, size_t len, bool zeros_if_missing, float *dst)>;
 
 static int dev_alloc(std::vector<void *> &list, void **p, size_t bytes) {
   LLRS_HIP(hipMalloc(p, bytes ? bytes : 4));
@@ -105,102 +116,113 @@ static void host_to_f32(uint32_t ty, const uint8_t *src, size_t n, float *dst) {
   }
 }
 
-// load_gguf_matrix + check_matrix + maybe_quantize (src/loader.rs:406-456, 497-507).
-static int load_matrix(llrs_model *m, const Fetch &fetch, const std::string &name, size_t rows,
-                       size_t cols, int quantization, llrs_tensor **out) {
-  bool present = false;
-  uint32_t ty = 0;
-  std::vector<uint64_t> dims;
-  const uint8_t *data = nullptr;
-  size_t nbytes = 0;
-  std::vector<uint8_t> storage;
-  LLRS_TRY(fetch(name, present, ty, dims, data, nbytes, storage));
-  if (!present) return set_error(LLRS_E_INVALID, "missing GGUF tensor %s", name.c_str());
-  if (dims.size() > 2)
-    return set_error(LLRS_E_INVALID, "tensor %s has %zu dimensions; Qwen2 loader supports 1D/2D weights",
-                     name.c_str(), dims.size());
-  size_t r = dims.size() == 2 ? dims[1] : 0, c = dims[0];
-  if (dims.size() != 2 || r != rows || c != cols)
-    return set_error(LLRS_E_INVALID, "tensor %s has shape [%zu, %zu], expected [%zu, %zu]",
-                     name.c_str(), dims.size() == 2 ? r : c, dims.size() == 2 ? c : (size_t)0,
-                     rows, cols);
-  std::vector<uint8_t> qbuf;
-  if (quantization != LLRS_QUANT_NONE &&
-      (ty == LLRS_F32 || ty == LLRS_F16 || ty == LLRS_BF16)) {
-    std::vector<float> vals(rows * cols);
-    host_to_f32(ty, data, rows * cols, vals.data());
-    uint32_t want = recipe_type(quantization, name, cols);
-    if (want == LLRS_F32) {
-      qbuf.resize(vals.size() * 4);
-      memcpy(qbuf.data(), vals.data(), qbuf.size());
-      ty = LLRS_F32;
-    } else {
-      ty = quantize_rows(want, vals.data(), rows, cols, qbuf);
-    }
-    data = qbuf.data();
-    nbytes = qbuf.size();
-  }
+// maybe_quantize (src/loader.rs:406-447) on the GPU: f32 values are uploaded
+// and encoded by the same encoders the host quantizer uses (bit-identical).
+static int quantize_on_device(llrs_backend *b, uint32_t want, const float *vals, size_t rows,
+                              size_t cols, llrs_tensor **out) {
+  if (want == LLRS_F32) return llrs_tensor_upload(b, vals, rows * cols * 4, LLRS_F32, rows, cols, out);
+  float *dv = nullptr;
+  LLRS_HIP(hipMalloc(&dv, rows * cols * 4 + 4));
   llrs_tensor *t = nullptr;
-  LLRS_TRY(llrs_tensor_upload(m->b, data, nbytes, ty, rows, cols, &t));
-  m->tensors.push_back(t);
+  int rc = tensor_alloc(b, want, rows, cols, &t);
+  hipError_t e = hipSuccess;
+  if (rc == LLRS_OK) {
+    e = hipMemcpyAsync(dv, vals, rows * cols * 4, hipMemcpyHostToDevice, b->stream);
+    if (e == hipSuccess) rc = launch_encode(want, dv, rows, cols, t->dev, t->row_bytes, b->stream);
+    if (e == hipSuccess && rc == LLRS_OK) e = hipStreamSynchronize(b->stream);
+  }
+  (void)hipFree(dv);
+  if (rc == LLRS_OK && e != hipSuccess) rc = set_error(LLRS_E_HIP, "device quantization failed: %s", hipGetErrorString(e));
+  if (rc != LLRS_OK) {
+    if (t) llrs_tensor_free(t);
+    return rc;
+  }
   *out = t;
   return LLRS_OK;
 }
 
+// load_gguf_matrix + check_matrix + maybe_quantize (src/loader.rs:406-456, 497-507).
+static int gguf_matrix(llrs_model *m, const GgufFile &g, const std::string &name, size_t rows,
+                       size_t cols, int quantization, llrs_tensor **out) {
+  const GgufTensorInfo *t = g.tensor(name);
+  if (!t) return set_error(LLRS_E_INVALID, "missing GGUF tensor %s", name.c_str());
+  const std::vector<uint64_t> &dims = t->dims;
+  if (dims.size() > 2)
+    return set_error(LLRS_E_INVALID, "tensor %s has %zu dimensions; Qwen2 loader supports 1D/2D weights",
+                     name.c_str(), dims.size());
+  if (dims.size() != 2 || dims[1] != rows || dims[0] != cols)
+    return set_error(LLRS_E_INVALID, "tensor %s has shape [%llu, %llu], expected [%zu, %zu]",
+                     name.c_str(), (unsigned long long)(dims.size() == 2 ? dims[1] : dims[0]),
+                     (unsigned long long)(dims.size() == 2 ? dims[0] : 0), rows, cols);
+  uint32_t ty = t->type;
+  if (quantization != LLRS_QUANT_NONE && (ty == LLRS_F32 || ty == LLRS_F16 || ty == LLRS_BF16)) {
+    std::vector<float> vals(rows * cols);
+    host_to_f32(ty, g.data(*t), rows * cols, vals.data());
+    return quantize_on_device(m->b, recipe_type(quantization, name, cols), vals.data(), rows, cols, out);
+  }
+  return llrs_tensor_upload(m->b, g.data(*t), t->nbytes, ty, rows, cols, out);
+}
+
 // load_gguf_vector (src/loader.rs:509-517): any type, dequantized bit-exactly
-// (value_at) on the device into an f32 vector.
-static int load_vector(llrs_model *m, const Fetch &fetch, const std::string &name, size_t len,
-                       bool zeros_if_missing, float **out) {
-  bool present = false;
-  uint32_t ty = 0;
-  std::vector<uint64_t> dims;
-  const uint8_t *data = nullptr;
-  size_t nbytes = 0;
-  std::vector<uint8_t> storage;
-  LLRS_TRY(fetch(name, present, ty, dims, data, nbytes, storage));
-  LLRS_TRY(dev_alloc(m->vecs, (void **)out, len * 4));
-  if (!present) {
+// (value_at) on the device into an f32 vector; missing Q/K/V biases are zeros
+// (src/loader.rs:528-531).
+static int gguf_vector(llrs_model *m, const GgufFile &g, const std::string &name, size_t len,
+                       bool zeros_if_missing, float *dst) {
+  const GgufTensorInfo *t = g.tensor(name);
+  if (!t) {
     if (!zeros_if_missing) return set_error(LLRS_E_INVALID, "missing GGUF tensor %s", name.c_str());
-    LLRS_HIP(hipMemsetAsync(*out, 0, len * 4, m->b->stream));  // missing Q/K/V bias -> zeros
+    LLRS_HIP(hipMemsetAsync(dst, 0, len * 4, m->b->stream));
     LLRS_HIP(hipStreamSynchronize(m->b->stream));
     return LLRS_OK;
   }
-  if (dims.size() != 1 || dims[0] != len)
+  if (t->dims.size() != 1 || t->dims[0] != len)
     return set_error(LLRS_E_INVALID, "tensor %s has the wrong shape, expected [%zu]", name.c_str(), len);
-  llrs_tensor *t = nullptr;
-  LLRS_TRY(llrs_tensor_upload(m->b, data, nbytes, ty, 1, len, &t));
-  int rc = launch_dequant_row(t, 0, *out, m->b->stream);
+  llrs_tensor *tmp = nullptr;
+  LLRS_TRY(llrs_tensor_upload(m->b, g.data(*t), t->nbytes, t->type, 1, len, &tmp));
+  int rc = launch_dequant_row(tmp, 0, dst, m->b->stream);
   hipError_t e = hipStreamSynchronize(m->b->stream);
-  llrs_tensor_free(t);
+  llrs_tensor_free(tmp);
   LLRS_TRY(rc);
   if (e != hipSuccess) return set_error(LLRS_E_HIP, "vector dequant failed: %s", hipGetErrorString(e));
   return LLRS_OK;
 }
 
-static int build_model(llrs_model *m, const Fetch &fetch, int quantization) {
+static int build_model(llrs_model *m, const MatFn &mat, const VecFn &vec) {
   const llrs_model_config &c = m->cfg;
   size_t H = c.hidden_size, F = c.intermediate_size, KV = c.kv_width;
-  LLRS_TRY(load_matrix(m, fetch, "token_embd.weight", c.vocab_size, H, quantization, &m->embed));
-  LLRS_TRY(load_vector(m, fetch, "output_norm.weight", H, false, &m->norm));
+  auto M = [&](const std::string &name, size_t rows, size_t cols, llrs_tensor **out) -> int {
+    LLRS_TRY(mat(name, rows, cols, out));
+    m->tensors.push_back(*out);
+    m->refs.push_back({name, *out, nullptr, 0});
+    return LLRS_OK;
+  };
+  auto V = [&](const std::string &name, size_t len, bool zeros, float **out) -> int {
+    LLRS_TRY(dev_alloc(m->vecs, (void **)out, len * 4));
+    LLRS_TRY(vec(name, len, zeros, *out));
+    m->refs.push_back({name, nullptr, *out, len});
+    return LLRS_OK;
+  };
+  LLRS_TRY(M("token_embd.weight", c.vocab_size, H, &m->embed));
+  LLRS_TRY(V("output_norm.weight", H, false, &m->norm));
   m->layers.resize(c.num_hidden_layers);
   for (size_t i = 0; i < c.num_hidden_layers; i++) {
     DevLayer &L = m->layers[i];
     std::string p = "blk." + std::to_string(i) + ".";
-    LLRS_TRY(load_vector(m, fetch, p + "attn_norm.weight", H, false, &L.attn_norm));
-    LLRS_TRY(load_matrix(m, fetch, p + "attn_q.weight", H, H, quantization, &L.q));
-    LLRS_TRY(load_vector(m, fetch, p + "attn_q.bias", H, true, &L.bq));
-    LLRS_TRY(load_matrix(m, fetch, p + "attn_k.weight", KV, H, quantization, &L.k));
-    LLRS_TRY(load_vector(m, fetch, p + "attn_k.bias", KV, true, &L.bk));
-    LLRS_TRY(load_matrix(m, fetch, p + "attn_v.weight", KV, H, quantization, &L.v));
-    LLRS_TRY(load_vector(m, fetch, p + "attn_v.bias", KV, true, &L.bv));
-    LLRS_TRY(load_matrix(m, fetch, p + "attn_output.weight", H, H, quantization, &L.o));
-    LLRS_TRY(load_vector(m, fetch, p + "ffn_norm.weight", H, false, &L.ffn_norm));
-    LLRS_TRY(load_matrix(m, fetch, p + "ffn_gate.weight", F, H, quantization, &L.gate));
-    LLRS_TRY(load_matrix(m, fetch, p + "ffn_up.weight", F, H, quantization, &L.up));
-    LLRS_TRY(load_matrix(m, fetch, p + "ffn_down.weight", H, F, quantization, &L.down));
+    LLRS_TRY(V(p + "attn_norm.weight", H, false, &L.attn_norm));
+    LLRS_TRY(M(p + "attn_q.weight", H, H, &L.q));
+    LLRS_TRY(V(p + "attn_q.bias", H, true, &L.bq));
+    LLRS_TRY(M(p + "attn_k.weight", KV, H, &L.k));
+    LLRS_TRY(V(p + "attn_k.bias", KV, true, &L.bk));
+    LLRS_TRY(M(p + "attn_v.weight", KV, H, &L.v));
+    LLRS_TRY(V(p + "attn_v.bias", KV, true, &L.bv));
+    LLRS_TRY(M(p + "attn_output.weight", H, H, &L.o));
+    LLRS_TRY(V(p + "ffn_norm.weight", H, false, &L.ffn_norm));
+    LLRS_TRY(M(p + "ffn_gate.weight", F, H, &L.gate));
+    LLRS_TRY(M(p + "ffn_up.weight", F, H, &L.up));
+    LLRS_TRY(M(p + "ffn_down.weight", H, F, &L.down));
   }
   if (c.tie_word_embeddings) m->lm_head = m->embed;
-  else LLRS_TRY(load_matrix(m, fetch, "output.weight", c.vocab_size, H, quantization, &m->lm_head));
+  else LLRS_TRY(M("output.weight", c.vocab_size, H, &m->lm_head));
   // Bytes one decode step streams from HBM for weights.
   size_t wb = m->lm_head->nbytes + m->embed->row_bytes + H * 4;
   for (auto &L : m->layers)
@@ -260,19 +282,13 @@ static int load_gguf_impl(llrs_backend *b, const char *path, int quantization, l
   if (!m) return set_error(LLRS_E_OOM, "out of host memory");
   m->b = b;
   m->cfg = c;
-  Fetch fetch = [&](const std::string &name, bool &present, uint32_t &type,
-                    std::vector<uint64_t> &dims, const uint8_t *&data, size_t &nbytes,
-                    std::vector<uint8_t> &) -> int {
-    const GgufTensorInfo *t = g.tensor(name);
-    present = t != nullptr;
-    if (!t) return LLRS_OK;
-    type = t->type;
-    dims = t->dims;
-    data = g.data(*t);
-    nbytes = t->nbytes;
-    return LLRS_OK;
+  MatFn mat = [&](const std::string &name, size_t rows, size_t cols, llrs_tensor **t) {
+    return gguf_matrix(m, g, name, rows, cols, quantization, t);
   };
-  int rc = build_model(m, fetch, quantization);
+  VecFn vec = [&](const std::string &name, size_t len, bool zeros, float *dst) {
+    return gguf_vector(m, g, name, len, zeros, dst);
+  };
+  int rc = build_model(m, mat, vec);
   if (rc != LLRS_OK) {
     free_model(m);
     return rc;
@@ -300,10 +316,36 @@ static int synth_config_to_model(const llrs_synth_config &s, llrs_model_config &
 
 // ------------------------------------------------------------------ decode step
 
+enum Proj { P_Q = 0, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN, P_LM_HEAD };
+
+// The decode step's launch for projection `which` of layer `l`; the bench's
+// per-kernel timing calls this same function.
+static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hipStream_t s) {
+  if (which == P_LM_HEAD) return launch_gemv_generic(m->lm_head, kv->hidden, kv->logits, nullptr, false, s);
+  DevLayer &L = m->layers[l];
+  switch (which) {
+    case P_Q: return launch_gemv_generic(L.q, kv->hidden, kv->q, L.bq, false, s);
+    case P_K: return launch_gemv_generic(L.k, kv->hidden, kv->k, L.bk, false, s);
+    case P_V: return launch_gemv_generic(L.v, kv->hidden, kv->v, L.bv, false, s);
+    case P_O: return launch_gemv_generic(L.o, kv->attn, kv->residual, nullptr, true, s);
+    case P_GATE: return launch_gemv_generic(L.gate, kv->hidden, kv->gate, nullptr, false, s);
+    case P_UP: return launch_gemv_generic(L.up, kv->hidden, kv->up, nullptr, false, s);
+    case P_DOWN: return launch_gemv_generic(L.down, kv->act, kv->residual, nullptr, true, s);
+    default: return set_error(LLRS_E_INVALID, "unknown projection %d", which);
+  }
+}
+
+static size_t projection_bytes(llrs_model *m, int which) {
+  if (which == P_LM_HEAD) return m->lm_head->nbytes;
+  const DevLayer &L = m->layers[0];
+  const llrs_tensor *t[] = {L.q, L.k, L.v, L.o, L.gate, L.up, L.down};
+  return t[which]->nbytes;
+}
+
 static int enqueue_step(llrs_model *m, llrs_kv *kv, int mode) {
   const llrs_model_config &c = m->cfg;
   hipStream_t s = m->b->stream;
-  int H = (int)c.hidden_size, F = (int)c.intermediate_size, KVW = (int)c.kv_width;
+  int H = (int)c.hidden_size, F = (int)c.intermediate_size;
   int nh = (int)c.num_attention_heads, nkv = (int)c.num_key_value_heads, hd = (int)c.head_dim;
   size_t layer_stride = kv->max_seq_len * c.kv_width;
   LLRS_TRY(launch_embed(m->embed, kv->tok_by_pos, kv->pos, kv->residual, s));
@@ -311,23 +353,22 @@ static int enqueue_step(llrs_model *m, llrs_kv *kv, int mode) {
     DevLayer &L = m->layers[l];
     float *kc = kv->k_cache + l * layer_stride, *vc = kv->v_cache + l * layer_stride;
     LLRS_TRY(launch_rmsnorm(kv->residual, L.attn_norm, kv->hidden, H, c.rms_norm_eps, s));
-    LLRS_TRY(launch_gemv_generic(L.q, kv->hidden, kv->q, L.bq, false, s));
-    LLRS_TRY(launch_gemv_generic(L.k, kv->hidden, kv->k, L.bk, false, s));
-    LLRS_TRY(launch_gemv_generic(L.v, kv->hidden, kv->v, L.bv, false, s));
+    LLRS_TRY(launch_projection(m, kv, l, P_Q, s));
+    LLRS_TRY(launch_projection(m, kv, l, P_K, s));
+    LLRS_TRY(launch_projection(m, kv, l, P_V, s));
     LLRS_TRY(launch_rope_kv(kv->q, kv->k, kv->v, kv->rope, kv->pos, kc, vc, nh, nkv, hd, s));
     LLRS_TRY(launch_attention(kv->q, kc, vc, kv->pos, kv->scores, kv->attn, nh, nkv, hd,
                               (int)kv->max_seq_len, s));
-    LLRS_TRY(launch_gemv_generic(L.o, kv->attn, kv->residual, nullptr, true, s));
+    LLRS_TRY(launch_projection(m, kv, l, P_O, s));
     LLRS_TRY(launch_rmsnorm(kv->residual, L.ffn_norm, kv->hidden, H, c.rms_norm_eps, s));
-    LLRS_TRY(launch_gemv_generic(L.gate, kv->hidden, kv->gate, nullptr, false, s));
-    LLRS_TRY(launch_gemv_generic(L.up, kv->hidden, kv->up, nullptr, false, s));
+    LLRS_TRY(launch_projection(m, kv, l, P_GATE, s));
+    LLRS_TRY(launch_projection(m, kv, l, P_UP, s));
     LLRS_TRY(launch_silu_mul(kv->gate, kv->up, kv->act, F, s));
-    LLRS_TRY(launch_gemv_generic(L.down, kv->act, kv->residual, nullptr, true, s));
+    LLRS_TRY(launch_projection(m, kv, l, P_DOWN, s));
   }
-  (void)KVW;
   if (mode == LLRS_LOGITS_COMPUTE) {
     LLRS_TRY(launch_rmsnorm(kv->residual, m->norm, kv->hidden, H, c.rms_norm_eps, s));
-    LLRS_TRY(launch_gemv_generic(m->lm_head, kv->hidden, kv->logits, nullptr, false, s));
+    LLRS_TRY(launch_projection(m, kv, 0, P_LM_HEAD, s));
     LLRS_TRY(launch_argmax(kv->logits, (int)c.vocab_size, kv->pos, kv->tok_by_pos, kv->next_token,
                            1, s));
   } else {
@@ -514,31 +555,86 @@ int llrs_model_synthetic(llrs_backend *b, const llrs_synth_config *cfg, llrs_mod
   if (!m) return set_error(LLRS_E_OOM, "out of host memory");
   m->b = b;
   m->cfg = c;
-  Fetch fetch = [&](const std::string &name, bool &present, uint32_t &type,
-                    std::vector<uint64_t> &dims, const uint8_t *&data, size_t &nbytes,
-                    std::vector<uint8_t> &storage) -> int {
-    present = false;
-    for (size_t i = 0; i < specs.size(); i++) {
-      if (specs[i].name != name) continue;
-      GgufOutTensor t;
-      LLRS_TRY(synth_tensor(*cfg, i, specs[i], t));
-      present = true;
-      type = t.type;
-      dims = t.dims;
-      storage.swap(t.bytes);
-      data = storage.data();
-      nbytes = storage.size();
-      break;
-    }
-    return LLRS_OK;
+  // Generated and encoded on the GPU with the host generator's functions, so
+  // the bytes equal those llrs_synth_write_gguf writes for the same config.
+  auto find = [&](const std::string &name) -> long {
+    for (size_t i = 0; i < specs.size(); i++)
+      if (specs[i].name == name) return (long)i;
+    return -1;
   };
-  int rc = build_model(m, fetch, LLRS_QUANT_NONE);
+  MatFn mat = [&](const std::string &name, size_t rows, size_t cols, llrs_tensor **t) -> int {
+    long i = find(name);
+    if (i < 0) return set_error(LLRS_E_INVALID, "missing tensor %s", name.c_str());
+    uint32_t ty = synth_type(*cfg, specs[i]);
+    LLRS_TRY(tensor_alloc(b, ty, rows, cols, t));
+    int rc = launch_synth_encode(ty, enc::tensor_key(cfg->seed, (uint64_t)i), rows, cols,
+                                 cfg->weight_std, false, (*t)->dev, (*t)->row_bytes, b->stream);
+    if (rc != LLRS_OK) {
+      llrs_tensor_free(*t);
+      *t = nullptr;
+    }
+    return rc;
+  };
+  VecFn vec = [&](const std::string &name, size_t len, bool, float *dst) -> int {
+    long i = find(name);
+    if (i < 0) return set_error(LLRS_E_INVALID, "missing tensor %s", name.c_str());
+    return launch_synth_encode(LLRS_F32, enc::tensor_key(cfg->seed, (uint64_t)i), 1, len,
+                               cfg->weight_std, specs[i].kind == SynthSpec::GAIN,
+                               (uint8_t *)dst, len * 4, b->stream);
+  };
+  int rc = build_model(m, mat, vec);
+  if (rc == LLRS_OK) {
+    hipError_t e = hipStreamSynchronize(b->stream);
+    if (e != hipSuccess) rc = set_error(LLRS_E_HIP, "synthetic generation failed: %s", hipGetErrorString(e));
+  }
   if (rc != LLRS_OK) {
     free_model(m);
     return rc;
   }
   *out = m;
   return LLRS_OK;
+}
+
+int llrs_model_export_gguf(const llrs_model *m, const char *path) {
+  clear_error();
+  if (!m || !path) return set_error(LLRS_E_INVALID, "model/path is NULL");
+  LLRS_HIP(hipSetDevice(m->b->device));
+  const llrs_model_config &c = m->cfg;
+  GgufWriter w;
+  w.add_str("general.architecture", "qwen2");
+  w.add_u32("general.alignment", 32);
+  w.add_u32("qwen2.embedding_length", (uint32_t)c.hidden_size);
+  w.add_u32("qwen2.feed_forward_length", (uint32_t)c.intermediate_size);
+  w.add_u32("qwen2.attention.head_count", (uint32_t)c.num_attention_heads);
+  w.add_u32("qwen2.attention.head_count_kv", (uint32_t)c.num_key_value_heads);
+  w.add_u32("qwen2.block_count", (uint32_t)c.num_hidden_layers);
+  w.add_u32("qwen2.context_length", (uint32_t)c.max_position_embeddings);
+  w.add_f32("qwen2.attention.layer_norm_rms_epsilon", c.rms_norm_eps);
+  w.add_f32("qwen2.rope.freq_base", c.rope_theta);
+  std::vector<GgufOutTensor> infos;
+  std::vector<size_t> sizes;
+  for (const auto &r : m->refs) {
+    GgufOutTensor t;
+    t.name = r.name;
+    if (r.mat) {
+      t.dims = {r.mat->cols, r.mat->rows};
+      t.type = r.mat->type;
+      sizes.push_back(r.mat->nbytes);
+    } else {
+      t.dims = {r.len};
+      t.type = LLRS_F32;
+      sizes.push_back(r.len * 4);
+    }
+    infos.push_back(t);
+  }
+  return w.write_streamed(path, infos, sizes, [&](size_t i, std::vector<uint8_t> &buf) -> int {
+    const TensorRef &r = m->refs[i];
+    buf.resize(sizes[i]);
+    const void *src = r.mat ? (const void *)r.mat->dev : (const void *)r.vec;
+    LLRS_HIP(hipMemcpyAsync(buf.data(), src, sizes[i], hipMemcpyDeviceToHost, m->b->stream));
+    LLRS_HIP(hipStreamSynchronize(m->b->stream));
+    return LLRS_OK;
+  });
 }
 
 int llrs_kv_create(llrs_model *m, size_t max_seq_len, llrs_kv **out) {
@@ -658,6 +754,36 @@ int llrs_read_kv(llrs_kv *kv, size_t layer, int which, float *out, size_t n) {
   LLRS_HIP(hipSetDevice(kv->m->b->device));
   LLRS_HIP(hipMemcpyAsync(out, src, n * 4, hipMemcpyDeviceToHost, kv->m->b->stream));
   LLRS_HIP(hipStreamSynchronize(kv->m->b->stream));
+  return LLRS_OK;
+}
+
+int llrs_profile_projection(llrs_model *m, llrs_kv *kv, int which, int iters, double *avg_us,
+                            size_t *bytes_per_launch) {
+  clear_error();
+  if (!m || !kv || kv->m != m || !avg_us) return set_error(LLRS_E_INVALID, "bad arguments");
+  if (which < P_Q || which > P_LM_HEAD) return set_error(LLRS_E_INVALID, "unknown projection %d", which);
+  if (iters < 1) return set_error(LLRS_E_INVALID, "iters must be positive");
+  LLRS_HIP(hipSetDevice(m->b->device));
+  hipStream_t s = m->b->stream;
+  size_t layers = which == P_LM_HEAD ? 1 : m->cfg.num_hidden_layers;
+  hipEvent_t e0, e1;
+  LLRS_HIP(hipEventCreate(&e0));
+  LLRS_HIP(hipEventCreate(&e1));
+  int rc = LLRS_OK;
+  for (size_t l = 0; l < layers && rc == LLRS_OK; l++) rc = launch_projection(m, kv, l, which, s);  // warm
+  hipError_t e = hipEventRecord(e0, s);
+  for (int it = 0; it < iters && rc == LLRS_OK && e == hipSuccess; it++)
+    for (size_t l = 0; l < layers && rc == LLRS_OK; l++) rc = launch_projection(m, kv, l, which, s);
+  if (e == hipSuccess) e = hipEventRecord(e1, s);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  LLRS_TRY(rc);
+  if (e != hipSuccess) return set_error(LLRS_E_HIP, "event timing failed: %s", hipGetErrorString(e));
+  *avg_us = 1000.0 * (double)ms / (double)(iters * layers);
+  if (bytes_per_launch) *bytes_per_launch = projection_bytes(m, which);
   return LLRS_OK;
 }
 

@@ -1,35 +1,53 @@
-// Host-side GGML quantizers: QuantTensor::quantize_{q4k,q5_0,q8_0,q6k}
-// (src/quant.rs:187-259) and their block encoders (src/quant.rs:650-967),
-// which the reference's loader calls for `--quantize q4k|q4km`
-// (src/loader.rs:406-447) and which the synthetic-model generator uses.
+// GGML block encoders and the synthetic-weight RNG, shared by host and device.
 //
-// Rust semantics kept: f32::round rounds half away from zero (roundf),
-// f32::max/min ignore NaN (fmaxf/fminf), float -> int `as` casts saturate
-// with NaN -> 0, no fused multiply-add (this file is built with
-// -ffp-contract=off), sequential f32 sums, f16 encoding round-to-nearest-even.
-#include "quantize.h"
+// The encoders restate the reference's quantizers (src/quant.rs:650-967).
+// Rust semantics are kept: f32::round = roundf (half away from zero),
+// f32::max/min = fmaxf/fminf, saturating float->int `as` casts with NaN -> 0,
+// sequential f32 sums, f16 encoding round-to-nearest-even.  Every file that
+// includes this header is compiled with -ffp-contract=off, and every
+// operation used is an IEEE-754 correctly rounded one (+ - * / sqrt, round,
+// floor, min, max), so the host build and the gfx950 build produce the same
+// bytes for the same input.
+#pragma once
 
-#include <cmath>
-#include <cstring>
+#include <stdint.h>
+#include <string.h>
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#include <hip/hip_runtime.h>
+#define LLRS_HD __host__ __device__ inline
+#else
+#include <math.h>
+#define LLRS_HD inline
+#endif
 
 namespace llrs {
+namespace enc {
 
-uint16_t f32_to_f16_bits(float f) {
-  uint32_t x;
-  memcpy(&x, &f, 4);
-  uint32_t sign = (x >> 16) & 0x8000u;
-  uint32_t ax = x & 0x7fffffffu;
+LLRS_HD uint32_t f2u(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+LLRS_HD float u2f(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// f32 -> IEEE binary16 bits, round to nearest even (half::f16::from_f32).
+LLRS_HD uint16_t f32_to_f16(float f) {
+  uint32_t x = f2u(f), sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
   if (ax >= 0x7f800000u) {
     if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
     return (uint16_t)(sign | 0x7c00u);
   }
   if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // >= 65520 rounds to inf
-  if (ax < 0x38800000u) {                                     // below 2^-14: subnormal f16
-    if (ax < 0x33000000u) return (uint16_t)sign;              // <= 2^-25 rounds to zero
-    uint32_t e = ax >> 23, m = (ax & 0x7fffffu) | 0x800000u;
-    uint32_t s = 126 - e;
-    uint32_t r = m >> s, rem = m & ((1u << s) - 1), halfway = 1u << (s - 1);
-    if (rem > halfway || (rem == halfway && (r & 1))) r++;
+  if (ax < 0x38800000u) {                                     // f16 subnormal range
+    if (ax < 0x33000000u) return (uint16_t)sign;
+    uint32_t e = ax >> 23, m = (ax & 0x7fffffu) | 0x800000u, s = 126 - e;
+    uint32_t r = m >> s, rem = m & ((1u << s) - 1), half = 1u << (s - 1);
+    if (rem > half || (rem == half && (r & 1))) r++;
     return (uint16_t)(sign | r);
   }
   uint32_t r = (ax >> 13) - (112u << 10), rem = ax & 0x1fffu;
@@ -37,7 +55,7 @@ uint16_t f32_to_f16_bits(float f) {
   return (uint16_t)(sign | r);
 }
 
-float f16_bits_to_f32_host(uint16_t h) {
+LLRS_HD float f16_to_f32(uint16_t h) {
   uint32_t sign = (uint32_t)(h & 0x8000u) << 16, exp = (h >> 10) & 0x1f, man = h & 0x3ffu, bits;
   if (exp == 0) {
     if (man == 0) {
@@ -55,56 +73,55 @@ float f16_bits_to_f32_host(uint16_t h) {
   } else {
     bits = sign | ((exp + 112) << 23) | (man << 13);
   }
-  float f;
-  memcpy(&f, &bits, 4);
-  return f;
+  return u2f(bits);
 }
 
-static inline float f16_round(float v) { return f16_bits_to_f32_host(f32_to_f16_bits(v)); }
+LLRS_HD float f16_round(float v) { return f16_to_f32(f32_to_f16(v)); }
 
-static inline void put_f16(std::vector<uint8_t> &out, float v) {
-  uint16_t h = f32_to_f16_bits(v);
-  out.push_back((uint8_t)(h & 0xff));
-  out.push_back((uint8_t)(h >> 8));
+LLRS_HD void put_f16(uint8_t *o, float v) {
+  uint16_t h = f32_to_f16(v);
+  o[0] = (uint8_t)(h & 0xff);
+  o[1] = (uint8_t)(h >> 8);
 }
 
-// Rust `as` casts from f32: saturating, NaN -> 0, truncation toward zero.
-static inline uint8_t as_u8(float f) {
-  if (std::isnan(f) || f <= 0.f) return 0;
+LLRS_HD bool is_nan(float f) { return (f2u(f) & 0x7fffffffu) > 0x7f800000u; }
+// Rust `as` from f32: saturating, NaN -> 0, truncation toward zero.
+LLRS_HD uint8_t as_u8(float f) {
+  if (is_nan(f) || f <= 0.f) return 0;
   if (f >= 255.f) return 255;
   return (uint8_t)f;
 }
-static inline int8_t as_i8(float f) {
-  if (std::isnan(f)) return 0;
+LLRS_HD int8_t as_i8(float f) {
+  if (is_nan(f)) return 0;
   if (f <= -128.f) return -128;
   if (f >= 127.f) return 127;
   return (int8_t)f;
 }
-static inline int32_t as_i32(float f) {
-  if (std::isnan(f)) return 0;
+LLRS_HD int32_t as_i32(float f) {
+  if (is_nan(f)) return 0;
   if (f <= -2147483648.f) return INT32_MIN;
   if (f >= 2147483648.f) return INT32_MAX;
   return (int32_t)f;
 }
-static inline float clampf(float v, float lo, float hi) {
-  // f32::clamp: NaN passes through (then the cast maps it to 0).
+// f32::clamp: NaN passes through.
+LLRS_HD float clampf(float v, float lo, float hi) {
   if (v < lo) v = lo;
   if (v > hi) v = hi;
   return v;
 }
 
-// quantize_block_q8_0 (src/quant.rs:650-662).
-static void block_q8_0(const float *v, std::vector<uint8_t> &out) {
+// quantize_block_q8_0 (src/quant.rs:650-662): 32 values -> 34 bytes.
+LLRS_HD void block_q8_0(const float *v, uint8_t *out) {
   float abs_max = 0.f;
   for (int i = 0; i < 32; i++) abs_max = fmaxf(abs_max, fabsf(v[i]));
   float d = abs_max / 127.0f;
   float inv = d == 0.f ? 0.f : 1.0f / d;
   put_f16(out, d);
-  for (int i = 0; i < 32; i++) out.push_back((uint8_t)as_i8(clampf(roundf(v[i] * inv), -127.f, 127.f)));
+  for (int i = 0; i < 32; i++) out[2 + i] = (uint8_t)as_i8(clampf(roundf(v[i] * inv), -127.f, 127.f));
 }
 
 // make_qx_quants_16 (src/quant.rs:726-777).
-static float make_qx_quants_16(const float *v, uint8_t *codes) {
+LLRS_HD float make_qx_quants_16(const float *v, uint8_t *codes) {
   float mx = 0.f, abs_max = 0.f;
   for (int i = 0; i < 16; i++)
     if (fabsf(v[i]) > abs_max) {
@@ -112,7 +129,7 @@ static float make_qx_quants_16(const float *v, uint8_t *codes) {
       mx = v[i];
     }
   if (abs_max < 1e-15f) {
-    memset(codes, 0, 16);
+    for (int i = 0; i < 16; i++) codes[i] = 0;
     return 0.f;
   }
   float inv_scale = -32.0f / mx;
@@ -149,8 +166,8 @@ static float make_qx_quants_16(const float *v, uint8_t *codes) {
   return scale;
 }
 
-// quantize_block_q6k (src/quant.rs:664-724).
-static void block_q6k(const float *v, std::vector<uint8_t> &out) {
+// quantize_block_q6k (src/quant.rs:664-724): 256 values -> 210 bytes.
+LLRS_HD void block_q6k(const float *v, uint8_t *out) {
   uint8_t codes[256];
   float scales[16];
   float max_scale = 0.f, max_abs_scale = 0.f;
@@ -163,7 +180,7 @@ static void block_q6k(const float *v, std::vector<uint8_t> &out) {
     }
   }
   if (max_abs_scale < 1e-15f) {
-    out.insert(out.end(), 210, 0);
+    for (int i = 0; i < 210; i++) out[i] = 0;
     return;
   }
   float inv_scale = -128.0f / max_scale;
@@ -179,25 +196,23 @@ static void block_q6k(const float *v, std::vector<uint8_t> &out) {
       codes[g * 16 + i] = (uint8_t)(level + 32);
     }
   }
-  uint8_t low[128], high[64];
   for (int half = 0; half < 2; half++) {
     int base = half * 128;
     for (int lane = 0; lane < 32; lane++) {
       uint8_t q1 = codes[base + lane], q2 = codes[base + 32 + lane], q3 = codes[base + 64 + lane],
               q4 = codes[base + 96 + lane];
-      low[half * 64 + lane] = (uint8_t)((q1 & 0x0f) | ((q3 & 0x0f) << 4));
-      low[half * 64 + 32 + lane] = (uint8_t)((q2 & 0x0f) | ((q4 & 0x0f) << 4));
-      high[half * 32 + lane] = (uint8_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+      out[half * 64 + lane] = (uint8_t)((q1 & 0x0f) | ((q3 & 0x0f) << 4));
+      out[half * 64 + 32 + lane] = (uint8_t)((q2 & 0x0f) | ((q4 & 0x0f) << 4));
+      out[128 + half * 32 + lane] =
+          (uint8_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
     }
   }
-  out.insert(out.end(), low, low + 128);
-  out.insert(out.end(), high, high + 64);
-  for (int g = 0; g < 16; g++) out.push_back((uint8_t)scale_codes[g]);
-  put_f16(out, d);
+  for (int g = 0; g < 16; g++) out[192 + g] = (uint8_t)scale_codes[g];
+  put_f16(out + 208, d);
 }
 
-// quantize_block_q5_0 (src/quant.rs:779-807).
-static void block_q5_0(const float *v, std::vector<uint8_t> &out) {
+// quantize_block_q5_0 (src/quant.rs:779-807): 32 values -> 22 bytes.
+LLRS_HD void block_q5_0(const float *v, uint8_t *out) {
   float max_value = 0.f, abs_max = 0.f;
   for (int i = 0; i < 32; i++)
     if (fabsf(v[i]) > abs_max) {
@@ -207,22 +222,20 @@ static void block_q5_0(const float *v, std::vector<uint8_t> &out) {
   float d = abs_max == 0.f ? 0.f : max_value / -16.0f;
   float inv = d == 0.f ? 0.f : 1.0f / d;
   put_f16(out, d);
-  size_t qh_pos = out.size();
-  out.insert(out.end(), 4, 0);
   uint32_t high = 0;
   for (int j = 0; j < 16; j++) {
     uint8_t q0 = as_u8(clampf(floorf(v[j] * inv + 16.5f), 0.f, 31.f));
     uint8_t q1 = as_u8(clampf(floorf(v[j + 16] * inv + 16.5f), 0.f, 31.f));
-    out.push_back((uint8_t)((q0 & 0x0f) | ((q1 & 0x0f) << 4)));
+    out[6 + j] = (uint8_t)((q0 & 0x0f) | ((q1 & 0x0f) << 4));
     high |= (((uint32_t)q0 >> 4) & 1) << j;
     high |= (((uint32_t)q1 >> 4) & 1) << (j + 16);
   }
-  for (int k = 0; k < 4; k++) out[qh_pos + k] = (uint8_t)(high >> (8 * k));
+  for (int k = 0; k < 4; k++) out[2 + k] = (uint8_t)(high >> (8 * k));
 }
 
 // make_qkx2_quants (src/quant.rs:892-967).
-static float make_qkx2_quants(const float *v, const float *w, uint8_t *codes, float *out_min,
-                              uint8_t *aux) {
+LLRS_HD float make_qkx2_quants(const float *v, const float *w, uint8_t *codes, float *out_min,
+                               uint8_t *aux) {
   float mn = v[0], mx = v[0];
   float sum_w = w[0], sum_x = w[0] * v[0];
   for (int i = 1; i < 32; i++) {
@@ -233,7 +246,7 @@ static float make_qkx2_quants(const float *v, const float *w, uint8_t *codes, fl
   }
   mn = fminf(mn, 0.f);
   if (mx == mn) {
-    memset(codes, 0, 32);
+    for (int i = 0; i < 32; i++) codes[i] = 0;
     *out_min = -mn;
     return 0.f;
   }
@@ -272,7 +285,7 @@ static float make_qkx2_quants(const float *v, const float *w, uint8_t *codes, fl
         err += w[i] * diff * diff;
       }
       if (err < best_error) {
-        memcpy(codes, aux, 32);
+        for (int i = 0; i < 32; i++) codes[i] = aux[i];
         best_error = err;
         scale = cs;
         mn = cm;
@@ -283,8 +296,8 @@ static float make_qkx2_quants(const float *v, const float *w, uint8_t *codes, fl
   return scale;
 }
 
-// quantize_block_q4k (src/quant.rs:809-890).
-static void block_q4k(const float *v, std::vector<uint8_t> &out) {
+// quantize_block_q4k (src/quant.rs:809-890): 256 values -> 144 bytes.
+LLRS_HD void block_q4k(const float *v, uint8_t *out) {
   float local_scales[8], local_mins[8], max_scale = 0.f, max_min = 0.f;
   uint8_t codes[256], aux[32];
   for (int g = 0; g < 8; g++) {
@@ -318,8 +331,8 @@ static void block_q4k(const float *v, std::vector<uint8_t> &out) {
   }
   float d = max_scale / 63.0f, dmin = max_min / 63.0f;
   put_f16(out, d);
-  put_f16(out, dmin);
-  out.insert(out.end(), scales, scales + 12);
+  put_f16(out + 2, dmin);
+  for (int i = 0; i < 12; i++) out[4 + i] = scales[i];
   d = f16_round(d);
   dmin = f16_round(dmin);
   for (int g = 0; g < 8; g++) {
@@ -331,59 +344,93 @@ static void block_q4k(const float *v, std::vector<uint8_t> &out) {
   }
   for (int pair = 0; pair < 4; pair++)
     for (int i = 0; i < 32; i++)
-      out.push_back((uint8_t)(codes[pair * 64 + i] | (codes[pair * 64 + 32 + i] << 4)));
+      out[16 + pair * 32 + i] = (uint8_t)(codes[pair * 64 + i] | (codes[pair * 64 + 32 + i] << 4));
 }
 
-uint32_t quantize_rows(uint32_t requested, const float *values, size_t rows, size_t cols,
-                       std::vector<uint8_t> &out) {
-  uint32_t ty = requested;
-  // Fallback rules of quantize_q4k / quantize_q6k / quantize_q5_0 / quantize_q8_0.
-  if (ty == LLRS_Q4_K && cols % 256) ty = LLRS_Q5_0;
-  if (ty == LLRS_Q6_K && cols % 256) ty = LLRS_Q8_0;
-  if ((ty == LLRS_Q5_0 || ty == LLRS_Q8_0) && cols % 32) ty = LLRS_F32;
-  out.clear();
-  if (ty == LLRS_F32) {
-    out.resize(rows * cols * 4);
-    memcpy(out.data(), values, rows * cols * 4);
-    return ty;
-  }
-  out.reserve(row_bytes(ty, cols) * rows);
-  for (size_t r = 0; r < rows; r++) {
-    const float *row = values + r * cols;
-    switch (ty) {
-      case LLRS_Q4_K: for (size_t c = 0; c < cols; c += 256) block_q4k(row + c, out); break;
-      case LLRS_Q6_K: for (size_t c = 0; c < cols; c += 256) block_q6k(row + c, out); break;
-      case LLRS_Q5_0: for (size_t c = 0; c < cols; c += 32) block_q5_0(row + c, out); break;
-      case LLRS_Q8_0: for (size_t c = 0; c < cols; c += 32) block_q8_0(row + c, out); break;
-      default: break;
-    }
-  }
-  return ty;
+// ------------------------------------------------------------ synthetic RNG
+
+LLRS_HD uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
 }
 
+// Natural log for x in (0, 1]: x = m * 2^e with m in [sqrt(1/2), sqrt(2)),
+// ln m = 2 atanh(s), s = (m-1)/(m+1), atanh by its odd series to s^13.
+LLRS_HD float ln_unit(float x) {
+  uint32_t b = f2u(x);
+  int e = (int)(b >> 23) - 127;
+  float m = u2f((b & 0x7fffffu) | 0x3f800000u);
+  if (m > 1.41421356f) {
+    m = m * 0.5f;
+    e += 1;
+  }
+  float s = (m - 1.0f) / (m + 1.0f), s2 = s * s;
+  float p = 1.0f / 13.0f;
+  p = p * s2 + 1.0f / 11.0f;
+  p = p * s2 + 1.0f / 9.0f;
+  p = p * s2 + 1.0f / 7.0f;
+  p = p * s2 + 1.0f / 5.0f;
+  p = p * s2 + 1.0f / 3.0f;
+  return (float)e * 0.69314718f + 2.0f * (s + s * s2 * p);
+}
+
+// sin and cos of 2*pi*t for t in [0, 1): quadrant from 4t, Taylor series on [0, pi/2).
+LLRS_HD void sincos_turn(float t, float &sn, float &cs) {
+  float q = t * 4.0f;
+  int k = (int)q;
+  if (k > 3) k = 3;
+  float a = (q - (float)k) * 1.57079633f, a2 = a * a;
+  float s = 1.0f / 1307674368000.0f;  // 1/15!
+  s = s * -a2 + 1.0f / 6227020800.0f;
+  s = s * -a2 + 1.0f / 39916800.0f;
+  s = s * -a2 + 1.0f / 362880.0f;
+  s = s * -a2 + 1.0f / 5040.0f;
+  s = s * -a2 + 1.0f / 120.0f;
+  s = s * -a2 + 1.0f / 6.0f;
+  s = a - a * a2 * s;
+  float c = 1.0f / 20922789888000.0f;  // 1/16!
+  c = c * -a2 + 1.0f / 87178291200.0f;
+  c = c * -a2 + 1.0f / 479001600.0f;
+  c = c * -a2 + 1.0f / 3628800.0f;
+  c = c * -a2 + 1.0f / 40320.0f;
+  c = c * -a2 + 1.0f / 720.0f;
+  c = c * -a2 + 1.0f / 24.0f;
+  c = c * a2 - 0.5f;
+  c = 1.0f + a2 * c;
+  switch (k) {
+    case 0: sn = s; cs = c; break;
+    case 1: sn = c; cs = -s; break;
+    case 2: sn = -s; cs = -c; break;
+    default: sn = -c; cs = s; break;
+  }
+}
+
+// Key of tensor `index` of a synthetic model with `seed`.
+LLRS_HD uint64_t tensor_key(uint64_t seed, uint64_t index) {
+  return mix64(seed + 0x9E3779B97F4A7C15ull * (index + 1));
+}
+
+// The pair of N(0,1) samples for flat elements 2p and 2p+1 of a tensor
+// (Box-Muller on two 24-bit uniforms from one 64-bit hash).
+LLRS_HD void normal_pair(uint64_t key, uint64_t p, float &z0, float &z1) {
+  uint64_t h = mix64(key ^ (p * 0xD1B54A32D192ED03ull + 1));
+  float u1 = (float)((h >> 40) + 1) * 5.9604644775390625e-8f;       // (0, 1]
+  float u2 = (float)((h >> 16) & 0xffffffu) * 5.9604644775390625e-8f;  // [0, 1)
+  float r = sqrtf(-2.0f * ln_unit(u1));
+  float sn, cs;
+  sincos_turn(u2, sn, cs);
+  z0 = r * cs;
+  z1 = r * sn;
+}
+
+// Value of flat element e of a synthetic tensor: std * z (+1 for a norm gain).
+LLRS_HD float synth_value(uint64_t key, uint64_t e, float std_dev, bool gain) {
+  float z0, z1;
+  normal_pair(key, e >> 1, z0, z1);
+  float z = (e & 1) ? z1 : z0;
+  return gain ? 1.0f + std_dev * z : std_dev * z;
+}
+
+}  // namespace enc
 }  // namespace llrs
-
-extern "C" int llrs_quantize(uint32_t ggml_type, const float *values, size_t rows, size_t cols,
-                             void *out, size_t out_capacity, size_t *out_nbytes,
-                             uint32_t *out_type) {
-  using namespace llrs;
-  clear_error();
-  if (ggml_type != LLRS_Q4_K && ggml_type != LLRS_Q5_0 && ggml_type != LLRS_Q8_0 &&
-      ggml_type != LLRS_Q6_K)
-    return set_error(LLRS_E_UNSUPPORTED, "llrs_quantize supports Q4_K, Q5_0, Q8_0 and Q6_K");
-  if (!values && rows * cols) return set_error(LLRS_E_INVALID, "values is NULL");
-  uint32_t ty = ggml_type;
-  if (ty == LLRS_Q4_K && cols % 256) ty = LLRS_Q5_0;
-  if (ty == LLRS_Q6_K && cols % 256) ty = LLRS_Q8_0;
-  if ((ty == LLRS_Q5_0 || ty == LLRS_Q8_0) && cols % 32) ty = LLRS_F32;
-  size_t need = ty == LLRS_F32 ? rows * cols * 4 : row_bytes(ty, cols) * rows;
-  if (out_nbytes) *out_nbytes = need;
-  if (out_type) *out_type = ty;
-  if (!out) return LLRS_OK;
-  if (out_capacity < need)
-    return set_error(LLRS_E_INVALID, "output capacity %zu < %zu", out_capacity, need);
-  std::vector<uint8_t> buf;
-  quantize_rows(ggml_type, values, rows, cols, buf);
-  memcpy(out, buf.data(), need);
-  return LLRS_OK;
-}

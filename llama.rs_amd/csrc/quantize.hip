@@ -1,0 +1,155 @@
+// Load-time quantization on the host (QuantTensor::quantize_*, src/quant.rs:187-259)
+// and synthetic-weight generation + quantization on the GPU.  Both use the
+// shared encoders and RNG of quant_encode.h; this file is compiled with
+// -ffp-contract=off for host and device, so both sides emit identical bytes.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+
+#include "common.h"
+#include "quant_encode.h"
+#include "quantize.h"
+
+namespace llrs {
+
+uint16_t f32_to_f16_bits(float f) { return enc::f32_to_f16(f); }
+float f16_bits_to_f32_host(uint16_t h) { return enc::f16_to_f32(h); }
+
+uint32_t final_quant_type(uint32_t requested, size_t cols) {
+  uint32_t ty = requested;
+  if (ty == LLRS_Q4_K && cols % 256) ty = LLRS_Q5_0;  // quantize_q4k -> quantize_q5_0
+  if (ty == LLRS_Q6_K && cols % 256) ty = LLRS_Q8_0;  // quantize_q6k -> quantize_q8_0
+  if ((ty == LLRS_Q5_0 || ty == LLRS_Q8_0) && cols % 32) ty = LLRS_F32;
+  return ty;
+}
+
+void encode_row(uint32_t ty, const float *v, size_t cols, uint8_t *out) {
+  switch (ty) {
+    case LLRS_Q4_K: for (size_t c = 0; c < cols; c += 256) enc::block_q4k(v + c, out + c / 256 * 144); break;
+    case LLRS_Q6_K: for (size_t c = 0; c < cols; c += 256) enc::block_q6k(v + c, out + c / 256 * 210); break;
+    case LLRS_Q5_0: for (size_t c = 0; c < cols; c += 32) enc::block_q5_0(v + c, out + c / 32 * 22); break;
+    case LLRS_Q8_0: for (size_t c = 0; c < cols; c += 32) enc::block_q8_0(v + c, out + c / 32 * 34); break;
+    default: memcpy(out, v, cols * 4); break;
+  }
+}
+
+uint32_t quantize_rows(uint32_t requested, const float *values, size_t rows, size_t cols,
+                       std::vector<uint8_t> &out) {
+  uint32_t ty = final_quant_type(requested, cols);
+  size_t rb = ty == LLRS_F32 ? cols * 4 : row_bytes(ty, cols);
+  out.assign(rb * rows, 0);
+  for (size_t r = 0; r < rows; r++) encode_row(ty, values + r * cols, cols, out.data() + r * rb);
+  return ty;
+}
+
+// One thread per GGML block: generate its values from the tensor's RNG key
+// and encode them.  ty is a quantized type (or F32 for one value per thread).
+template <uint32_t TY>
+__global__ __launch_bounds__(64) void synth_encode_kernel(uint64_t key, uint64_t rows, uint64_t cols,
+                                                          float sd, int gain, uint8_t *out,
+                                                          uint64_t rbytes) {
+  constexpr int BS = TY == LLRS_Q4_K || TY == LLRS_Q6_K ? 256 : TY == LLRS_F32 ? 1 : 32;
+  constexpr int TS = TY == LLRS_Q4_K ? 144 : TY == LLRS_Q6_K ? 210 : TY == LLRS_Q5_0 ? 22
+                     : TY == LLRS_Q8_0 ? 34 : 4;
+  uint64_t per_row = cols / BS, total = rows * per_row;
+  for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < total;
+       b += (uint64_t)gridDim.x * blockDim.x) {
+    uint64_t r = b / per_row, j = b % per_row;
+    uint64_t e0 = r * cols + j * BS;
+    uint8_t *dst = out + r * rbytes + j * TS;
+    if constexpr (TY == LLRS_F32) {
+      float v = enc::synth_value(key, e0, sd, gain != 0);
+      memcpy(dst, &v, 4);
+    } else {
+      float v[BS];
+      for (int i = 0; i < BS; i++) v[i] = enc::synth_value(key, e0 + i, sd, gain != 0);
+      if constexpr (TY == LLRS_Q4_K) enc::block_q4k(v, dst);
+      else if constexpr (TY == LLRS_Q6_K) enc::block_q6k(v, dst);
+      else if constexpr (TY == LLRS_Q5_0) enc::block_q5_0(v, dst);
+      else enc::block_q8_0(v, dst);
+    }
+  }
+}
+
+// Quantizes device f32 rows with the encoders (GPU load-time quantization).
+template <uint32_t TY>
+__global__ __launch_bounds__(64) void encode_kernel(const float *__restrict__ vals, uint64_t rows,
+                                                    uint64_t cols, uint8_t *out, uint64_t rbytes) {
+  constexpr int BS = TY == LLRS_Q4_K || TY == LLRS_Q6_K ? 256 : 32;
+  constexpr int TS = TY == LLRS_Q4_K ? 144 : TY == LLRS_Q6_K ? 210 : TY == LLRS_Q5_0 ? 22 : 34;
+  uint64_t per_row = cols / BS, total = rows * per_row;
+  for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < total;
+       b += (uint64_t)gridDim.x * blockDim.x) {
+    uint64_t r = b / per_row, j = b % per_row;
+    float v[BS];
+    for (int i = 0; i < BS; i++) v[i] = vals[r * cols + j * BS + i];
+    uint8_t *dst = out + r * rbytes + j * TS;
+    if constexpr (TY == LLRS_Q4_K) enc::block_q4k(v, dst);
+    else if constexpr (TY == LLRS_Q6_K) enc::block_q6k(v, dst);
+    else if constexpr (TY == LLRS_Q5_0) enc::block_q5_0(v, dst);
+    else enc::block_q8_0(v, dst);
+  }
+}
+
+static dim3 grid_for(uint64_t n) {
+  uint64_t g = (n + 63) / 64;
+  if (g > 65536) g = 65536;
+  if (g == 0) g = 1;
+  return dim3((unsigned)g);
+}
+
+int launch_synth_encode(uint32_t ty, uint64_t key, size_t rows, size_t cols, float sd, bool gain,
+                        uint8_t *out, size_t rbytes, hipStream_t s) {
+  uint64_t n = ty == LLRS_F32 ? rows * cols : rows * (cols / (size_t)block_size(ty));
+  dim3 g = grid_for(n), b(64);
+  int gi = gain ? 1 : 0;
+  switch (ty) {
+    case LLRS_F32: hipLaunchKernelGGL(synth_encode_kernel<LLRS_F32>, g, b, 0, s, key, rows, cols, sd, gi, out, rbytes); break;
+    case LLRS_Q4_K: hipLaunchKernelGGL(synth_encode_kernel<LLRS_Q4_K>, g, b, 0, s, key, rows, cols, sd, gi, out, rbytes); break;
+    case LLRS_Q6_K: hipLaunchKernelGGL(synth_encode_kernel<LLRS_Q6_K>, g, b, 0, s, key, rows, cols, sd, gi, out, rbytes); break;
+    case LLRS_Q5_0: hipLaunchKernelGGL(synth_encode_kernel<LLRS_Q5_0>, g, b, 0, s, key, rows, cols, sd, gi, out, rbytes); break;
+    case LLRS_Q8_0: hipLaunchKernelGGL(synth_encode_kernel<LLRS_Q8_0>, g, b, 0, s, key, rows, cols, sd, gi, out, rbytes); break;
+    default: return set_error(LLRS_E_UNSUPPORTED, "cannot synthesize %s", type_name(ty));
+  }
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+int launch_encode(uint32_t ty, const float *vals, size_t rows, size_t cols, uint8_t *out,
+                  size_t rbytes, hipStream_t s) {
+  uint64_t n = rows * (cols / (size_t)block_size(ty));
+  dim3 g = grid_for(n), b(64);
+  switch (ty) {
+    case LLRS_Q4_K: hipLaunchKernelGGL(encode_kernel<LLRS_Q4_K>, g, b, 0, s, vals, rows, cols, out, rbytes); break;
+    case LLRS_Q6_K: hipLaunchKernelGGL(encode_kernel<LLRS_Q6_K>, g, b, 0, s, vals, rows, cols, out, rbytes); break;
+    case LLRS_Q5_0: hipLaunchKernelGGL(encode_kernel<LLRS_Q5_0>, g, b, 0, s, vals, rows, cols, out, rbytes); break;
+    case LLRS_Q8_0: hipLaunchKernelGGL(encode_kernel<LLRS_Q8_0>, g, b, 0, s, vals, rows, cols, out, rbytes); break;
+    default: return set_error(LLRS_E_UNSUPPORTED, "cannot encode %s", type_name(ty));
+  }
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+}  // namespace llrs
+
+extern "C" int llrs_quantize(uint32_t ggml_type, const float *values, size_t rows, size_t cols,
+                             void *out, size_t out_capacity, size_t *out_nbytes,
+                             uint32_t *out_type) {
+  using namespace llrs;
+  clear_error();
+  if (ggml_type != LLRS_Q4_K && ggml_type != LLRS_Q5_0 && ggml_type != LLRS_Q8_0 &&
+      ggml_type != LLRS_Q6_K)
+    return set_error(LLRS_E_UNSUPPORTED, "llrs_quantize supports Q4_K, Q5_0, Q8_0 and Q6_K");
+  if (!values && rows * cols) return set_error(LLRS_E_INVALID, "values is NULL");
+  uint32_t ty = final_quant_type(ggml_type, cols);
+  size_t need = ty == LLRS_F32 ? rows * cols * 4 : row_bytes(ty, cols) * rows;
+  if (out_nbytes) *out_nbytes = need;
+  if (out_type) *out_type = ty;
+  if (!out) return LLRS_OK;
+  if (out_capacity < need)
+    return set_error(LLRS_E_INVALID, "output capacity %zu < %zu", out_capacity, need);
+  std::vector<uint8_t> buf;
+  quantize_rows(ggml_type, values, rows, cols, buf);
+  memcpy(out, buf.data(), need);
+  return LLRS_OK;
+}

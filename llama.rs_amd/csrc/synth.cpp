@@ -1,50 +1,23 @@
 // Synthetic Qwen2 models: random-init weights from a seed, quantized with the
 // reference's load-time recipes (maybe_quantize, src/loader.rs:406-447).
 //
-// Every tensor row has its own SplitMix64 stream keyed by (seed, tensor index,
-// row), so generation is deterministic for any thread count.  Normals come
-// from Box-Muller in f32 with glibc logf/sqrtf/cosf/sinf.  Matrices and
-// biases are N(0, std); RMSNorm gains are 1 + N(0, std) so the residual
-// stream keeps its scale through the layers (gains drawn around zero would
-// collapse it and make greedy ties likely).
+// Element e (row-major) of the tensor with index t is
+//   std * z(seed, t, e)        (matrices, biases)
+//   1 + std * z(seed, t, e)    (RMSNorm gains, so the residual stream keeps its
+//                               scale; gains drawn around zero would collapse it)
+// where z is a Box-Muller normal from a counter-based hash (quant_encode.h).
+// The host path here and the GPU path (launch_synth_encode) use the same
+// functions, so a GGUF written here holds exactly the bytes that
+// llrs_model_synthetic builds in HBM.
 #include "synth.h"
 
-#include <cmath>
 #include <cstring>
 #include <thread>
 
+#include "quant_encode.h"
 #include "quantize.h"
 
 namespace llrs {
-
-static inline uint64_t mix64(uint64_t z) {
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-  return z ^ (z >> 31);
-}
-
-struct SplitMix64 {
-  uint64_t s;
-  uint64_t next() {
-    s += 0x9E3779B97F4A7C15ull;
-    return mix64(s);
-  }
-};
-
-// N(0,1) samples into out[0..n) from the stream of (seed, tensor, row).
-void synth_normals(uint64_t seed, uint64_t tensor, uint64_t row, float *out, size_t n) {
-  SplitMix64 g{mix64(seed + 0x9E3779B97F4A7C15ull * (tensor + 1)) ^
-               mix64((row + 1) * 0xD1B54A32D192ED03ull)};
-  const float two_pi = 6.28318530717958647692f;
-  for (size_t i = 0; i < n; i += 2) {
-    float u1 = (float)((g.next() >> 40) + 1) * 5.9604644775390625e-8f;  // (0, 1]
-    float u2 = (float)(g.next() >> 40) * 5.9604644775390625e-8f;        // [0, 1)
-    float r = sqrtf(-2.0f * logf(u1));
-    float th = two_pi * u2;
-    out[i] = r * cosf(th);
-    if (i + 1 < n) out[i + 1] = r * sinf(th);
-  }
-}
 
 std::vector<SynthSpec> synth_specs(const llrs_synth_config &c) {
   std::vector<SynthSpec> v;
@@ -76,8 +49,6 @@ std::vector<SynthSpec> synth_specs(const llrs_synth_config &c) {
   return v;
 }
 
-// The tensor type maybe_quantize produces for `name` (src/loader.rs:406-447),
-// after the quantizers' own fallbacks (src/quant.rs:190-259).
 uint32_t recipe_type(int recipe, const std::string &name, uint64_t cols) {
   if (recipe == LLRS_QUANT_NONE) return LLRS_F32;
   uint32_t want = LLRS_Q4_K;
@@ -89,52 +60,40 @@ uint32_t recipe_type(int recipe, const std::string &name, uint64_t cols) {
       want = LLRS_Q8_0;
     else if (name.find("mlp.down_proj.weight") != std::string::npos ||
              name.find("ffn_down.weight") != std::string::npos)
+      // Down projections stay at Q6_K in the reference's recipe.
       want = LLRS_Q6_K;
   }
-  if (want == LLRS_Q4_K && cols % 256) want = LLRS_Q5_0;
-  if (want == LLRS_Q6_K && cols % 256) want = LLRS_Q8_0;
-  if ((want == LLRS_Q5_0 || want == LLRS_Q8_0) && cols % 32) want = LLRS_F32;
-  return want;
+  return final_quant_type(want, cols);
+}
+
+uint32_t synth_type(const llrs_synth_config &c, const SynthSpec &spec) {
+  return spec.kind == SynthSpec::MATRIX ? recipe_type(c.recipe, spec.name, spec.cols) : LLRS_F32;
 }
 
 int synth_tensor(const llrs_synth_config &c, size_t index, const SynthSpec &spec,
                  GgufOutTensor &out) {
   out.name = spec.name;
-  const float sd = c.weight_std;
-  if (spec.kind != SynthSpec::MATRIX) {
-    out.dims = {spec.cols};
-    out.type = LLRS_F32;
-    std::vector<float> v(spec.cols);
-    synth_normals(c.seed, index, 0, v.data(), v.size());
-    for (auto &x : v) x = spec.kind == SynthSpec::GAIN ? 1.0f + sd * x : sd * x;
-    out.bytes.resize(v.size() * 4);
-    memcpy(out.bytes.data(), v.data(), out.bytes.size());
-    return LLRS_OK;
-  }
-  uint32_t ty = recipe_type(c.recipe, spec.name, spec.cols);
-  out.dims = {spec.cols, spec.rows};
+  uint32_t ty = synth_type(c, spec);
   out.type = ty;
+  out.dims = spec.kind == SynthSpec::MATRIX ? std::vector<uint64_t>{spec.cols, spec.rows}
+                                            : std::vector<uint64_t>{spec.cols};
   size_t rb = ty == LLRS_F32 ? spec.cols * 4 : row_bytes(ty, spec.cols);
   try {
     out.bytes.assign(rb * spec.rows, 0);
   } catch (...) {
     return set_error(LLRS_E_OOM, "out of host memory for %s", spec.name.c_str());
   }
+  uint64_t key = enc::tensor_key(c.seed, index);
+  bool gain = spec.kind == SynthSpec::GAIN;
   unsigned nt = c.threads > 0 ? (unsigned)c.threads : std::thread::hardware_concurrency();
   if (nt == 0) nt = 1;
-  if (nt > spec.rows) nt = (unsigned)spec.rows ? (unsigned)spec.rows : 1;
+  if (nt > spec.rows) nt = (unsigned)spec.rows;
   auto work = [&](size_t r0, size_t r1) {
     std::vector<float> vals(spec.cols);
-    std::vector<uint8_t> q;
     for (size_t r = r0; r < r1; r++) {
-      synth_normals(c.seed, index, r, vals.data(), spec.cols);
-      for (auto &x : vals) x *= sd;
-      if (ty == LLRS_F32) {
-        memcpy(out.bytes.data() + r * rb, vals.data(), rb);
-      } else {
-        quantize_rows(ty, vals.data(), 1, spec.cols, q);  // ty is final: no further fallback
-        memcpy(out.bytes.data() + r * rb, q.data(), rb);
-      }
+      for (size_t j = 0; j < spec.cols; j++)
+        vals[j] = enc::synth_value(key, r * spec.cols + j, c.weight_std, gain);
+      encode_row(ty, vals.data(), spec.cols, out.bytes.data() + r * rb);
     }
   };
   std::vector<std::thread> th;

@@ -92,6 +92,10 @@ class HipQwen2Model:
     def backend(self) -> HipBackend:
         return self._backend
 
+    def export_gguf(self, path) -> None:
+        """Writes the device model to a GGUF v3 file (native block bytes)."""
+        _check(lib().llrs_model_export_gguf(self.handle, str(path).encode()))
+
     def weight_bytes(self) -> int:
         return int(lib().llrs_model_weight_bytes(self.handle))
 
@@ -109,6 +113,17 @@ class HipQwen2Model:
         _check(lib().llrs_decode_greedy(self.handle, kv_cache.handle, start_pos, n_steps,
                                         out.ctypes.data_as(U32P)))
         return out[:n_steps]
+
+    PROJECTIONS = ("q", "k", "v", "o", "gate", "up", "down", "lm_head")
+
+    def profile_projection(self, kv_cache: "KVCache", which: str, iters: int = 10):
+        """(mean launch time in us, bytes per launch) of one projection's decode-step
+        launch, timed with HIP events on the backend's stream."""
+        us, nb = C.c_double(), SZ()
+        _check(lib().llrs_profile_projection(self.handle, kv_cache.handle,
+                                             self.PROJECTIONS.index(which), iters, C.byref(us),
+                                             C.byref(nb)))
+        return us.value, nb.value
 
     def __del__(self):
         h = getattr(self, "handle", None)
