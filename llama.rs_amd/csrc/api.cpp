@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <cstdlib>
 #include <new>
 
 #include "common.h"
@@ -42,6 +43,28 @@ static int ensure_scratch(llrs_backend *b, size_t nx, size_t ny) {
     b->y_cap = ny;
   }
   return LLRS_OK;
+}
+
+// y = W x on the device: the tuned kernel for the types and widths it covers,
+// the generic kernel otherwise (or when LLRS_GENERIC_GEMV is set).
+static int launch_matvec(llrs_backend *b, const llrs_tensor *w, const float *x, float *y) {
+  const char *e = getenv("LLRS_GENERIC_GEMV");
+  bool generic = e && *e && *e != '0';
+  if (generic || !fast_gemv_supports(w->type, w->cols) || w->rows > (size_t)INT32_MAX)
+    return launch_gemv_generic(w, x, y, nullptr, false, b->stream);
+  FastGemvArgs a{};
+  a.seg[0].w = w->dev;
+  a.seg[0].type = w->type;
+  a.seg[0].rows = (int)w->rows;
+  a.seg[0].row_bytes = (long)w->row_bytes;
+  a.seg[0].out = y;
+  a.nseg = 1;
+  a.rows = (int)w->rows;
+  a.cols = (int)w->cols;
+  a.x = x;
+  a.epi = kEpiStore;
+  int grid = 2 * b->cu_count, quads = (a.rows + 3) / 4;
+  return launch_gemv_fast(a, quads < grid ? quads : grid, b->stream);
 }
 
 // validate_matvec (src/quant.rs:303-318).
@@ -215,7 +238,7 @@ int llrs_matvec(llrs_backend *b, const llrs_tensor *w, const float *x, size_t nx
   LLRS_HIP(hipSetDevice(b->device));
   LLRS_TRY(ensure_scratch(b, nx ? nx : 1, ny));
   if (nx) LLRS_HIP(hipMemcpyAsync(b->x_dev, x, nx * 4, hipMemcpyHostToDevice, b->stream));
-  LLRS_TRY(launch_gemv_generic(w, b->x_dev, b->y_dev, nullptr, false, b->stream));
+  LLRS_TRY(launch_matvec(b, w, b->x_dev, b->y_dev));
   LLRS_HIP(hipMemcpyAsync(y, b->y_dev, ny * 4, hipMemcpyDeviceToHost, b->stream));
   LLRS_HIP(hipStreamSynchronize(b->stream));
   return LLRS_OK;
@@ -227,7 +250,7 @@ int llrs_matvec_dev(llrs_backend *b, const llrs_tensor *w, const float *x_dev, f
   if (w->rows == 0) return LLRS_OK;
   if (!x_dev || !y_dev) return set_error(LLRS_E_INVALID, "x_dev/y_dev is NULL");
   LLRS_HIP(hipSetDevice(b->device));
-  return launch_gemv_generic(w, x_dev, y_dev, nullptr, false, b->stream);
+  return launch_matvec(b, w, x_dev, y_dev);
 }
 
 int llrs_dequant_row(llrs_backend *b, const llrs_tensor *w, size_t row, float *out, size_t n) {

@@ -7,17 +7,29 @@
 
 namespace llrs {
 
-int launch_embed(const llrs_tensor *emb, const uint32_t *tok_by_pos, const int *pos, float *out,
-                 hipStream_t s);
+// Fused RoPE + KV append + GQA attention of one layer.
+struct AttnArgs {
+  const float *q, *k, *v;  // projections of the current token (q, k before RoPE)
+  const float *rope;       // [max_seq][hd]: cos of the half, then sin of the half
+  const int *pos;
+  float *k_cache, *v_cache;  // this layer's [max_seq][kv_width]
+  float *out;                // [nh * hd]
+  float *scratch;            // attention_scratch_floats(...) floats
+  unsigned *counters;        // [nkv], zero between launches
+  int nh, nkv, hd, max_seq, max_chunks;
+  long part_stride;          // floats per (KV head, chunk) partial: G*hd + hd + 2G
+  float scale;               // 1/sqrt(hd)
+};
+
+int launch_embed(const llrs_tensor *emb, const uint32_t *tok_by_pos, const int *pos, int max_seq,
+                 float *out, hipStream_t s);
 int launch_rmsnorm(const float *in, const float *w, float *out, int n, float eps, hipStream_t s);
-int launch_rope_kv(float *q, const float *k, const float *v, const float *rope, const int *pos,
-                   float *kc, float *vc, int nh, int nkv, int hd, hipStream_t s);
-int launch_attention(const float *q, const float *kc, const float *vc, const int *pos,
-                     float *scores, float *out, int nh, int nkv, int hd, int max_seq,
-                     hipStream_t s);
+size_t attention_scratch_floats(int nh, int nkv, int hd, int max_seq);
+int attention_chunks(int max_seq);
+int launch_attention(const AttnArgs &args, hipStream_t s);
 int launch_silu_mul(const float *g, const float *u, float *out, int n, hipStream_t s);
-int launch_argmax(const float *logits, int n, int *pos, uint32_t *tok_by_pos, uint32_t *next_token,
-                  int advance, hipStream_t s);
-int launch_advance(int *pos, hipStream_t s);
+int launch_argmax(const float *logits, int n, int *pos, int max_seq, uint32_t *tok_by_pos,
+                  uint32_t *next_token, int advance, hipStream_t s);
+int launch_advance(int *pos, int max_seq, hipStream_t s);
 
 }  // namespace llrs

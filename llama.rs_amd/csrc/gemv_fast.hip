@@ -1,0 +1,692 @@
+// Tuned batch-1 dequant-GEMV for the decode step's weight types (Q4_K, Q6_K,
+// Q8_0, Q5_0) with fused prologue (RMSNorm) and epilogues (bias, residual add,
+// SiLU(gate)*up, LM-head logits + greedy argmax).
+//
+// y[r] = sum_c W[r, c] * x[c] (KernelBackend::matvec, src/backend.rs:143-162;
+// dot_row_scalar, src/quant.rs:458-648).
+//
+// Activation digits.  Each workgroup converts x (optionally x * norm_gain) to
+// int8 "digits" in LDS: per 16-element block b with scale s_b = max|x|/127,
+//     x_j ~= s_b / 16384 * X_j,   X_j = 16384 d1_j + 128 d2_j + d3_j,
+// d1 in [-127, 127], d2, d3 in [-64, 64] (|error| <= 0.5 of X, 2.4e-7 of the
+// block maximum: the precision of f32).  Weight codes stay in their native
+// GGUF blocks and are multiplied with the digits by v_dot4_i32_i8 (4 int8
+// MACs per instruction, exact int32 accumulation); per-block f16 scales and
+// x-block scales are applied in f32.  Mins/offsets use the exact integer
+// sums of X per block.  In LDS, x-block b lives at slot (b % 4) * (nb / 4) +
+// b / 4, so the lanes of a wave read consecutive 16-byte slots.
+//
+// Work split.  Workgroup w owns whole row quads [w*Q/G, (w+1)*Q/G); each wave
+// takes one quad at a time, its 64 lanes splitting the row's blocks ("units"),
+// so a lane's digits serve four rows.  The raw weight loads of the next
+// (quad, unit) step are issued before the current step is computed.
+// Q8_0/Q5_0/Q6_K blocks have even but not 4-byte-aligned offsets: their
+// fields are loaded as aligned dwords and realigned with v_alignbyte_b32.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "gemv.h"
+#include "quant_dev.h"
+
+namespace llrs {
+
+namespace {
+
+constexpr int kR = 4;  // rows per wave step
+
+struct Lds {
+  const int8_t *dig;  // [3][cols] digit planes, x-blocks permuted by slot()
+  const float *xs;    // [nb] s_b / 16384 (slot order)
+  const int *sx;      // [nb] sum of X over the block (slot order)
+  const float *xsum32;  // [cols/32] sum of reconstructed x per 32 columns
+  int cols, nb4;        // nb4 = number of x-blocks / 4
+};
+
+__device__ __forceinline__ int slot(int b, int nb4) { return (b & 3) * nb4 + (b >> 2); }
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) {
+  return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+__device__ __forceinline__ int combine(int a1, int a2, int a3) {
+  return (a1 << 14) + (a2 << 7) + a3;
+}
+__device__ __forceinline__ uint32_t pick(const uint4 &v, int e) {
+  return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+}
+
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// Nine dwords from the dword holding p (p 2-byte aligned): raw[0..8].
+__device__ __forceinline__ void load9(const uint8_t *p, uint32_t (&raw)[9], uint32_t &sh) {
+  uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t *base = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
+  sh = (uint32_t)(a & 3);  // byte shift for v_alignbyte_b32 (0 or 2)
+  u32x4a4 v0 = *reinterpret_cast<const u32x4a4 *>(base);
+  u32x4a4 v1 = *reinterpret_cast<const u32x4a4 *>(base + 4);
+  raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
+  raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
+  raw[8] = base[8];
+}
+__device__ __forceinline__ uint32_t realign(const uint32_t (&raw)[9], int k, uint32_t sh) {
+  return __builtin_amdgcn_alignbyte(raw[k + 1], raw[k], sh);
+}
+
+// Digits (3 planes) of x-block b for the lane, as 4 dwords each.
+__device__ __forceinline__ void dig_block(const Lds &L, int b, uint4 (&d)[3]) {
+  int s = slot(b, L.nb4) * 16;
+#pragma unroll
+  for (int p = 0; p < 3; p++) d[p] = *reinterpret_cast<const uint4 *>(L.dig + p * L.cols + s);
+}
+
+// ------------------------------------------------------------------ per type
+// Traits<TY>: units per row; Raw = raw loads of one row for one unit; load();
+// Dig = the lane's digits of one unit; digits(); dot() = contribution of one
+// row's unit.
+
+template <uint32_t TY> struct Traits;
+
+// Q4_K: unit u = block u/4, sub-block pair p = u%4 (groups 2p, 2p+1 = 64
+// weights, x-blocks 4u .. 4u+3).  y += d*sc_g * sum(q x) - dmin*m_g * sum(x).
+template <> struct Traits<LLRS_Q4_K> {
+  static constexpr int kColsPerUnit = 64;
+  struct Raw { uint4 hdr, q0, q1; };
+  struct Dig { uint4 g[4][3]; float xs[4]; float xsum[2]; };
+  static __device__ __forceinline__ void load(const uint8_t *row, int u, Raw &r) {
+    const uint8_t *blk = row + (size_t)(u >> 2) * 144;
+    int p = u & 3;
+    r.hdr = *reinterpret_cast<const uint4 *>(blk);
+    r.q0 = *reinterpret_cast<const uint4 *>(blk + 16 + p * 32);
+    r.q1 = *reinterpret_cast<const uint4 *>(blk + 32 + p * 32);
+  }
+  static __device__ __forceinline__ void digits(const Lds &L, int u, Dig &D) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      dig_block(L, 4 * u + j, D.g[j]);
+      D.xs[j] = L.xs[slot(4 * u + j, L.nb4)];
+    }
+    D.xsum[0] = L.xsum32[2 * u];
+    D.xsum[1] = L.xsum32[2 * u + 1];
+  }
+  static __device__ __forceinline__ float dot(const Raw &r, int u, const Dig &D) {
+    int p = u & 3;
+    float d = f16_bits_to_f32((uint16_t)(r.hdr.x & 0xffff));
+    float dmin = f16_bits_to_f32((uint16_t)(r.hdr.x >> 16));
+    // scale_min_k4 for groups 2p and 2p+1 (src/quant.rs:338-347).
+    int sc[2], mn[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      int g = 2 * p + t;
+      int hh = (g & 3) * 8;
+      int lo_sc = (r.hdr.y >> hh) & 63, lo_mn = (r.hdr.z >> hh) & 63;
+      int hi_sc = ((r.hdr.w >> hh) & 15) | (((r.hdr.y >> (hh + 6)) & 3) << 4);
+      int hi_mn = ((r.hdr.w >> (hh + 4)) & 15) | (((r.hdr.z >> (hh + 6)) & 3) << 4);
+      sc[t] = g < 4 ? lo_sc : hi_sc;
+      mn[t] = g < 4 ? lo_mn : hi_mn;
+    }
+    uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    int acc[4][3] = {};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      int lo = (int)(w[k] & 0x0f0f0f0fu), hi = (int)((w[k] >> 4) & 0x0f0f0f0fu);
+      int h = k >> 2, e = k & 3;
+#pragma unroll
+      for (int pl = 0; pl < 3; pl++) {
+        acc[h][pl] = sdot4(lo, (int)pick(D.g[h][pl], e), acc[h][pl]);          // group 2p
+        acc[2 + h][pl] = sdot4(hi, (int)pick(D.g[2 + h][pl], e), acc[2 + h][pl]);  // group 2p+1
+      }
+    }
+    float y = 0.f;
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      float s = (float)combine(acc[2 * g][0], acc[2 * g][1], acc[2 * g][2]) * D.xs[2 * g] +
+                (float)combine(acc[2 * g + 1][0], acc[2 * g + 1][1], acc[2 * g + 1][2]) * D.xs[2 * g + 1];
+      y += d * (float)sc[g] * s - dmin * (float)mn[g] * D.xsum[g];
+    }
+    return y;
+  }
+};
+
+// Q6_K: unit u = block u/4, half h = (u%4)/2, j = u%2: quarters j and j+2 of
+// that half (64 weights sharing 32 ql bytes and the half's 32 qh bytes).
+template <> struct Traits<LLRS_Q6_K> {
+  static constexpr int kColsPerUnit = 64;
+  struct Raw { uint32_t ql[9], qh[9]; uint32_t shl, shh; uint32_t sc; uint16_t d; };
+  struct Dig { uint4 g[4][3]; float xs[4]; int sx[4]; };
+  static __device__ __forceinline__ int xb(int u, int i) {  // x-block i of unit u
+    int h = (u & 3) >> 1, j = u & 1;
+    return (u >> 2) * 16 + h * 8 + j * 2 + (i >> 1) * 4 + (i & 1);
+  }
+  static __device__ __forceinline__ void load(const uint8_t *row, int u, Raw &r) {
+    const uint8_t *blk = row + (size_t)(u >> 2) * 210;
+    int h = (u & 3) >> 1, j = u & 1;
+    load9(blk + h * 64 + j * 32, r.ql, r.shl);
+    load9(blk + 128 + h * 32, r.qh, r.shh);
+    r.sc = (uint32_t)ld_u16(blk + 192 + h * 8 + 2 * j) |
+           ((uint32_t)ld_u16(blk + 192 + h * 8 + 2 * j + 4) << 16);
+    r.d = ld_u16(blk + 208);
+  }
+  static __device__ __forceinline__ void digits(const Lds &L, int u, Dig &D) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      int b = xb(u, i), s = slot(b, L.nb4);
+      dig_block(L, b, D.g[i]);
+      D.xs[i] = L.xs[s];
+      D.sx[i] = L.sx[s];
+    }
+  }
+  static __device__ __forceinline__ float dot(const Raw &r, int u, const Dig &D) {
+    int j = u & 1, sh_a = 2 * j, sh_b = 2 * j + 4;
+    float d = f16_bits_to_f32(r.d);
+    int acc[4][3] = {};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      uint32_t ql = realign(r.ql, k, r.shl), qh = realign(r.qh, k, r.shh);
+      int qa = (int)((ql & 0x0f0f0f0fu) | (((qh >> sh_a) & 0x03030303u) << 4));         // quarter j
+      int qb = (int)(((ql >> 4) & 0x0f0f0f0fu) | (((qh >> sh_b) & 0x03030303u) << 4));  // quarter j+2
+      int e = k >> 2, f = k & 3;
+#pragma unroll
+      for (int p = 0; p < 3; p++) {
+        acc[e][p] = sdot4(qa, (int)pick(D.g[e][p], f), acc[e][p]);
+        acc[2 + e][p] = sdot4(qb, (int)pick(D.g[2 + e][p], f), acc[2 + e][p]);
+      }
+    }
+    float y = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      // (q - 32) * X summed = sum q*X - 32 * sum X, exact in int32.
+      int I = combine(acc[i][0], acc[i][1], acc[i][2]) - 32 * D.sx[i];
+      int s8 = (int)(int8_t)((r.sc >> (8 * i)) & 0xff);  // i: j/0, j/1, j+2/0, j+2/1
+      y += d * (float)s8 * ((float)I * D.xs[i]);
+    }
+    return y;
+  }
+};
+
+// Q8_0: unit u = block u (32 weights, x-blocks 2u, 2u+1).
+template <> struct Traits<LLRS_Q8_0> {
+  static constexpr int kColsPerUnit = 32;
+  struct Raw { uint32_t q[9]; uint32_t sh; uint16_t d; };
+  struct Dig { uint4 g[2][3]; float xs[2]; };
+  static __device__ __forceinline__ void load(const uint8_t *row, int u, Raw &r) {
+    const uint8_t *blk = row + (size_t)u * 34;
+    load9(blk + 2, r.q, r.sh);
+    r.d = ld_u16(blk);
+  }
+  static __device__ __forceinline__ void digits(const Lds &L, int u, Dig &D) {
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      dig_block(L, 2 * u + e, D.g[e]);
+      D.xs[e] = L.xs[slot(2 * u + e, L.nb4)];
+    }
+  }
+  static __device__ __forceinline__ float dot(const Raw &r, int, const Dig &D) {
+    int acc[2][3] = {};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      int q = (int)realign(r.q, k, r.sh);
+      int e = k >> 2, f = k & 3;
+#pragma unroll
+      for (int p = 0; p < 3; p++) acc[e][p] = sdot4(q, (int)pick(D.g[e][p], f), acc[e][p]);
+    }
+    float s = (float)combine(acc[0][0], acc[0][1], acc[0][2]) * D.xs[0] +
+              (float)combine(acc[1][0], acc[1][1], acc[1][2]) * D.xs[1];
+    return f16_bits_to_f32(r.d) * s;
+  }
+};
+
+// Q5_0: unit u = block u (32 weights): d, qh (32 high bits), 16 bytes of nibbles.
+template <> struct Traits<LLRS_Q5_0> {
+  static constexpr int kColsPerUnit = 32;
+  struct Raw { uint32_t w[6]; uint32_t sh; uint16_t d; };
+  struct Dig { uint4 g[2][3]; float xs[2]; int sx[2]; };
+  static __device__ __forceinline__ void load(const uint8_t *row, int u, Raw &r) {
+    const uint8_t *blk = row + (size_t)u * 22;
+    uintptr_t a = reinterpret_cast<uintptr_t>(blk + 2);
+    const uint32_t *base = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
+    r.sh = (uint32_t)(a & 3);
+    u32x4a4 v0 = *reinterpret_cast<const u32x4a4 *>(base);
+    r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
+    r.w[4] = base[4];
+    r.w[5] = base[5];
+    r.d = ld_u16(blk);
+  }
+  static __device__ __forceinline__ void digits(const Lds &L, int u, Dig &D) {
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      int s = slot(2 * u + e, L.nb4);
+      dig_block(L, 2 * u + e, D.g[e]);
+      D.xs[e] = L.xs[s];
+      D.sx[e] = L.sx[s];
+    }
+  }
+  static __device__ __forceinline__ uint32_t spread4(uint32_t t) {  // bits 0..3 -> bit 4 of bytes
+    return ((t & 15u) * 0x00204081u & 0x01010101u) << 4;
+  }
+  static __device__ __forceinline__ float dot(const Raw &r, int, const Dig &D) {
+    uint32_t qh = __builtin_amdgcn_alignbyte(r.w[1], r.w[0], r.sh);
+    int acc[2][3] = {};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      uint32_t v = __builtin_amdgcn_alignbyte(r.w[k + 2], r.w[k + 1], r.sh);
+      int qa = (int)((v & 0x0f0f0f0fu) | spread4(qh >> (4 * k)));
+      int qb = (int)(((v >> 4) & 0x0f0f0f0fu) | spread4(qh >> (16 + 4 * k)));
+#pragma unroll
+      for (int p = 0; p < 3; p++) {
+        acc[0][p] = sdot4(qa, (int)pick(D.g[0][p], k), acc[0][p]);
+        acc[1][p] = sdot4(qb, (int)pick(D.g[1][p], k), acc[1][p]);
+      }
+    }
+    // d * (q - 16) summed against x.
+    int I0 = combine(acc[0][0], acc[0][1], acc[0][2]) - 16 * D.sx[0];
+    int I1 = combine(acc[1][0], acc[1][1], acc[1][2]) - 16 * D.sx[1];
+    return f16_bits_to_f32(r.d) * ((float)I0 * D.xs[0] + (float)I1 * D.xs[1]);
+  }
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Sum of each of four per-lane values over the wave: returns the total of
+// row ((lane >> 5) << 1 | (lane >> 4) & 1) in lanes 0, 16, 32, 48.
+__device__ __forceinline__ float wave_sum4(const float (&v)[4], int lane) {
+  bool hi = lane & 32;
+  float s0 = hi ? v[0] : v[2], s1 = hi ? v[1] : v[3];
+  float k0 = hi ? v[2] : v[0], k1 = hi ? v[3] : v[1];
+  k0 += __shfl_xor(s0, 32, 64);
+  k1 += __shfl_xor(s1, 32, 64);
+  bool hb = lane & 16;
+  float k = (hb ? k1 : k0) + __shfl_xor(hb ? k0 : k1, 16, 64);
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
+  return k;
+}
+
+// x (times the RMSNorm gain when given) as digits in LDS; returns
+// 1/sqrt(mean(x^2) + eps) with a gain, 1 without.  One pass over x.
+__device__ float digitize(const float *__restrict__ x, const float *__restrict__ gain, float eps,
+                          int cols, uint8_t *smem, float *red) {
+  const int nt = blockDim.x, tid = threadIdx.x, nb = cols >> 4, nb4 = nb >> 2;
+  int8_t *dig = reinterpret_cast<int8_t *>(smem);
+  float *xs = reinterpret_cast<float *>(smem + 3 * cols);
+  int *sx = reinterpret_cast<int *>(xs + nb);
+  float *xsum32 = reinterpret_cast<float *>(sx + nb);
+  float ss = 0.f;
+  // nb is a multiple of 4 and nt of 64, so the lanes b and b^1 of one wave
+  // always hold the two x-blocks of a 32-column group.
+  for (int b = tid; b < nb; b += nt) {
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float4 a = *reinterpret_cast<const float4 *>(x + b * 16 + q * 4);
+      v[4 * q] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w;
+    }
+    if (gain) {
+#pragma unroll
+      for (int j = 0; j < 16; j++) ss += v[j] * v[j];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        float4 g = *reinterpret_cast<const float4 *>(gain + b * 16 + q * 4);
+        v[4 * q] *= g.x; v[4 * q + 1] *= g.y; v[4 * q + 2] *= g.z; v[4 * q + 3] *= g.w;
+      }
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) m = fmaxf(m, fabsf(v[j]));
+    uint32_t p1[4] = {0, 0, 0, 0}, p2[4] = {0, 0, 0, 0}, p3[4] = {0, 0, 0, 0};
+    int sum = 0;
+    float scale = 0.f;
+    if (m > 0.f) {
+      float is = 127.0f / m;
+      scale = (m / 127.0f) * (1.0f / 16384.0f);
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        float t = v[j] * is;
+        float a1 = rintf(t);
+        float t2 = (t - a1) * 128.0f;
+        float a2 = rintf(t2);
+        float a3 = rintf((t2 - a2) * 128.0f);
+        int i1 = (int)a1, i2 = (int)a2, i3 = (int)a3;
+        sum += i1 * 16384 + i2 * 128 + i3;
+        p1[j >> 2] |= (uint32_t)(i1 & 0xff) << (8 * (j & 3));
+        p2[j >> 2] |= (uint32_t)(i2 & 0xff) << (8 * (j & 3));
+        p3[j >> 2] |= (uint32_t)(i3 & 0xff) << (8 * (j & 3));
+      }
+    }
+    int s = slot(b, nb4);
+    *reinterpret_cast<uint4 *>(dig + s * 16) = make_uint4(p1[0], p1[1], p1[2], p1[3]);
+    *reinterpret_cast<uint4 *>(dig + cols + s * 16) = make_uint4(p2[0], p2[1], p2[2], p2[3]);
+    *reinterpret_cast<uint4 *>(dig + 2 * cols + s * 16) = make_uint4(p3[0], p3[1], p3[2], p3[3]);
+    xs[s] = scale;
+    sx[s] = sum;
+    float part = scale * (float)sum;
+    float pair = __shfl_xor(part, 1, 64);
+    if ((b & 1) == 0) xsum32[b >> 1] = part + pair;
+  }
+  if (gain) {
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+  }
+  __syncthreads();
+  float inv = 1.0f;
+  if (gain) {
+    float t = 0.f;
+    for (int i = 0; i < (nt >> 6); i++) t += red[i];
+    inv = 1.0f / sqrtf(t / (float)cols + eps);
+  }
+  return inv;
+}
+
+__device__ __forceinline__ uint32_t total_order_key(float f) {
+  int32_t b = __float_as_int(f);
+  b ^= (int32_t)((uint32_t)(b >> 31) >> 1);
+  return (uint32_t)b ^ 0x80000000u;
+}
+
+// Sum of each of two per-lane values over the wave: the total of row
+// (lane >> 5) ends up in lanes 0 and 32.
+__device__ __forceinline__ float wave_sum2(float v0, float v1, int lane) {
+  bool hi = lane & 32;
+  float k = (hi ? v1 : v0) + __shfl_xor(hi ? v0 : v1, 32, 64);
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
+  return k;
+}
+
+// Rows per wave step for a type (kept small enough to double-buffer the raw
+// loads in registers); dual gate/up steps hold two rows of each matrix.
+template <uint32_t TY, bool DUAL> struct RowsPerStep { static constexpr int value = DUAL ? 2 : 4; };
+template <> struct RowsPerStep<LLRS_Q6_K, false> { static constexpr int value = 2; };
+
+// All dots of this wave's rows of one segment (and of `U` for SwiGLU),
+// streamed as (row group, unit-iteration) steps whose raw loads run one step
+// ahead of the arithmetic.  Row groups are R rows at row_lo + (first + k *
+// stride) * R.  begin() issues the first step's loads (it may run before
+// the activation digits exist); run() streams the rest; `emit(row_in_range,
+// y, y_up)` runs in one lane per row.
+template <uint32_t TY, bool DUAL>
+struct SegStream {
+  using T = Traits<TY>;
+  static constexpr int R = RowsPerStep<TY, DUAL>::value;
+  FastSeg S, U;
+  int row_lo, row_hi, first, stride, units, iters, steps, lane;
+  typename T::Raw cur[R], nxt[R], cu[DUAL ? R : 1], nu[DUAL ? R : 1];
+
+  __device__ __forceinline__ int rowof(int step, int i) const {
+    return row_lo + (first + (step / iters) * stride) * R + i;
+  }
+  __device__ __forceinline__ void load(int step, typename T::Raw (&dst)[R],
+                                       typename T::Raw (&dstu)[DUAL ? R : 1]) {
+    int u = (step % iters) * 64 + lane;
+    if (u >= units) return;
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      int r = rowof(step, i);
+      if (r >= row_hi) continue;
+      T::load(S.w + (size_t)(r - row_lo) * S.row_bytes, u, dst[i]);
+      if constexpr (DUAL) T::load(U.w + (size_t)(r - row_lo) * U.row_bytes, u, dstu[i]);
+    }
+  }
+  __device__ __forceinline__ void begin(const FastSeg &S_, const FastSeg &U_, int lo, int hi,
+                                        int first_, int stride_, int cols, int lane_) {
+    S = S_;
+    U = U_;
+    row_lo = lo;
+    row_hi = hi;
+    first = first_;
+    stride = stride_;
+    lane = lane_;
+    units = cols / T::kColsPerUnit;
+    iters = (units + 63) / 64;
+    const int ngroups = (row_hi - row_lo + R - 1) / R;
+    int nmine = first < ngroups ? (ngroups - first + stride - 1) / stride : 0;
+    steps = __builtin_amdgcn_readfirstlane(nmine) * iters;
+    if (steps > 0) load(0, cur, cu);
+  }
+  template <class Emit>
+  __device__ __forceinline__ void run(const Lds &L, Emit &&emit);
+};
+
+template <uint32_t TY, bool DUAL>
+template <class Emit>
+__device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&emit) {
+  float acc[R], acc2[R];
+#pragma unroll
+  for (int i = 0; i < R; i++) acc[i] = acc2[i] = 0.f;
+  for (int s = 0; s < steps; s++) {
+    if (s + 1 < steps) load(s + 1, nxt, nu);
+    int u = (s % iters) * 64 + lane;
+    if (u < units) {
+      typename T::Dig D;
+      T::digits(L, u, D);
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        if (rowof(s, i) < row_hi) {
+          acc[i] += T::dot(cur[i], u, D);
+          if constexpr (DUAL) acc2[i] += T::dot(cu[i], u, D);
+        }
+      }
+    }
+    if (s % iters == iters - 1) {
+      if constexpr (DUAL) {
+        // rows 0, 1 of gate and of up: gate sums land in lanes 0/16, up in 32/48.
+        float v[4] = {acc[0], acc[1], acc2[0], acc2[1]};
+        float t = wave_sum4(v, lane);
+        float up = __shfl_xor(t, 32, 64);
+        if ((lane & 47) == 0) {  // lanes 0 and 16
+          int r = rowof(s, (lane >> 4) & 1);
+          if (r < row_hi) emit(r - row_lo, t, up);
+        }
+      } else if constexpr (R == 4) {
+        float t = wave_sum4(acc, lane);
+        if ((lane & 15) == 0) {
+          int r = rowof(s, ((lane >> 5) << 1) | ((lane >> 4) & 1));
+          if (r < row_hi) emit(r - row_lo, t, 0.f);
+        }
+      } else {
+        float t = wave_sum2(acc[0], acc[1], lane);
+        if ((lane & 31) == 0) {
+          int r = rowof(s, lane >> 5);
+          if (r < row_hi) emit(r - row_lo, t, 0.f);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < R; i++) acc[i] = acc2[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      cur[i] = nxt[i];
+      if constexpr (DUAL) cu[i] = nu[i];
+    }
+  }
+}
+
+}  // namespace
+
+template <uint32_t TA, uint32_t TB, bool DUAL>
+__global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float red[16];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+  // Whole row quads per workgroup (segment row counts are multiples of 4).
+  const int quads = (a.rows + kR - 1) / kR;
+  const int wq0 = (int)((long)blockIdx.x * quads / gridDim.x);
+  const int wq1 = (int)((long)(blockIdx.x + 1) * quads / gridDim.x);
+  auto seg_range = [&](int s, int base, int &lo, int &hi) {
+    lo = max(wq0 * kR, base);
+    hi = min(min(wq1 * kR, a.rows), base + a.seg[s].rows);
+  };
+  auto shifted = [](FastSeg X, int rows) {
+    X.w += (size_t)rows * X.row_bytes;
+    return X;
+  };
+
+  // The workgroup's first segment; when it streams with type TA its first
+  // weight loads are issued now, so HBM latency overlaps the prologue.
+  int s0 = 0, base0 = 0;
+  while (s0 + 1 < a.nseg && wq0 * kR >= base0 + a.seg[s0].rows) base0 += a.seg[s0++].rows;
+  const bool s0_is_ta = DUAL || TA == TB || s0 + 1 < a.nseg;
+  SegStream<TA, DUAL> A;
+  if (s0_is_ta) {
+    int lo, hi;
+    seg_range(s0, base0, lo, hi);
+    const FastSeg Sw = shifted(a.seg[s0], lo - base0);
+    const FastSeg Uw = DUAL ? shifted(a.seg[1], lo - base0) : Sw;
+    A.begin(Sw, Uw, lo, max(lo, hi), wave, nw, a.cols, lane);
+  }
+
+  const float inv = digitize(a.x, a.norm, a.eps, a.cols, smem, red);
+  Lds L;
+  L.cols = a.cols;
+  L.nb4 = a.cols >> 6;
+  L.dig = reinterpret_cast<const int8_t *>(smem);
+  L.xs = reinterpret_cast<const float *>(smem + 3 * a.cols);
+  L.sx = reinterpret_cast<const int *>(L.xs + (a.cols >> 4));
+  L.xsum32 = reinterpret_cast<const float *>(L.sx + (a.cols >> 4));
+
+  unsigned long long best = 0;
+  // Output of row r of the rows [lo, hi) of segment S (starting at output row base).
+  auto emitter = [&](const FastSeg &S, int lo, int base) {
+    return [&, lo, base](int r, float v, float v2) {
+      int rs = lo - base + r;  // row within the segment
+      v *= inv;
+      switch (a.epi) {
+        case kEpiStore: S.out[rs] = S.bias ? v + S.bias[rs] : v; break;
+        case kEpiAdd: S.out[rs] += v; break;
+        case kEpiSwiGlu: {
+          float u = v2 * inv;
+          a.seg[2].out[rs] = (v / (1.0f + expf(-v))) * u;
+          break;
+        }
+        default: {
+          S.out[rs] = v;
+          unsigned long long key = ((unsigned long long)total_order_key(v) << 32) | (uint32_t)rs;
+          best = key > best ? key : best;
+        }
+      }
+    };
+  };
+  // Segments of type TA (all of them unless the last one has type TB); the
+  // first one's loads are already in flight.  Dual launches have one segment.
+  const int nseg_a = (DUAL || TA == TB) ? a.nseg : a.nseg - 1;
+  int base = base0;
+  for (int s = s0; s < nseg_a; s++) {
+    const FastSeg &S = a.seg[s];
+    int lo, hi;
+    seg_range(s, base, lo, hi);
+    if (lo < hi) {
+      if (!DUAL && s != s0) {
+        const FastSeg Sw = shifted(S, lo - base);
+        A.begin(Sw, Sw, lo, hi, wave, nw, a.cols, lane);
+      }
+      A.run(L, emitter(S, lo, base));
+    }
+    base += S.rows;
+  }
+  if constexpr (!DUAL && TA != TB) {
+    const int s = a.nseg - 1;
+    if (s >= s0) {
+      const FastSeg &S = a.seg[s];
+      int lo, hi;
+      seg_range(s, base, lo, hi);
+      if (lo < hi) {
+        const FastSeg Sw = shifted(S, lo - base);
+        SegStream<TB, false> B;
+        B.begin(Sw, Sw, lo, hi, wave, nw, a.cols, lane);
+        B.run(L, emitter(S, lo, base));
+      }
+    }
+  }
+  if (a.epi == kEpiLogits) {
+    // Max under total_cmp, last index on ties (src/engine.rs:233-241): keys
+    // order by (value, index), reduced per block then across blocks.
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      unsigned long long other = __shfl_xor(best, o, 64);
+      best = other > best ? other : best;
+    }
+    __shared__ unsigned long long wbest[16];
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int i = 1; i < nw; i++) best = wbest[i] > best ? wbest[i] : best;
+      atomicMax(a.amax_key, best);
+      __threadfence();
+      unsigned done = atomicAdd(a.done, 1u);
+      if (done == gridDim.x - 1) {  // last block: publish the token, advance the position
+        __threadfence();
+        unsigned long long k = atomicMax(a.amax_key, 0ull);
+        uint32_t tok = (uint32_t)(k & 0xffffffffu);
+        int p = *a.pos + 1;
+        if (p > a.max_pos) p = a.max_pos;  // never index past the context
+        *a.pos = p;
+        a.tok_by_pos[p] = tok;
+        *a.next_token = tok;
+        *a.amax_key = 0ull;  // ready for the next step
+        *a.done = 0u;
+      }
+    }
+  }
+}
+
+size_t fast_gemv_lds_bytes(int cols) {
+  return (size_t)3 * cols + (size_t)(cols >> 4) * 8 + (size_t)(cols >> 5) * 4;
+}
+
+bool fast_gemv_supports(uint32_t type, size_t cols) {
+  if (cols == 0 || cols % 64 || cols > 24576) return false;
+  switch (type) {
+    case LLRS_Q4_K: case LLRS_Q6_K: return cols % 256 == 0;
+    case LLRS_Q8_0: case LLRS_Q5_0: return true;
+    default: return false;
+  }
+}
+
+template <uint32_t TA, uint32_t TB, bool DUAL>
+static void launch_one(const FastGemvArgs &args, int grid, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((gemv_fast_kernel<TA, TB, DUAL>), dim3(grid), dim3(256), lds, s, args);
+}
+
+int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
+  size_t lds = fast_gemv_lds_bytes(args.cols);
+  uint32_t ta = args.seg[0].type, tb = args.seg[args.nseg - 1].type;
+  for (int i = 0; i + 1 < args.nseg; i++)
+    if (args.seg[i].type != ta) return set_error(LLRS_E_UNSUPPORTED, "mixed leading segment types");
+  if (args.epi == kEpiSwiGlu) {
+    if (args.nseg != 1 || args.seg[1].type != ta)
+      return set_error(LLRS_E_UNSUPPORTED, "gate and up must share a type");
+#define DUAL1(A)                                  \
+  if (ta == A) {                                  \
+    launch_one<A, A, true>(args, grid, lds, s);   \
+    LLRS_HIP(hipGetLastError());                  \
+    return LLRS_OK;                               \
+  }
+    DUAL1(LLRS_Q4_K) DUAL1(LLRS_Q5_0) DUAL1(LLRS_Q8_0) DUAL1(LLRS_Q6_K)
+#undef DUAL1
+  }
+#define PAIR(A, B)                                 \
+  if (ta == A && tb == B) {                        \
+    launch_one<A, B, false>(args, grid, lds, s);   \
+    LLRS_HIP(hipGetLastError());                   \
+    return LLRS_OK;                                \
+  }
+  PAIR(LLRS_Q4_K, LLRS_Q4_K) PAIR(LLRS_Q6_K, LLRS_Q6_K) PAIR(LLRS_Q8_0, LLRS_Q8_0)
+  PAIR(LLRS_Q5_0, LLRS_Q5_0) PAIR(LLRS_Q4_K, LLRS_Q8_0) PAIR(LLRS_Q5_0, LLRS_Q8_0)
+  PAIR(LLRS_Q4_K, LLRS_Q6_K) PAIR(LLRS_Q4_K, LLRS_Q5_0)
+#undef PAIR
+  return set_error(LLRS_E_UNSUPPORTED, "no tuned GEMV for %s + %s", type_name(ta), type_name(tb));
+}
+
+bool fast_gemv_supports_pair(uint32_t ta, uint32_t tb) {
+  auto ok = [](uint32_t a, uint32_t b) {
+    return (a == b && (a == LLRS_Q4_K || a == LLRS_Q6_K || a == LLRS_Q8_0 || a == LLRS_Q5_0)) ||
+           (a == LLRS_Q4_K && (b == LLRS_Q8_0 || b == LLRS_Q6_K || b == LLRS_Q5_0)) ||
+           (a == LLRS_Q5_0 && b == LLRS_Q8_0);
+  };
+  return ok(ta, tb);
+}
+
+}  // namespace llrs

@@ -62,9 +62,12 @@ struct llrs_kv {
   float *k_cache = nullptr, *v_cache = nullptr;  // [layer][pos][kv_width]
   float *hidden = nullptr, *residual = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
         *attn = nullptr, *gate = nullptr, *up = nullptr, *act = nullptr, *logits = nullptr,
-        *scores = nullptr, *rope = nullptr;
+        *scores = nullptr, *rope = nullptr;  // scores: attention partials scratch
+  unsigned *attn_counters = nullptr;         // [nkv] chunk completion counters
   int *pos = nullptr;
   uint32_t *tok_by_pos = nullptr, *next_token = nullptr;
+  unsigned long long *amax_key = nullptr;  // LM-head argmax accumulator (zero between steps)
+  unsigned *done = nullptr;                // LM-head block completion counter
   uint32_t *pinned = nullptr;  // host staging, max_seq_len + 2 words
   hipGraph_t graph[2] = {nullptr, nullptr};
   hipGraphExec_t exec[2] = {nullptr, nullptr};
@@ -316,21 +319,126 @@ static int synth_config_to_model(const llrs_synth_config &s, llrs_model_config &
 
 // ------------------------------------------------------------------ decode step
 
-enum Proj { P_Q = 0, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN, P_LM_HEAD };
+// Projection groups of the decode step: each is one launch on the tuned path
+// (fused RMSNorm prologue / epilogues), or the generic sequence otherwise.
+enum Proj { P_QKV = 0, P_O, P_GATE_UP, P_DOWN, P_LM_HEAD, P_COUNT };
 
-// The decode step's launch for projection `which` of layer `l`; the bench's
-// per-kernel timing calls this same function.
+static bool fast_ok(const llrs_tensor *t) {
+  return t->rows % 4 == 0 && t->rows <= INT32_MAX && fast_gemv_supports(t->type, t->cols);
+}
+
+static bool use_fast(llrs_model *m, size_t l, int which) {
+  const char *e = getenv("LLRS_GENERIC_GEMV");
+  if (e && *e && *e != '0') return false;
+  if (which == P_LM_HEAD) return fast_ok(m->lm_head);
+  const DevLayer &L = m->layers[l];
+  switch (which) {
+    case P_QKV:
+      return fast_ok(L.q) && fast_ok(L.k) && fast_ok(L.v) && L.q->type == L.k->type &&
+             fast_gemv_supports_pair(L.q->type, L.v->type);
+    case P_O: return fast_ok(L.o);
+    case P_GATE_UP: return fast_ok(L.gate) && fast_ok(L.up) && L.gate->type == L.up->type;
+    default: return fast_ok(L.down);
+  }
+}
+
+static int fast_grid(llrs_model *m, int rows) {
+  int g = 2 * m->b->cu_count;
+  int quads = (rows + 3) / 4;
+  return quads < g ? quads : g;
+}
+
+static FastSeg seg_of(const llrs_tensor *t, const float *bias, float *out) {
+  FastSeg s;
+  s.w = t->dev;
+  s.type = t->type;
+  s.rows = (int)t->rows;
+  s.row_bytes = (long)t->row_bytes;
+  s.bias = bias;
+  s.out = out;
+  return s;
+}
+
+// The decode step's launch(es) for projection group `which` of layer `l`; the
+// bench's per-kernel timing calls this same function.
 static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hipStream_t s) {
-  if (which == P_LM_HEAD) return launch_gemv_generic(m->lm_head, kv->hidden, kv->logits, nullptr, false, s);
+  const llrs_model_config &c = m->cfg;
+  const int H = (int)c.hidden_size, F = (int)c.intermediate_size;
+  const float eps = c.rms_norm_eps;
+  const bool fast = use_fast(m, l, which);
+  FastGemvArgs a{};
+  a.eps = eps;
+  a.cols = H;
+  a.x = kv->residual;
+  if (which == P_LM_HEAD) {
+    if (!fast) {
+      LLRS_TRY(launch_rmsnorm(kv->residual, m->norm, kv->hidden, H, eps, s));
+      LLRS_TRY(launch_gemv_generic(m->lm_head, kv->hidden, kv->logits, nullptr, false, s));
+      return launch_argmax(kv->logits, (int)c.vocab_size, kv->pos, (int)kv->max_seq_len,
+                           kv->tok_by_pos, kv->next_token, 1, s);
+    }
+    a.seg[0] = seg_of(m->lm_head, nullptr, kv->logits);
+    a.nseg = 1;
+    a.rows = (int)c.vocab_size;
+    a.norm = m->norm;
+    a.epi = kEpiLogits;
+    a.amax_key = kv->amax_key;
+    a.done = kv->done;
+    a.pos = kv->pos;
+    a.tok_by_pos = kv->tok_by_pos;
+    a.next_token = kv->next_token;
+    a.max_pos = (int)kv->max_seq_len;
+    return launch_gemv_fast(a, fast_grid(m, a.rows), s);
+  }
   DevLayer &L = m->layers[l];
   switch (which) {
-    case P_Q: return launch_gemv_generic(L.q, kv->hidden, kv->q, L.bq, false, s);
-    case P_K: return launch_gemv_generic(L.k, kv->hidden, kv->k, L.bk, false, s);
-    case P_V: return launch_gemv_generic(L.v, kv->hidden, kv->v, L.bv, false, s);
-    case P_O: return launch_gemv_generic(L.o, kv->attn, kv->residual, nullptr, true, s);
-    case P_GATE: return launch_gemv_generic(L.gate, kv->hidden, kv->gate, nullptr, false, s);
-    case P_UP: return launch_gemv_generic(L.up, kv->hidden, kv->up, nullptr, false, s);
-    case P_DOWN: return launch_gemv_generic(L.down, kv->act, kv->residual, nullptr, true, s);
+    case P_QKV:
+      if (!fast) {
+        LLRS_TRY(launch_rmsnorm(kv->residual, L.attn_norm, kv->hidden, H, eps, s));
+        LLRS_TRY(launch_gemv_generic(L.q, kv->hidden, kv->q, L.bq, false, s));
+        LLRS_TRY(launch_gemv_generic(L.k, kv->hidden, kv->k, L.bk, false, s));
+        return launch_gemv_generic(L.v, kv->hidden, kv->v, L.bv, false, s);
+      }
+      a.seg[0] = seg_of(L.q, L.bq, kv->q);
+      a.seg[1] = seg_of(L.k, L.bk, kv->k);
+      a.seg[2] = seg_of(L.v, L.bv, kv->v);
+      a.nseg = 3;
+      a.rows = (int)(L.q->rows + L.k->rows + L.v->rows);
+      a.norm = L.attn_norm;
+      a.epi = kEpiStore;
+      return launch_gemv_fast(a, fast_grid(m, a.rows), s);
+    case P_O:
+      if (!fast) return launch_gemv_generic(L.o, kv->attn, kv->residual, nullptr, true, s);
+      a.seg[0] = seg_of(L.o, nullptr, kv->residual);
+      a.nseg = 1;
+      a.rows = H;
+      a.x = kv->attn;
+      a.epi = kEpiAdd;
+      return launch_gemv_fast(a, fast_grid(m, a.rows), s);
+    case P_GATE_UP:
+      if (!fast) {
+        LLRS_TRY(launch_rmsnorm(kv->residual, L.ffn_norm, kv->hidden, H, eps, s));
+        LLRS_TRY(launch_gemv_generic(L.gate, kv->hidden, kv->gate, nullptr, false, s));
+        LLRS_TRY(launch_gemv_generic(L.up, kv->hidden, kv->up, nullptr, false, s));
+        return launch_silu_mul(kv->gate, kv->up, kv->act, F, s);
+      }
+      a.seg[0] = seg_of(L.gate, nullptr, kv->gate);
+      a.seg[1] = seg_of(L.up, nullptr, kv->up);
+      a.seg[2] = seg_of(L.gate, nullptr, kv->act);
+      a.nseg = 1;
+      a.rows = F;
+      a.norm = L.ffn_norm;
+      a.epi = kEpiSwiGlu;
+      return launch_gemv_fast(a, fast_grid(m, a.rows), s);
+    case P_DOWN:
+      if (!fast) return launch_gemv_generic(L.down, kv->act, kv->residual, nullptr, true, s);
+      a.seg[0] = seg_of(L.down, nullptr, kv->residual);
+      a.nseg = 1;
+      a.rows = H;
+      a.cols = F;
+      a.x = kv->act;
+      a.epi = kEpiAdd;
+      return launch_gemv_fast(a, fast_grid(m, a.rows), s);
     default: return set_error(LLRS_E_INVALID, "unknown projection %d", which);
   }
 }
@@ -338,41 +446,49 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
 static size_t projection_bytes(llrs_model *m, int which) {
   if (which == P_LM_HEAD) return m->lm_head->nbytes;
   const DevLayer &L = m->layers[0];
-  const llrs_tensor *t[] = {L.q, L.k, L.v, L.o, L.gate, L.up, L.down};
-  return t[which]->nbytes;
+  switch (which) {
+    case P_QKV: return L.q->nbytes + L.k->nbytes + L.v->nbytes;
+    case P_O: return L.o->nbytes;
+    case P_GATE_UP: return L.gate->nbytes + L.up->nbytes;
+    default: return L.down->nbytes;
+  }
 }
 
 static int enqueue_step(llrs_model *m, llrs_kv *kv, int mode) {
   const llrs_model_config &c = m->cfg;
   hipStream_t s = m->b->stream;
-  int H = (int)c.hidden_size, F = (int)c.intermediate_size;
-  int nh = (int)c.num_attention_heads, nkv = (int)c.num_key_value_heads, hd = (int)c.head_dim;
+  const int max_seq = (int)kv->max_seq_len;
   size_t layer_stride = kv->max_seq_len * c.kv_width;
-  LLRS_TRY(launch_embed(m->embed, kv->tok_by_pos, kv->pos, kv->residual, s));
+  AttnArgs at{};
+  at.q = kv->q;
+  at.k = kv->k;
+  at.v = kv->v;
+  at.rope = kv->rope;
+  at.pos = kv->pos;
+  at.out = kv->attn;
+  at.scratch = kv->scores;
+  at.counters = kv->attn_counters;
+  at.nh = (int)c.num_attention_heads;
+  at.nkv = (int)c.num_key_value_heads;
+  at.hd = (int)c.head_dim;
+  at.max_seq = max_seq;
+  at.max_chunks = attention_chunks(max_seq);
+  at.part_stride = (long)(at.nh / at.nkv) * at.hd + at.hd + 2 * (at.nh / at.nkv);
+  at.scale = 1.0f / sqrtf((float)c.head_dim);
+  LLRS_TRY(launch_embed(m->embed, kv->tok_by_pos, kv->pos, max_seq, kv->residual, s));
   for (size_t l = 0; l < c.num_hidden_layers; l++) {
-    DevLayer &L = m->layers[l];
-    float *kc = kv->k_cache + l * layer_stride, *vc = kv->v_cache + l * layer_stride;
-    LLRS_TRY(launch_rmsnorm(kv->residual, L.attn_norm, kv->hidden, H, c.rms_norm_eps, s));
-    LLRS_TRY(launch_projection(m, kv, l, P_Q, s));
-    LLRS_TRY(launch_projection(m, kv, l, P_K, s));
-    LLRS_TRY(launch_projection(m, kv, l, P_V, s));
-    LLRS_TRY(launch_rope_kv(kv->q, kv->k, kv->v, kv->rope, kv->pos, kc, vc, nh, nkv, hd, s));
-    LLRS_TRY(launch_attention(kv->q, kc, vc, kv->pos, kv->scores, kv->attn, nh, nkv, hd,
-                              (int)kv->max_seq_len, s));
+    at.k_cache = kv->k_cache + l * layer_stride;
+    at.v_cache = kv->v_cache + l * layer_stride;
+    LLRS_TRY(launch_projection(m, kv, l, P_QKV, s));
+    LLRS_TRY(launch_attention(at, s));
     LLRS_TRY(launch_projection(m, kv, l, P_O, s));
-    LLRS_TRY(launch_rmsnorm(kv->residual, L.ffn_norm, kv->hidden, H, c.rms_norm_eps, s));
-    LLRS_TRY(launch_projection(m, kv, l, P_GATE, s));
-    LLRS_TRY(launch_projection(m, kv, l, P_UP, s));
-    LLRS_TRY(launch_silu_mul(kv->gate, kv->up, kv->act, F, s));
+    LLRS_TRY(launch_projection(m, kv, l, P_GATE_UP, s));
     LLRS_TRY(launch_projection(m, kv, l, P_DOWN, s));
   }
   if (mode == LLRS_LOGITS_COMPUTE) {
-    LLRS_TRY(launch_rmsnorm(kv->residual, m->norm, kv->hidden, H, c.rms_norm_eps, s));
     LLRS_TRY(launch_projection(m, kv, 0, P_LM_HEAD, s));
-    LLRS_TRY(launch_argmax(kv->logits, (int)c.vocab_size, kv->pos, kv->tok_by_pos, kv->next_token,
-                           1, s));
   } else {
-    LLRS_TRY(launch_advance(kv->pos, s));
+    LLRS_TRY(launch_advance(kv->pos, max_seq, s));
   }
   return LLRS_OK;
 }
@@ -451,9 +567,13 @@ static int kv_create_impl(llrs_model *m, size_t max_seq, llrs_kv **out) {
       (rc = A((void **)&kv->v, KV * 4)) || (rc = A((void **)&kv->attn, H * 4)) ||
       (rc = A((void **)&kv->gate, F * 4)) || (rc = A((void **)&kv->up, F * 4)) ||
       (rc = A((void **)&kv->act, F * 4)) || (rc = A((void **)&kv->logits, c.vocab_size * 4)) ||
-      (rc = A((void **)&kv->scores, c.num_attention_heads * max_seq * 4)) ||
+      (rc = A((void **)&kv->scores, attention_scratch_floats((int)c.num_attention_heads,
+                                                             (int)c.num_key_value_heads,
+                                                             (int)c.head_dim, (int)max_seq) * 4)) ||
+      (rc = A((void **)&kv->attn_counters, 4 * c.num_key_value_heads + 64)) ||
       (rc = A((void **)&kv->rope, max_seq * c.head_dim * 4)) || (rc = A((void **)&kv->pos, 64)) ||
-      (rc = A((void **)&kv->tok_by_pos, (max_seq + 1) * 4)) || (rc = A((void **)&kv->next_token, 64))) {
+      (rc = A((void **)&kv->tok_by_pos, (max_seq + 1) * 4)) || (rc = A((void **)&kv->next_token, 64)) ||
+      (rc = A((void **)&kv->amax_key, 64)) || (rc = A((void **)&kv->done, 64))) {
     free_kv(kv);
     return rc;
   }
@@ -474,6 +594,9 @@ static int kv_create_impl(llrs_model *m, size_t max_seq, llrs_kv **out) {
   if (e == hipSuccess) e = hipMemsetAsync(kv->logits, 0, c.vocab_size * 4, s);
   if (e == hipSuccess) e = hipMemsetAsync(kv->tok_by_pos, 0, (max_seq + 1) * 4, s);
   if (e == hipSuccess) e = hipMemsetAsync(kv->pos, 0, 64, s);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->amax_key, 0, 64, s);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->done, 0, 64, s);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->attn_counters, 0, 4 * c.num_key_value_heads + 64, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) {
     free_kv(kv);
@@ -701,8 +824,8 @@ int llrs_decode_greedy(llrs_model *m, llrs_kv *kv, size_t start_pos, size_t n_st
   hipStream_t s = m->b->stream;
   LLRS_TRY(stage_tokens(kv, nullptr, 0, start_pos));
   // token = argmax(current logits) for position start_pos; nothing advances.
-  LLRS_TRY(launch_argmax(kv->logits, (int)m->cfg.vocab_size, kv->pos, kv->tok_by_pos,
-                         kv->next_token, 0, s));
+  LLRS_TRY(launch_argmax(kv->logits, (int)m->cfg.vocab_size, kv->pos, (int)kv->max_seq_len,
+                         kv->tok_by_pos, kv->next_token, 0, s));
   for (size_t i = 0; i < n_steps; i++) LLRS_TRY(run_step(m, kv, LLRS_LOGITS_COMPUTE));
   LLRS_HIP(hipMemcpyAsync(kv->pinned, kv->tok_by_pos + start_pos, n_steps * 4,
                           hipMemcpyDeviceToHost, s));
@@ -722,8 +845,8 @@ int llrs_argmax(llrs_kv *kv, uint32_t *out_token) {
   uint32_t saved = 0;
   LLRS_HIP(hipMemcpy(&saved, kv->pos, 4, hipMemcpyDeviceToHost));
   LLRS_TRY(stage_tokens(kv, nullptr, 0, kv->max_seq_len));
-  LLRS_TRY(launch_argmax(kv->logits, (int)m->cfg.vocab_size, kv->pos, kv->tok_by_pos,
-                         kv->next_token, 0, s));
+  LLRS_TRY(launch_argmax(kv->logits, (int)m->cfg.vocab_size, kv->pos, (int)kv->max_seq_len,
+                         kv->tok_by_pos, kv->next_token, 0, s));
   LLRS_HIP(hipMemcpyAsync(kv->pinned, kv->next_token, 4, hipMemcpyDeviceToHost, s));
   LLRS_HIP(hipStreamSynchronize(s));
   *out_token = kv->pinned[0];
@@ -761,10 +884,22 @@ int llrs_profile_projection(llrs_model *m, llrs_kv *kv, int which, int iters, do
                             size_t *bytes_per_launch) {
   clear_error();
   if (!m || !kv || kv->m != m || !avg_us) return set_error(LLRS_E_INVALID, "bad arguments");
-  if (which < P_Q || which > P_LM_HEAD) return set_error(LLRS_E_INVALID, "unknown projection %d", which);
+  if (which < 0 || which >= P_COUNT) return set_error(LLRS_E_INVALID, "unknown projection %d", which);
   if (iters < 1) return set_error(LLRS_E_INVALID, "iters must be positive");
   LLRS_HIP(hipSetDevice(m->b->device));
   hipStream_t s = m->b->stream;
+  // The LM-head launch advances the device position; keep the caller's.
+  int saved_pos = 0;
+  LLRS_HIP(hipStreamSynchronize(s));
+  LLRS_HIP(hipMemcpy(&saved_pos, kv->pos, 4, hipMemcpyDeviceToHost));
+  struct Restore {
+    llrs_kv *kv;
+    int pos;
+    ~Restore() {
+      (void)hipStreamSynchronize(kv->m->b->stream);
+      (void)hipMemcpy(kv->pos, &pos, 4, hipMemcpyHostToDevice);
+    }
+  } restore{kv, saved_pos};
   size_t layers = which == P_LM_HEAD ? 1 : m->cfg.num_hidden_layers;
   hipEvent_t e0, e1;
   LLRS_HIP(hipEventCreate(&e0));

@@ -114,7 +114,9 @@ class HipQwen2Model:
                                         out.ctypes.data_as(U32P)))
         return out[:n_steps]
 
-    PROJECTIONS = ("q", "k", "v", "o", "gate", "up", "down", "lm_head")
+    # Launch groups of the decode step: fused Q/K/V (+RMSNorm), O (+residual),
+    # gate/up (+RMSNorm, SiLU*up), down (+residual), LM head (+RMSNorm, argmax).
+    PROJECTIONS = ("qkv", "o", "gate_up", "down", "lm_head")
 
     def profile_projection(self, kv_cache: "KVCache", which: str, iters: int = 10):
         """(mean launch time in us, bytes per launch) of one projection's decode-step
