@@ -53,7 +53,8 @@ bool fast_gemv_supports(uint32_t type, size_t cols);
 // Whether a launch whose leading segments have type ta and last segment tb
 // has a tuned instantiation.
 bool fast_gemv_supports_pair(uint32_t ta, uint32_t tb);
-size_t fast_gemv_lds_bytes(int cols);
+// Dynamic LDS of one workgroup: the digitised activation and its rows' results.
+size_t fast_gemv_lds_bytes(int cols, int rows, int grid);
 int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s);
 
 }  // namespace llrs

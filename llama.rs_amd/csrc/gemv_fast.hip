@@ -42,6 +42,13 @@ struct Lds {
   int cols, nb4;        // nb4 = number of x-blocks / 4
 };
 
+// LDS bytes of the digitised activation: 3 digit planes, per-block scales and
+// sums, per-32 sums.
+__host__ __device__ constexpr size_t fast_gemv_digit_bytes(int cols) {
+  return (size_t)3 * cols + (size_t)(cols >> 4) * 8 + (size_t)(cols >> 5) * 4;
+}
+constexpr size_t kMaxLds = 160 * 1024;
+
 __device__ __forceinline__ int slot(int b, int nb4) { return (b & 3) * nb4 + (b >> 2); }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
@@ -58,9 +65,10 @@ typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 // Nine dwords from the dword holding p (p 2-byte aligned): raw[0..8].
 __device__ __forceinline__ void load9(const uint8_t *p, uint32_t (&raw)[9], uint32_t &sh) {
-  uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint32_t *base = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
-  sh = (uint32_t)(a & 3);  // byte shift for v_alignbyte_b32 (0 or 2)
+  // The aligned pointer is derived from p itself (not from an integer) so the
+  // compiler keeps it in the global address space: global_load, not flat_load.
+  sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3);  // byte shift for v_alignbyte_b32 (0 or 2)
+  const uint32_t *base = reinterpret_cast<const uint32_t *>(p - sh);
   u32x4a4 v0 = *reinterpret_cast<const u32x4a4 *>(base);
   u32x4a4 v1 = *reinterpret_cast<const u32x4a4 *>(base + 4);
   raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
@@ -241,9 +249,8 @@ template <> struct Traits<LLRS_Q5_0> {
   struct Dig { uint4 g[2][3]; float xs[2]; int sx[2]; };
   static __device__ __forceinline__ void load(const uint8_t *row, int u, Raw &r) {
     const uint8_t *blk = row + (size_t)u * 22;
-    uintptr_t a = reinterpret_cast<uintptr_t>(blk + 2);
-    const uint32_t *base = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
-    r.sh = (uint32_t)(a & 3);
+    r.sh = (uint32_t)(reinterpret_cast<uintptr_t>(blk + 2) & 3);
+    const uint32_t *base = reinterpret_cast<const uint32_t *>(blk + 2 - r.sh);
     u32x4a4 v0 = *reinterpret_cast<const u32x4a4 *>(base);
     r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
     r.w[4] = base[4];
@@ -417,16 +424,17 @@ struct SegStream {
   __device__ __forceinline__ int rowof(int step, int i) const {
     return row_lo + (first + (step / iters) * stride) * R + i;
   }
+  // Loads are branch-free (indices past the segment are clamped onto its last
+  // row and unit and their products discarded), so the compiler can count the
+  // outstanding loads statically and wait only for the current step's.
   __device__ __forceinline__ void load(int step, typename T::Raw (&dst)[R],
                                        typename T::Raw (&dstu)[DUAL ? R : 1]) {
-    int u = (step % iters) * 64 + lane;
-    if (u >= units) return;
+    const int u = min((step % iters) * 64 + lane, units - 1);
 #pragma unroll
     for (int i = 0; i < R; i++) {
-      int r = rowof(step, i);
-      if (r >= row_hi) continue;
-      T::load(S.w + (size_t)(r - row_lo) * S.row_bytes, u, dst[i]);
-      if constexpr (DUAL) T::load(U.w + (size_t)(r - row_lo) * U.row_bytes, u, dstu[i]);
+      const int r = min(rowof(step, i), row_hi - 1) - row_lo;
+      T::load(S.w + (size_t)r * S.row_bytes, u, dst[i]);
+      if constexpr (DUAL) T::load(U.w + (size_t)r * U.row_bytes, u, dstu[i]);
     }
   }
   __device__ __forceinline__ void begin(const FastSeg &S_, const FastSeg &U_, int lo, int hi,
@@ -452,21 +460,26 @@ struct SegStream {
 template <uint32_t TY, bool DUAL>
 template <class Emit>
 __device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&emit) {
+  using Raw = typename T::Raw;
+  constexpr int RU = DUAL ? R : 1;
   float acc[R], acc2[R];
 #pragma unroll
   for (int i = 0; i < R; i++) acc[i] = acc2[i] = 0.f;
-  for (int s = 0; s < steps; s++) {
-    if (s + 1 < steps) load(s + 1, nxt, nu);
-    int u = (s % iters) * 64 + lane;
-    if (u < units) {
-      typename T::Dig D;
-      T::digits(L, u, D);
+  // One step on buffers (c, cu_) while the next step's loads go to (n, nu_).
+  auto step = [&](int s, Raw (&c)[R], Raw (&cu_)[RU], Raw (&n)[R], Raw (&nu_)[RU]) {
+    load(s + 1, n, nu_);  // past the last step: a clamped, unused reload
+    const int u0 = (s % iters) * 64 + lane;
+    const int u = min(u0, units - 1);
+    typename T::Dig D;
+    T::digits(L, u, D);
 #pragma unroll
-      for (int i = 0; i < R; i++) {
-        if (rowof(s, i) < row_hi) {
-          acc[i] += T::dot(cur[i], u, D);
-          if constexpr (DUAL) acc2[i] += T::dot(cu[i], u, D);
-        }
+    for (int i = 0; i < R; i++) {
+      const bool live = u0 < units && rowof(s, i) < row_hi;
+      float d = T::dot(c[i], u, D);
+      acc[i] += live ? d : 0.f;
+      if constexpr (DUAL) {
+        float d2 = T::dot(cu_[i], u, D);
+        acc2[i] += live ? d2 : 0.f;
       }
     }
     if (s % iters == iters - 1) {
@@ -495,11 +508,12 @@ __device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&em
 #pragma unroll
       for (int i = 0; i < R; i++) acc[i] = acc2[i] = 0.f;
     }
-#pragma unroll
-    for (int i = 0; i < R; i++) {
-      cur[i] = nxt[i];
-      if constexpr (DUAL) cu[i] = nu[i];
-    }
+  };
+  // Unrolled by two with the buffers swapping roles: no register copies, so
+  // the in-flight loads never have to be waited for early.
+  for (int s = 0; s < steps; s += 2) {
+    step(s, cur, cu, nxt, nu);
+    if (s + 1 < steps) step(s + 1, nxt, nu, cur, cu);
   }
 }
 
@@ -547,26 +561,15 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
   L.sx = reinterpret_cast<const int *>(L.xs + (a.cols >> 4));
   L.xsum32 = reinterpret_cast<const float *>(L.sx + (a.cols >> 4));
 
-  unsigned long long best = 0;
-  // Output of row r of the rows [lo, hi) of segment S (starting at output row base).
-  auto emitter = [&](const FastSeg &S, int lo, int base) {
-    return [&, lo, base](int r, float v, float v2) {
-      int rs = lo - base + r;  // row within the segment
+  // Row results wait in LDS (x inv_rms, SiLU(gate)*up applied) until the
+  // streaming is over, so no epilogue memory access stalls the weight loads.
+  float *ybuf = reinterpret_cast<float *>(smem + fast_gemv_digit_bytes(a.cols));
+  const int wrow0 = wq0 * kR;
+  auto emitter = [&](int lo) {
+    return [&, lo](int r, float v, float v2) {
       v *= inv;
-      switch (a.epi) {
-        case kEpiStore: S.out[rs] = S.bias ? v + S.bias[rs] : v; break;
-        case kEpiAdd: S.out[rs] += v; break;
-        case kEpiSwiGlu: {
-          float u = v2 * inv;
-          a.seg[2].out[rs] = (v / (1.0f + expf(-v))) * u;
-          break;
-        }
-        default: {
-          S.out[rs] = v;
-          unsigned long long key = ((unsigned long long)total_order_key(v) << 32) | (uint32_t)rs;
-          best = key > best ? key : best;
-        }
-      }
+      if constexpr (DUAL) v = (v / (1.0f + expf(-v))) * (v2 * inv);
+      ybuf[lo - wrow0 + r] = v;
     };
   };
   // Segments of type TA (all of them unless the last one has type TB); the
@@ -582,7 +585,7 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
         const FastSeg Sw = shifted(S, lo - base);
         A.begin(Sw, Sw, lo, hi, wave, nw, a.cols, lane);
       }
-      A.run(L, emitter(S, lo, base));
+      A.run(L, emitter(lo));
     }
     base += S.rows;
   }
@@ -596,7 +599,28 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
         const FastSeg Sw = shifted(S, lo - base);
         SegStream<TB, false> B;
         B.begin(Sw, Sw, lo, hi, wave, nw, a.cols, lane);
-        B.run(L, emitter(S, lo, base));
+        B.run(L, emitter(lo));
+      }
+    }
+  }
+  __syncthreads();
+
+  // Epilogue over the workgroup's rows, coalesced.
+  unsigned long long best = 0;
+  const int wrow1 = min(wq1 * kR, a.rows);
+  for (int g = wrow0 + (int)threadIdx.x; g < wrow1; g += blockDim.x) {
+    int s = 0, rs = g;
+    while (s + 1 < a.nseg && rs >= a.seg[s].rows) rs -= a.seg[s++].rows;
+    const FastSeg &S = a.seg[s];
+    const float v = ybuf[g - wrow0];
+    switch (a.epi) {
+      case kEpiStore: S.out[rs] = S.bias ? v + S.bias[rs] : v; break;
+      case kEpiAdd: S.out[rs] += v; break;
+      case kEpiSwiGlu: a.seg[2].out[rs] = v; break;
+      default: {
+        S.out[rs] = v;
+        unsigned long long key = ((unsigned long long)total_order_key(v) << 32) | (uint32_t)rs;
+        best = key > best ? key : best;
       }
     }
   }
@@ -632,8 +656,10 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
   }
 }
 
-size_t fast_gemv_lds_bytes(int cols) {
-  return (size_t)3 * cols + (size_t)(cols >> 4) * 8 + (size_t)(cols >> 5) * 4;
+size_t fast_gemv_lds_bytes(int cols, int rows, int grid) {
+  const size_t quads = ((size_t)rows + kR - 1) / kR;
+  const size_t rows_per_wg = (quads + grid - 1) / grid * kR;
+  return fast_gemv_digit_bytes(cols) + rows_per_wg * sizeof(float);
 }
 
 bool fast_gemv_supports(uint32_t type, size_t cols) {
@@ -651,7 +677,9 @@ static void launch_one(const FastGemvArgs &args, int grid, size_t lds, hipStream
 }
 
 int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
-  size_t lds = fast_gemv_lds_bytes(args.cols);
+  if (grid <= 0) return set_error(LLRS_E_INVALID, "GEMV grid must be positive");
+  size_t lds = fast_gemv_lds_bytes(args.cols, args.rows, grid);
+  if (lds > kMaxLds) return set_error(LLRS_E_UNSUPPORTED, "GEMV needs %zu bytes of LDS (cols %d, rows %d, grid %d)", lds, args.cols, args.rows, grid);
   uint32_t ta = args.seg[0].type, tb = args.seg[args.nseg - 1].type;
   for (int i = 0; i + 1 < args.nseg; i++)
     if (args.seg[i].type != ta) return set_error(LLRS_E_UNSUPPORTED, "mixed leading segment types");
