@@ -63,8 +63,7 @@ static int launch_matvec(llrs_backend *b, const llrs_tensor *w, const float *x, 
   a.cols = (int)w->cols;
   a.x = x;
   a.epi = kEpiStore;
-  int grid = 2 * b->cu_count, quads = (a.rows + 3) / 4;
-  return launch_gemv_fast(a, quads < grid ? quads : grid, b->stream);
+  return launch_gemv_fast(a, fast_gemv_grid(b->cu_count, a.rows, false), b->stream);
 }
 
 // validate_matvec (src/quant.rs:303-318).

@@ -14,17 +14,19 @@ struct AttnArgs {
   const int *pos;
   float *k_cache, *v_cache;  // this layer's [max_seq][kv_width]
   float *out;                // [nh * hd]
-  float *scratch;            // attention_scratch_floats(...) floats
-  unsigned *counters;        // [nkv], zero between launches
-  int nh, nkv, hd, max_seq, max_chunks;
-  long part_stride;          // floats per (KV head, chunk) partial: G*hd + hd + 2G
+  float *scratch;            // attention_scratch_floats(nh, hd, max_seq) floats
+  unsigned *counters;        // [nh], zero between launches
+  int nh, nkv, hd, max_seq;
+  int max_chunks;            // attention_chunks(max_seq)
+  long part_stride;          // attention_part_stride(hd): floats per (head, chunk) partial
   float scale;               // 1/sqrt(hd)
 };
 
 int launch_embed(const llrs_tensor *emb, const uint32_t *tok_by_pos, const int *pos, int max_seq,
                  float *out, hipStream_t s);
 int launch_rmsnorm(const float *in, const float *w, float *out, int n, float eps, hipStream_t s);
-size_t attention_scratch_floats(int nh, int nkv, int hd, int max_seq);
+long attention_part_stride(int hd);
+size_t attention_scratch_floats(int nh, int hd, int max_seq);
 int attention_chunks(int max_seq);
 int launch_attention(const AttnArgs &args, hipStream_t s);
 int launch_silu_mul(const float *g, const float *u, float *out, int n, hipStream_t s);

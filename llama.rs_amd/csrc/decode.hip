@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "decode.h"
@@ -71,197 +72,231 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *__restrict__
 
 // ------------------------------------------------------------------ attention
 //
-// One workgroup per (KV head, chunk of kChunk positions); the chunks past the
+// One wave per (query head, chunk of kChunk positions); chunks past the
 // current position exit at once, so one grid (sized for the whole context)
 // serves every position of a captured graph.  Per chunk: split-half RoPE
-// (src/model.rs:87-95) on the group's query heads, scores q.k * 1/sqrt(hd),
-// softmax partials (max, sum of exp) and exp-weighted V sums
-// (src/model.rs:206-231, softmax_inplace 298-313).  The chunk holding the
-// current position also rotates the new key and appends key and value to
-// the cache (KVCache::update, src/cache.rs:38-53).  The last chunk of a KV
-// head to finish (atomic counter) merges the partials; if the total is not
-// finite and positive the weights fall back to uniform, as softmax_inplace does.
+// (src/model.rs:87-95) on the head's query, scores q.k * 1/sqrt(hd), softmax
+// partials (max, sum of exp) and exp-weighted V sums (src/model.rs:206-231,
+// softmax_inplace 298-313).  The chunk holding the current position also
+// rotates the new key, and the group's first head appends key and value to
+// the cache (KVCache::update, src/cache.rs:38-53).
+//
+// Decode attention moves a few MB per layer, so latency bounds it: each wave
+// issues all its K and V loads first, works without workgroup barriers, and
+// the chunks of a head meet through device-scope atomics only.  Partials are
+// stored write-through (device-scope relaxed atomic stores), the wave waits
+// for them to complete, then bumps the head's counter; the last chunk reads
+// them back with device-scope loads and folds them with the running-max
+// rescaling of flash decoding.  No cache write-back fence is needed.  A chunk
+// whose scores are all -inf contributes exp(-inf) = 0; without a finite
+// positive total the weights fall back to uniform, as softmax_inplace does.
 
-constexpr int kChunk = 64;  // positions per workgroup (one per lane of a wave)
+constexpr int kChunk = 32;  // positions per wave: lane = (half of the head, position)
 
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
-  extern __shared__ __align__(16) float sm[];
-  const int G = a.nh / a.nkv, hd = a.hd, half = hd / 2, kvw = a.nkv * hd;
-  const int kvh = blockIdx.y, chunk = blockIdx.x;
+__device__ __forceinline__ void store_dev(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int HD>
+__global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
+  constexpr int KH = HD / 2;              // dimensions per score lane
+  constexpr int NK4 = KH / 4;             // their float4s
+  constexpr int VW = HD >= 64 ? HD / 64 : 1;  // V floats per lane
+  constexpr int VL = HD / VW;             // lanes covering one V row
+  constexpr int RV = 64 / VL;             // V rows per load instruction
+  constexpr int NVI = kChunk / RV;        // V load instructions
+  static_assert(NK4 >= 1 && VW <= 2 && RV * VL == 64, "head_dim must be 16..128");
+  using VT = typename std::conditional<VW == 2, float2, float>::type;
+  __shared__ __align__(16) float qs[HD], kn[HD];
+
+  const int G = a.nh / a.nkv, kvw = a.nkv * HD;
+  const int h = blockIdx.y, kvh = h / G, chunk = blockIdx.x;
   const int pos = bounded_pos(a.pos, a.max_seq);
   const int c0 = chunk * kChunk;
   if (c0 > pos) return;
   const int n_active = pos / kChunk + 1;
   const int c1 = min(c0 + kChunk, pos + 1);  // exclusive
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float *qs = sm;                     // [G][hd] rotated queries
-  float *e = qs + G * hd;             // [G][kChunk] scores, then exp weights
-  __shared__ float mh[16], lh[16];    // per-head chunk max and sum of exp
-  const float *cs = a.rope + (size_t)pos * hd, *sn = cs + half;
+  const bool owns_new = pos < c1;
+  const int lane = threadIdx.x, half = lane >> 5, pl = lane & 31;
+  const float *kc = a.k_cache + (size_t)kvh * HD, *vc = a.v_cache + (size_t)kvh * HD;
 
-  for (int t = tid; t < G * half; t += blockDim.x) {
-    int h = t / half, i = t % half;
-    const float *x = a.q + (size_t)(kvh * G + h) * hd;
-    float re = x[i], im = x[i + half];
-    qs[h * hd + i] = re * cs[i] - im * sn[i];
-    qs[h * hd + i + half] = re * sn[i] + im * cs[i];
-  }
-  float *kc = a.k_cache, *vc = a.v_cache;
-  if (pos >= c0 && pos < c1) {  // this chunk appends the new key (rotated) and value
-    float *krow = kc + (size_t)pos * kvw + kvh * hd, *vrow = vc + (size_t)pos * kvw + kvh * hd;
-    const float *kx = a.k + kvh * hd, *vx = a.v + kvh * hd;
-    for (int i = tid; i < half; i += blockDim.x) {
-      float re = kx[i], im = kx[i + half];
-      krow[i] = re * cs[i] - im * sn[i];
-      krow[i + half] = re * sn[i] + im * cs[i];
-    }
-    for (int i = tid; i < hd; i += blockDim.x) vrow[i] = vx[i];
-  }
-  __syncthreads();
-
-  // Scores: 4 lanes per position, each a quarter of the head dimension.
-  const float scale = a.scale;
-  for (int base = 0; base < kChunk; base += blockDim.x / 4) {
-    int pl = base + tid / 4, qd = tid & 3;
-    int p = c0 + pl;
-    const int dq = hd / 4;
-    float part[16];
-#pragma unroll
-    for (int h = 0; h < 16; h++) part[h] = 0.f;
-    if (pl < kChunk && p < c1) {
-      const float *kr = kc + (size_t)p * kvw + kvh * hd + qd * dq;
-      for (int d = 0; d < dq; d += 4) {
-        float4 kv4 = *reinterpret_cast<const float4 *>(kr + d);
-#pragma unroll
-        for (int h = 0; h < 16; h++) {
-          if (h < G) {
-            const float *qq = qs + h * hd + qd * dq + d;
-            part[h] += qq[0] * kv4.x + qq[1] * kv4.y + qq[2] * kv4.z + qq[3] * kv4.w;
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < 16; h++) {
-      part[h] += __shfl_xor(part[h], 1, 64);
-      part[h] += __shfl_xor(part[h], 2, 64);
-    }
-    if (pl < kChunk && qd == 0) {
-#pragma unroll
-      for (int h = 0; h < 16; h++)
-        if (h < G) e[h * kChunk + pl] = p < c1 ? part[h] * scale : -INFINITY;
-    }
-  }
-  __syncthreads();
-
-  // Softmax partials: one wave per head, one lane per position.
-  const int nw = blockDim.x >> 6;
-  for (int h = wave; h < G; h += nw) {
-    float s = e[h * kChunk + lane];
-    bool valid = c0 + lane < c1;
-    float m = wave_max_f(valid ? s : -INFINITY);
-    float x = valid ? expf(s - m) : 0.f;
-    e[h * kChunk + lane] = x;
-    float l = wave_sum_f(x);
-    if (lane == 0) {
-      mh[h] = m;
-      lh[h] = l;
-    }
-  }
-  __syncthreads();
-
-  // Exp-weighted V sums (and plain V sums for the uniform fallback): thread
-  // (dv, ps) holds four head dimensions and the positions ps, ps + PS, ...;
-  // its V loads are issued together, then partial sums meet in LDS.
-  float *part_o = a.scratch + ((size_t)kvh * a.max_chunks + chunk) * a.part_stride;
-  const int d4n = hd / 4;                  // float4 columns per head
-  const int PS = blockDim.x / d4n;         // position slots
-  const int dv = tid % d4n, ps = tid / d4n;
-  float4 acc[16];
-#pragma unroll
-  for (int h = 0; h < 16; h++) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-  float4 vs = make_float4(0.f, 0.f, 0.f, 0.f);
+  // 1. Loads, all issued up front: this lane's query and new-key pair
+  //    (i, i + KH) with its RoPE factors and its dimensions of the new value;
+  //    then the chunk's keys (lane = half x position, KH dims) and values
+  //    (lane = VW consecutive dims of row lane / VL, RV rows per load).  Rows
+  //    past the chunk's end are clamped onto its first row and masked later.
+  const int ri = lane & (KH - 1);
+  const float *cs = a.rope + (size_t)pos * HD, *sn = cs + KH;
+  const float *qx = a.q + (size_t)h * HD, *kx = a.k + kvh * HD, *vx = a.v + kvh * HD;
+  const float q_re = qx[ri], q_im = qx[ri + KH], k_re = kx[ri], k_im = kx[ri + KH];
+  const float rc = cs[ri], rs = sn[ri];
+  const int vd = (lane % VL) * VW, vr0 = lane / VL;
+  const VT vnew = *reinterpret_cast<const VT *>(vx + vd);
+  float4 kr[NK4];
   {
-    constexpr int kMaxPer = 16;  // kChunk / PS with PS >= 4 (hd <= 256)
-    float4 vv[kMaxPer];
+    const float *kp = kc + (size_t)(c0 + pl < c1 ? c0 + pl : c0) * kvw + half * KH;
 #pragma unroll
-    for (int i = 0; i < kMaxPer; i++) {
-      int p = c0 + ps + i * PS;
-      vv[i] = (ps + i * PS < kChunk && p < c1)
-                  ? *reinterpret_cast<const float4 *>(vc + (size_t)p * kvw + kvh * hd + 4 * dv)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int i = 0; i < kMaxPer; i++) {
-      int pl = ps + i * PS;
-      if (pl >= kChunk || c0 + pl >= c1) continue;
-      vs.x += vv[i].x; vs.y += vv[i].y; vs.z += vv[i].z; vs.w += vv[i].w;
-#pragma unroll
-      for (int h = 0; h < 16; h++) {
-        if (h >= G) continue;
-        float w = e[h * kChunk + pl];
-        acc[h].x += w * vv[i].x; acc[h].y += w * vv[i].y;
-        acc[h].z += w * vv[i].z; acc[h].w += w * vv[i].w;
-      }
-    }
+    for (int j = 0; j < NK4; j++) kr[j] = *reinterpret_cast<const float4 *>(kp + 4 * j);
   }
-  __syncthreads();  // e[] is reused below as the reduction buffer
-  float *red = qs;  // [PS][G + 1][hd], fits in the qs + e region
+  VT vv[NVI];
 #pragma unroll
-  for (int h = 0; h < 16; h++)
-    if (h < G) *reinterpret_cast<float4 *>(red + ((size_t)ps * (G + 1) + h) * hd + 4 * dv) = acc[h];
-  *reinterpret_cast<float4 *>(red + ((size_t)ps * (G + 1) + G) * hd + 4 * dv) = vs;
-  __syncthreads();
-  for (int t = tid; t < (G + 1) * hd; t += blockDim.x) {
-    float s = 0.f;
-    for (int q = 0; q < PS; q++) s += red[(size_t)q * (G + 1) * hd + t];
-    part_o[t] = s;  // [G][hd] exp-weighted sums, then [hd] plain sums
-  }
-  if (tid < G) {
-    part_o[G * hd + hd + tid] = mh[tid];
-    part_o[G * hd + hd + G + tid] = lh[tid];
+  for (int i = 0; i < NVI; i++) {
+    const int p = c0 + i * RV + vr0;
+    vv[i] = *reinterpret_cast<const VT *>(vc + (size_t)(p < c1 ? p : c0) * kvw + vd);
   }
 
-  // The last chunk of this KV head merges all partials.
-  __threadfence();
-  __syncthreads();
-  __shared__ int last;
-  if (tid == 0) last = atomicAdd(a.counters + kvh, 1u) == (unsigned)(n_active - 1);
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  const float *base = a.scratch + (size_t)kvh * a.max_chunks * a.part_stride;
-  float *wsm = qs;  // [n_active][G] rescale weights, then [G] totals
-  for (int t = tid; t < n_active * G; t += blockDim.x)
-    wsm[t] = base[(size_t)(t / G) * a.part_stride + G * hd + hd + (t % G)];
-  __syncthreads();
-  __shared__ float Lh[16];
-  if (tid < G) {
-    float M = -INFINITY;
-    for (int c = 0; c < n_active; c++) M = fmaxf(M, wsm[c * G + tid]);
-    float L = 0.f;
-    for (int c = 0; c < n_active; c++) {
-      float w = expf(wsm[c * G + tid] - M);
-      L += w * base[(size_t)c * a.part_stride + G * hd + hd + G + tid];
-      wsm[c * G + tid] = w;
+  // 2. Rotated query and new key in LDS; the group's first head appends the
+  //    new key and value to the cache.
+  if (lane < KH) {
+    qs[ri] = q_re * rc - q_im * rs;
+    qs[ri + KH] = q_re * rs + q_im * rc;
+    const float r0 = k_re * rc - k_im * rs, r1 = k_re * rs + k_im * rc;
+    kn[ri] = r0;
+    kn[ri + KH] = r1;
+    if (owns_new && h % G == 0) {
+      float *krow = a.k_cache + (size_t)pos * kvw + kvh * HD;
+      krow[ri] = r0;
+      krow[ri + KH] = r1;
     }
-    Lh[tid] = L;
   }
-  __syncthreads();
-  for (int t = tid; t < G * hd; t += blockDim.x) {
-    int h = t / hd, dd = t % hd;
-    float O = 0.f, V = 0.f;
-#pragma unroll 8
-    for (int c = 0; c < n_active; c++) {
-      const float *pc = base + (size_t)c * a.part_stride;
-      O += wsm[c * G + h] * pc[h * hd + dd];
-      V += pc[G * hd + dd];
+  if (owns_new && h % G == 0 && lane < VL)
+    *reinterpret_cast<VT *>(a.v_cache + (size_t)pos * kvw + kvh * HD + vd) = vnew;
+  __syncthreads();  // one wave: orders the LDS writes before the reads below
+  if (owns_new) {
+    if (c0 + pl == pos) {
+#pragma unroll
+      for (int j = 0; j < NK4; j++) kr[j] = *reinterpret_cast<const float4 *>(kn + half * KH + 4 * j);
     }
-    float L = Lh[h];
-    float out = (isfinite(L) && L > 0.f) ? O / L : V / (float)(pos + 1);
-    a.out[(size_t)(kvh * G + h) * hd + dd] = out;
+#pragma unroll
+    for (int i = 0; i < NVI; i++)
+      if (c0 + i * RV + vr0 == pos) vv[i] = vnew;
   }
-  if (tid == 0) a.counters[kvh] = 0u;
+
+  // 3. Score of position pl (both halves end with the full dot), softmax partials.
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NK4; j++) {
+    const float4 q4 = *reinterpret_cast<const float4 *>(qs + half * KH + 4 * j);
+    s += q4.x * kr[j].x + q4.y * kr[j].y + q4.z * kr[j].z + q4.w * kr[j].w;
+  }
+  s += __shfl_xor(s, 32, 64);
+  const bool valid = c0 + pl < c1;
+  s = valid ? s * a.scale : -INFINITY;
+  float m = s;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  const float x = valid ? expf(s - m) : 0.f;
+  float l = x;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+
+  // 4. Exp-weighted and plain V sums of the lane's VW dimensions.
+  float O[VW], Vs[VW];
+#pragma unroll
+  for (int k = 0; k < VW; k++) O[k] = Vs[k] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NVI; i++) {
+    const int p = i * RV + vr0;  // position within the chunk
+    float wp;  // exp weight of position p, held by lane p
+    if constexpr (RV == 1)
+      wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i));
+    else
+      wp = __shfl(x, p, 64);
+    const float in = c0 + p < c1 ? 1.f : 0.f;
+    const float *e = reinterpret_cast<const float *>(&vv[i]);
+#pragma unroll
+    for (int k = 0; k < VW; k++) {
+      O[k] += wp * e[k];
+      Vs[k] += in * e[k];
+    }
+  }
+#pragma unroll
+  for (int o = VL; o < 64; o <<= 1) {
+#pragma unroll
+    for (int k = 0; k < VW; k++) {
+      O[k] += __shfl_xor(O[k], o, 64);
+      Vs[k] += __shfl_xor(Vs[k], o, 64);
+    }
+  }
+
+  float *out = a.out + (size_t)h * HD;
+  if (n_active == 1) {  // the only chunk: finish here
+    if (lane < VL) {
+      const bool ok = isfinite(l) && l > 0.f;
+#pragma unroll
+      for (int k = 0; k < VW; k++) out[vd + k] = ok ? O[k] / l : Vs[k] / (float)(pos + 1);
+    }
+    return;
+  }
+
+  // 5. Publish the partial: [HD] O sums, [HD] V sums, max, sum.
+  float *part = a.scratch + ((size_t)h * a.max_chunks + chunk) * a.part_stride;
+  if (lane < VL) {
+#pragma unroll
+    for (int k = 0; k < VW; k++) {
+      store_dev(part + vd + k, O[k]);
+      store_dev(part + HD + vd + k, Vs[k]);
+    }
+  }
+  if (lane == 0) {
+    store_dev(part + 2 * HD, m);
+    store_dev(part + 2 * HD + 1, l);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial is written through
+  unsigned prev = 0;
+  if (lane == 0)
+    prev = __hip_atomic_fetch_add(a.counters + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = __builtin_amdgcn_readfirstlane(prev);
+  if (prev != (unsigned)(n_active - 1)) return;
+
+  // 6. Merge (last chunk of the head): the lane's VW dimensions, chunks
+  //    folded with a running max, eight at a time.
+  const float *base = a.scratch + (size_t)h * a.max_chunks * a.part_stride;
+  const long stride = a.part_stride;
+  float M = -INFINITY, L = 0.f, R[VW];
+#pragma unroll
+  for (int k = 0; k < VW; k++) R[k] = 0.f;
+  const int d0 = (lane % VL) * VW;
+  for (int cb = 0; cb < n_active; cb += 8) {
+    float o[8][VW], mm[8], ll[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float *pc = base + (size_t)min(cb + j, n_active - 1) * stride;
+#pragma unroll
+      for (int k = 0; k < VW; k++) o[j][k] = load_dev(pc + d0 + k);
+      mm[j] = load_dev(pc + 2 * HD);
+      ll[j] = load_dev(pc + 2 * HD + 1);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      if (cb + j >= n_active || mm[j] == -INFINITY) continue;
+      const float Mn = fmaxf(M, mm[j]);
+      const float sa = expf(M - Mn), sb = expf(mm[j] - Mn);
+      L = L * sa + ll[j] * sb;
+#pragma unroll
+      for (int k = 0; k < VW; k++) R[k] = R[k] * sa + o[j][k] * sb;
+      M = Mn;
+    }
+  }
+  if (lane < VL) {
+    if (isfinite(L) && L > 0.f) {
+#pragma unroll
+      for (int k = 0; k < VW; k++) out[d0 + k] = R[k] / L;
+    } else {
+      float V[VW];
+#pragma unroll
+      for (int k = 0; k < VW; k++) V[k] = 0.f;
+      for (int c = 0; c < n_active; c++)
+#pragma unroll
+        for (int k = 0; k < VW; k++) V[k] += load_dev(base + (size_t)c * stride + HD + d0 + k);
+#pragma unroll
+      for (int k = 0; k < VW; k++) out[d0 + k] = V[k] / (float)(pos + 1);
+    }
+  }
+  if (lane == 0) __hip_atomic_store(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // silu(gate) * up (src/model.rs:251-254).
@@ -338,33 +373,32 @@ int launch_rmsnorm(const float *in, const float *w, float *out, int n, float eps
   return LLRS_OK;
 }
 
-size_t attention_scratch_floats(int nh, int nkv, int hd, int max_seq) {
-  int G = nh / nkv;
-  size_t chunks = (size_t)(max_seq + kChunk - 1) / kChunk;
-  size_t stride = (size_t)G * hd + hd + 2 * G;
-  return (size_t)nkv * chunks * stride;
-}
+long attention_part_stride(int hd) { return 2L * hd + 2; }
 
-int launch_attention(const AttnArgs &args, hipStream_t s) {
-  int G = args.nh / args.nkv;
-  if (args.nh % args.nkv || G > 16 || args.hd > 256 || args.hd % 16 || 256 % args.hd)
-    return set_error(LLRS_E_UNSUPPORTED, "attention geometry %d/%d heads, head_dim %d is not supported",
-                     args.nh, args.nkv, args.hd);
-  // Dynamic LDS: queries + scores; reused as the [PS][G+1][hd] V reduction
-  // buffer (PS * hd = 1024 floats per head) and the combine's weights.
-  size_t floats = (size_t)G * args.hd + (size_t)G * kChunk;
-  floats = std::max(floats, (size_t)1024 * (G + 1));
-  floats = std::max(floats, (size_t)args.max_chunks * G);
-  size_t lds = floats * sizeof(float);
-  if (lds > 160 * 1024)
-    return set_error(LLRS_E_UNSUPPORTED, "attention needs %zu bytes of LDS (context too long)", lds);
-  dim3 grid((unsigned)args.max_chunks, (unsigned)args.nkv);
-  hipLaunchKernelGGL(attention_kernel, grid, dim3(256), lds, s, args);
-  LLRS_HIP(hipGetLastError());
-  return LLRS_OK;
+size_t attention_scratch_floats(int nh, int hd, int max_seq) {
+  return (size_t)nh * (size_t)attention_chunks(max_seq) * (size_t)attention_part_stride(hd);
 }
 
 int attention_chunks(int max_seq) { return (max_seq + kChunk - 1) / kChunk; }
+
+int launch_attention(const AttnArgs &args, hipStream_t s) {
+  const int hd = args.hd;
+  if (args.nkv <= 0 || args.nh % args.nkv || !(hd == 16 || hd == 32 || hd == 64 || hd == 128))
+    return set_error(LLRS_E_UNSUPPORTED, "attention geometry %d/%d heads, head_dim %d is not supported",
+                     args.nh, args.nkv, hd);
+  if (args.part_stride != attention_part_stride(hd) || args.max_chunks != attention_chunks(args.max_seq))
+    return set_error(LLRS_E_INVALID, "attention scratch geometry does not match head_dim %d, context %d",
+                     hd, args.max_seq);
+  const dim3 grid((unsigned)args.max_chunks, (unsigned)args.nh);
+  switch (hd) {
+    case 16: hipLaunchKernelGGL(attention_kernel<16>, grid, dim3(64), 0, s, args); break;
+    case 32: hipLaunchKernelGGL(attention_kernel<32>, grid, dim3(64), 0, s, args); break;
+    case 64: hipLaunchKernelGGL(attention_kernel<64>, grid, dim3(64), 0, s, args); break;
+    default: hipLaunchKernelGGL(attention_kernel<128>, grid, dim3(64), 0, s, args); break;
+  }
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
 
 int launch_silu_mul(const float *g, const float *u, float *out, int n, hipStream_t s) {
   hipLaunchKernelGGL(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, s, g, u, out, n);

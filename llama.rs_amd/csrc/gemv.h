@@ -56,5 +56,9 @@ bool fast_gemv_supports_pair(uint32_t ta, uint32_t tb);
 // Dynamic LDS of one workgroup: the digitised activation and its rows' results.
 size_t fast_gemv_lds_bytes(int cols, int rows, int grid);
 int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s);
+// Workgroups for a launch over `rows` output rows: one per CU (two for the
+// dual gate/up kernel, whose waves hold half the rows), never more than the
+// row quads.
+int fast_gemv_grid(int cu_count, int rows, bool dual);
 
 }  // namespace llrs

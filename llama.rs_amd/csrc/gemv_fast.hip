@@ -7,12 +7,12 @@
 //
 // Activation digits.  Each workgroup converts x (optionally x * norm_gain) to
 // int8 "digits" in LDS: per 16-element block b with scale s_b = max|x|/127,
-//     x_j ~= s_b / 16384 * X_j,   X_j = 16384 d1_j + 128 d2_j + d3_j,
-// d1 in [-127, 127], d2, d3 in [-64, 64] (|error| <= 0.5 of X, 2.4e-7 of the
-// block maximum: the precision of f32).  Weight codes stay in their native
-// GGUF blocks and are multiplied with the digits by v_dot4_i32_i8 (4 int8
-// MACs per instruction, exact int32 accumulation); per-block f16 scales and
-// x-block scales are applied in f32.  Mins/offsets use the exact integer
+//     x_j ~= s_b / 128 * X_j,   X_j = 128 d1_j + d2_j,
+// d1 in [-127, 127], d2 in [-64, 64] (|error| <= 1/256 of s_b, 3.1e-5 of the
+// block maximum).  Weight codes stay in their native GGUF blocks and are
+// multiplied with the digits by v_dot4_i32_i8 (4 int8 MACs per instruction,
+// exact int32 accumulation, Horner over the two planes); per-block f16 scales
+// and x-block scales are applied in f32.  Mins/offsets use the exact integer
 // sums of X per block.  In LDS, x-block b lives at slot (b % 4) * (nb / 4) +
 // b / 4, so the lanes of a wave read consecutive 16-byte slots.
 //
@@ -35,17 +35,17 @@ namespace {
 constexpr int kR = 4;  // rows per wave step
 
 struct Lds {
-  const int8_t *dig;  // [3][cols] digit planes, x-blocks permuted by slot()
-  const float *xs;    // [nb] s_b / 16384 (slot order)
+  const int8_t *dig;  // [2][cols] digit planes, x-blocks permuted by slot()
+  const float *xs;    // [nb] s_b / 128 (slot order)
   const int *sx;      // [nb] sum of X over the block (slot order)
   const float *xsum32;  // [cols/32] sum of reconstructed x per 32 columns
   int cols, nb4;        // nb4 = number of x-blocks / 4
 };
 
-// LDS bytes of the digitised activation: 3 digit planes, per-block scales and
+// LDS bytes of the digitised activation: 2 digit planes, per-block scales and
 // sums, per-32 sums.
 __host__ __device__ constexpr size_t fast_gemv_digit_bytes(int cols) {
-  return (size_t)3 * cols + (size_t)(cols >> 4) * 8 + (size_t)(cols >> 5) * 4;
+  return (size_t)2 * cols + (size_t)(cols >> 4) * 8 + (size_t)(cols >> 5) * 4;
 }
 constexpr size_t kMaxLds = 160 * 1024;
 
@@ -54,13 +54,6 @@ __device__ __forceinline__ int slot(int b, int nb4) { return (b & 3) * nb4 + (b 
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
 }
-__device__ __forceinline__ int combine(int a1, int a2, int a3) {
-  return (a1 << 14) + (a2 << 7) + a3;
-}
-__device__ __forceinline__ uint32_t pick(const uint4 &v, int e) {
-  return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
-}
-
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 // Nine dwords from the dword holding p (p 2-byte aligned): raw[0..8].
@@ -79,11 +72,24 @@ __device__ __forceinline__ uint32_t realign(const uint32_t (&raw)[9], int k, uin
   return __builtin_amdgcn_alignbyte(raw[k + 1], raw[k], sh);
 }
 
-// Digits (3 planes) of x-block b for the lane, as 4 dwords each.
-__device__ __forceinline__ void dig_block(const Lds &L, int b, uint4 (&d)[3]) {
+// Digits (2 planes) of x-block b for the lane, as 4 dwords each.
+__device__ __forceinline__ void dig_block(const Lds &L, int b, uint4 (&d)[2]) {
   int s = slot(b, L.nb4) * 16;
 #pragma unroll
-  for (int p = 0; p < 3; p++) d[p] = *reinterpret_cast<const uint4 *>(L.dig + p * L.cols + s);
+  for (int p = 0; p < 2; p++) d[p] = *reinterpret_cast<const uint4 *>(L.dig + p * L.cols + s);
+}
+
+// sum_j q_j X_j over one x-block (16 weights packed as 4 dwords of int8
+// codes): Horner over the digit planes, X = 128 d1 + d2, exact in int32.
+__device__ __forceinline__ int block_dot(int q0, int q1, int q2, int q3, const uint4 (&d)[2]) {
+  int a = sdot4(q0, (int)d[0].x, 0);
+  a = sdot4(q1, (int)d[0].y, a);
+  a = sdot4(q2, (int)d[0].z, a);
+  a = sdot4(q3, (int)d[0].w, a);
+  a = sdot4(q0, (int)d[1].x, a << 7);
+  a = sdot4(q1, (int)d[1].y, a);
+  a = sdot4(q2, (int)d[1].z, a);
+  return sdot4(q3, (int)d[1].w, a);
 }
 
 // ------------------------------------------------------------------ per type
@@ -98,7 +104,7 @@ template <uint32_t TY> struct Traits;
 template <> struct Traits<LLRS_Q4_K> {
   static constexpr int kColsPerUnit = 64;
   struct Raw { uint4 hdr, q0, q1; };
-  struct Dig { uint4 g[4][3]; float xs[4]; float xsum[2]; };
+  struct Dig { uint4 g[4][2]; float xs[4]; float xsum[2]; };
   static __device__ __forceinline__ void load(const uint8_t *row, int u, Raw &r) {
     const uint8_t *blk = row + (size_t)(u >> 2) * 144;
     int p = u & 3;
@@ -116,41 +122,29 @@ template <> struct Traits<LLRS_Q4_K> {
     D.xsum[1] = L.xsum32[2 * u + 1];
   }
   static __device__ __forceinline__ float dot(const Raw &r, int u, const Dig &D) {
-    int p = u & 3;
-    float d = f16_bits_to_f32((uint16_t)(r.hdr.x & 0xffff));
-    float dmin = f16_bits_to_f32((uint16_t)(r.hdr.x >> 16));
-    // scale_min_k4 for groups 2p and 2p+1 (src/quant.rs:338-347).
-    int sc[2], mn[2];
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-      int g = 2 * p + t;
-      int hh = (g & 3) * 8;
-      int lo_sc = (r.hdr.y >> hh) & 63, lo_mn = (r.hdr.z >> hh) & 63;
-      int hi_sc = ((r.hdr.w >> hh) & 15) | (((r.hdr.y >> (hh + 6)) & 3) << 4);
-      int hi_mn = ((r.hdr.w >> (hh + 4)) & 15) | (((r.hdr.z >> (hh + 6)) & 3) << 4);
-      sc[t] = g < 4 ? lo_sc : hi_sc;
-      mn[t] = g < 4 ? lo_mn : hi_mn;
-    }
-    uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    int acc[4][3] = {};
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      int lo = (int)(w[k] & 0x0f0f0f0fu), hi = (int)((w[k] >> 4) & 0x0f0f0f0fu);
-      int h = k >> 2, e = k & 3;
-#pragma unroll
-      for (int pl = 0; pl < 3; pl++) {
-        acc[h][pl] = sdot4(lo, (int)pick(D.g[h][pl], e), acc[h][pl]);          // group 2p
-        acc[2 + h][pl] = sdot4(hi, (int)pick(D.g[2 + h][pl], e), acc[2 + h][pl]);  // group 2p+1
-      }
-    }
-    float y = 0.f;
-#pragma unroll
-    for (int g = 0; g < 2; g++) {
-      float s = (float)combine(acc[2 * g][0], acc[2 * g][1], acc[2 * g][2]) * D.xs[2 * g] +
-                (float)combine(acc[2 * g + 1][0], acc[2 * g + 1][1], acc[2 * g + 1][2]) * D.xs[2 * g + 1];
-      y += d * (float)sc[g] * s - dmin * (float)mn[g] * D.xsum[g];
-    }
-    return y;
+    const int p = u & 3;
+    const float d = f16_bits_to_f32((uint16_t)(r.hdr.x & 0xffff));
+    const float dmin = f16_bits_to_f32((uint16_t)(r.hdr.x >> 16));
+    // scale_min_k4 of groups 2p, 2p+1 (src/quant.rs:338-347) as byte pairs:
+    // groups < 4 keep 6 bits of scales[g] / scales[g+4]; groups >= 4 join the
+    // nibbles of scales[g+4] with the top two bits of scales[g-4] / scales[g].
+    const int sh = (p & 1) * 16;
+    const uint32_t Y = r.hdr.y >> sh, Z = r.hdr.z >> sh, W = r.hdr.w >> sh;
+    const uint32_t sc = p < 2 ? (Y & 0x3f3fu) : ((W & 0x0f0fu) | ((Y >> 2) & 0x3030u));
+    const uint32_t mn = p < 2 ? (Z & 0x3f3fu) : (((W >> 4) & 0x0f0fu) | ((Z >> 2) & 0x3030u));
+    // Blocks: group 2p = low nibbles of q0 then q1, group 2p+1 = high nibbles.
+    const uint32_t m4 = 0x0f0f0f0fu;
+    const int a0 = block_dot(r.q0.x & m4, r.q0.y & m4, r.q0.z & m4, r.q0.w & m4, D.g[0]);
+    const int a1 = block_dot(r.q1.x & m4, r.q1.y & m4, r.q1.z & m4, r.q1.w & m4, D.g[1]);
+    const int a2 = block_dot((r.q0.x >> 4) & m4, (r.q0.y >> 4) & m4, (r.q0.z >> 4) & m4,
+                             (r.q0.w >> 4) & m4, D.g[2]);
+    const int a3 = block_dot((r.q1.x >> 4) & m4, (r.q1.y >> 4) & m4, (r.q1.z >> 4) & m4,
+                             (r.q1.w >> 4) & m4, D.g[3]);
+    const float s0 = (float)a0 * D.xs[0] + (float)a1 * D.xs[1];
+    const float s1 = (float)a2 * D.xs[2] + (float)a3 * D.xs[3];
+    const float t = (float)(sc & 0xff) * s0 + (float)(sc >> 8) * s1;
+    const float m = (float)(mn & 0xff) * D.xsum[0] + (float)(mn >> 8) * D.xsum[1];
+    return d * t - dmin * m;
   }
 };
 
@@ -159,7 +153,7 @@ template <> struct Traits<LLRS_Q4_K> {
 template <> struct Traits<LLRS_Q6_K> {
   static constexpr int kColsPerUnit = 64;
   struct Raw { uint32_t ql[9], qh[9]; uint32_t shl, shh; uint32_t sc; uint16_t d; };
-  struct Dig { uint4 g[4][3]; float xs[4]; int sx[4]; };
+  struct Dig { uint4 g[4][2]; float xs[4]; int sx[4]; };
   static __device__ __forceinline__ int xb(int u, int i) {  // x-block i of unit u
     int h = (u & 3) >> 1, j = u & 1;
     return (u >> 2) * 16 + h * 8 + j * 2 + (i >> 1) * 4 + (i & 1);
@@ -183,30 +177,27 @@ template <> struct Traits<LLRS_Q6_K> {
     }
   }
   static __device__ __forceinline__ float dot(const Raw &r, int u, const Dig &D) {
-    int j = u & 1, sh_a = 2 * j, sh_b = 2 * j + 4;
-    float d = f16_bits_to_f32(r.d);
-    int acc[4][3] = {};
+    const int j = u & 1, sh_a = 2 * j, sh_b = 2 * j + 4;
+    int qa[8], qb[8];  // 6-bit codes of quarters j and j+2, 4 per dword
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-      uint32_t ql = realign(r.ql, k, r.shl), qh = realign(r.qh, k, r.shh);
-      int qa = (int)((ql & 0x0f0f0f0fu) | (((qh >> sh_a) & 0x03030303u) << 4));         // quarter j
-      int qb = (int)(((ql >> 4) & 0x0f0f0f0fu) | (((qh >> sh_b) & 0x03030303u) << 4));  // quarter j+2
-      int e = k >> 2, f = k & 3;
-#pragma unroll
-      for (int p = 0; p < 3; p++) {
-        acc[e][p] = sdot4(qa, (int)pick(D.g[e][p], f), acc[e][p]);
-        acc[2 + e][p] = sdot4(qb, (int)pick(D.g[2 + e][p], f), acc[2 + e][p]);
-      }
+      const uint32_t ql = realign(r.ql, k, r.shl), qh = realign(r.qh, k, r.shh);
+      qa[k] = (int)((ql & 0x0f0f0f0fu) | (((qh >> sh_a) & 0x03030303u) << 4));
+      qb[k] = (int)(((ql >> 4) & 0x0f0f0f0fu) | (((qh >> sh_b) & 0x03030303u) << 4));
     }
+    const int acc[4] = {block_dot(qa[0], qa[1], qa[2], qa[3], D.g[0]),
+                        block_dot(qa[4], qa[5], qa[6], qa[7], D.g[1]),
+                        block_dot(qb[0], qb[1], qb[2], qb[3], D.g[2]),
+                        block_dot(qb[4], qb[5], qb[6], qb[7], D.g[3])};
     float y = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       // (q - 32) * X summed = sum q*X - 32 * sum X, exact in int32.
-      int I = combine(acc[i][0], acc[i][1], acc[i][2]) - 32 * D.sx[i];
-      int s8 = (int)(int8_t)((r.sc >> (8 * i)) & 0xff);  // i: j/0, j/1, j+2/0, j+2/1
-      y += d * (float)s8 * ((float)I * D.xs[i]);
+      const int I = acc[i] - 32 * D.sx[i];
+      const int s8 = (int)(int8_t)((r.sc >> (8 * i)) & 0xff);  // i: j/0, j/1, j+2/0, j+2/1
+      y += (float)s8 * ((float)I * D.xs[i]);
     }
-    return y;
+    return f16_bits_to_f32(r.d) * y;
   }
 };
 
@@ -214,7 +205,7 @@ template <> struct Traits<LLRS_Q6_K> {
 template <> struct Traits<LLRS_Q8_0> {
   static constexpr int kColsPerUnit = 32;
   struct Raw { uint32_t q[9]; uint32_t sh; uint16_t d; };
-  struct Dig { uint4 g[2][3]; float xs[2]; };
+  struct Dig { uint4 g[2][2]; float xs[2]; };
   static __device__ __forceinline__ void load(const uint8_t *row, int u, Raw &r) {
     const uint8_t *blk = row + (size_t)u * 34;
     load9(blk + 2, r.q, r.sh);
@@ -228,17 +219,12 @@ template <> struct Traits<LLRS_Q8_0> {
     }
   }
   static __device__ __forceinline__ float dot(const Raw &r, int, const Dig &D) {
-    int acc[2][3] = {};
+    int q[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      int q = (int)realign(r.q, k, r.sh);
-      int e = k >> 2, f = k & 3;
-#pragma unroll
-      for (int p = 0; p < 3; p++) acc[e][p] = sdot4(q, (int)pick(D.g[e][p], f), acc[e][p]);
-    }
-    float s = (float)combine(acc[0][0], acc[0][1], acc[0][2]) * D.xs[0] +
-              (float)combine(acc[1][0], acc[1][1], acc[1][2]) * D.xs[1];
-    return f16_bits_to_f32(r.d) * s;
+    for (int k = 0; k < 8; k++) q[k] = (int)realign(r.q, k, r.sh);
+    const int a0 = block_dot(q[0], q[1], q[2], q[3], D.g[0]);
+    const int a1 = block_dot(q[4], q[5], q[6], q[7], D.g[1]);
+    return f16_bits_to_f32(r.d) * ((float)a0 * D.xs[0] + (float)a1 * D.xs[1]);
   }
 };
 
@@ -246,7 +232,7 @@ template <> struct Traits<LLRS_Q8_0> {
 template <> struct Traits<LLRS_Q5_0> {
   static constexpr int kColsPerUnit = 32;
   struct Raw { uint32_t w[6]; uint32_t sh; uint16_t d; };
-  struct Dig { uint4 g[2][3]; float xs[2]; int sx[2]; };
+  struct Dig { uint4 g[2][2]; float xs[2]; int sx[2]; };
   static __device__ __forceinline__ void load(const uint8_t *row, int u, Raw &r) {
     const uint8_t *blk = row + (size_t)u * 22;
     r.sh = (uint32_t)(reinterpret_cast<uintptr_t>(blk + 2) & 3);
@@ -270,22 +256,17 @@ template <> struct Traits<LLRS_Q5_0> {
     return ((t & 15u) * 0x00204081u & 0x01010101u) << 4;
   }
   static __device__ __forceinline__ float dot(const Raw &r, int, const Dig &D) {
-    uint32_t qh = __builtin_amdgcn_alignbyte(r.w[1], r.w[0], r.sh);
-    int acc[2][3] = {};
+    const uint32_t qh = __builtin_amdgcn_alignbyte(r.w[1], r.w[0], r.sh);
+    int qa[4], qb[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      uint32_t v = __builtin_amdgcn_alignbyte(r.w[k + 2], r.w[k + 1], r.sh);
-      int qa = (int)((v & 0x0f0f0f0fu) | spread4(qh >> (4 * k)));
-      int qb = (int)(((v >> 4) & 0x0f0f0f0fu) | spread4(qh >> (16 + 4 * k)));
-#pragma unroll
-      for (int p = 0; p < 3; p++) {
-        acc[0][p] = sdot4(qa, (int)pick(D.g[0][p], k), acc[0][p]);
-        acc[1][p] = sdot4(qb, (int)pick(D.g[1][p], k), acc[1][p]);
-      }
+      const uint32_t v = __builtin_amdgcn_alignbyte(r.w[k + 2], r.w[k + 1], r.sh);
+      qa[k] = (int)((v & 0x0f0f0f0fu) | spread4(qh >> (4 * k)));
+      qb[k] = (int)(((v >> 4) & 0x0f0f0f0fu) | spread4(qh >> (16 + 4 * k)));
     }
     // d * (q - 16) summed against x.
-    int I0 = combine(acc[0][0], acc[0][1], acc[0][2]) - 16 * D.sx[0];
-    int I1 = combine(acc[1][0], acc[1][1], acc[1][2]) - 16 * D.sx[1];
+    const int I0 = block_dot(qa[0], qa[1], qa[2], qa[3], D.g[0]) - 16 * D.sx[0];
+    const int I1 = block_dot(qb[0], qb[1], qb[2], qb[3], D.g[1]) - 16 * D.sx[1];
     return f16_bits_to_f32(r.d) * ((float)I0 * D.xs[0] + (float)I1 * D.xs[1]);
   }
 };
@@ -317,7 +298,7 @@ __device__ float digitize(const float *__restrict__ x, const float *__restrict__
                           int cols, uint8_t *smem, float *red) {
   const int nt = blockDim.x, tid = threadIdx.x, nb = cols >> 4, nb4 = nb >> 2;
   int8_t *dig = reinterpret_cast<int8_t *>(smem);
-  float *xs = reinterpret_cast<float *>(smem + 3 * cols);
+  float *xs = reinterpret_cast<float *>(smem + 2 * cols);
   int *sx = reinterpret_cast<int *>(xs + nb);
   float *xsum32 = reinterpret_cast<float *>(sx + nb);
   float ss = 0.f;
@@ -342,30 +323,26 @@ __device__ float digitize(const float *__restrict__ x, const float *__restrict__
     float m = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; j++) m = fmaxf(m, fabsf(v[j]));
-    uint32_t p1[4] = {0, 0, 0, 0}, p2[4] = {0, 0, 0, 0}, p3[4] = {0, 0, 0, 0};
+    uint32_t p1[4] = {0, 0, 0, 0}, p2[4] = {0, 0, 0, 0};
     int sum = 0;
     float scale = 0.f;
     if (m > 0.f) {
       float is = 127.0f / m;
-      scale = (m / 127.0f) * (1.0f / 16384.0f);
+      scale = (m / 127.0f) * (1.0f / 128.0f);
 #pragma unroll
       for (int j = 0; j < 16; j++) {
         float t = v[j] * is;
         float a1 = rintf(t);
-        float t2 = (t - a1) * 128.0f;
-        float a2 = rintf(t2);
-        float a3 = rintf((t2 - a2) * 128.0f);
-        int i1 = (int)a1, i2 = (int)a2, i3 = (int)a3;
-        sum += i1 * 16384 + i2 * 128 + i3;
+        float a2 = rintf((t - a1) * 128.0f);
+        int i1 = (int)a1, i2 = (int)a2;
+        sum += i1 * 128 + i2;
         p1[j >> 2] |= (uint32_t)(i1 & 0xff) << (8 * (j & 3));
         p2[j >> 2] |= (uint32_t)(i2 & 0xff) << (8 * (j & 3));
-        p3[j >> 2] |= (uint32_t)(i3 & 0xff) << (8 * (j & 3));
       }
     }
     int s = slot(b, nb4);
     *reinterpret_cast<uint4 *>(dig + s * 16) = make_uint4(p1[0], p1[1], p1[2], p1[3]);
     *reinterpret_cast<uint4 *>(dig + cols + s * 16) = make_uint4(p2[0], p2[1], p2[2], p2[3]);
-    *reinterpret_cast<uint4 *>(dig + 2 * cols + s * 16) = make_uint4(p3[0], p3[1], p3[2], p3[3]);
     xs[s] = scale;
     sx[s] = sum;
     float part = scale * (float)sum;
@@ -557,7 +534,7 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
   L.cols = a.cols;
   L.nb4 = a.cols >> 6;
   L.dig = reinterpret_cast<const int8_t *>(smem);
-  L.xs = reinterpret_cast<const float *>(smem + 3 * a.cols);
+  L.xs = reinterpret_cast<const float *>(smem + 2 * a.cols);
   L.sx = reinterpret_cast<const int *>(L.xs + (a.cols >> 4));
   L.xsum32 = reinterpret_cast<const float *>(L.sx + (a.cols >> 4));
 
@@ -706,6 +683,11 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
   PAIR(LLRS_Q4_K, LLRS_Q6_K) PAIR(LLRS_Q4_K, LLRS_Q5_0)
 #undef PAIR
   return set_error(LLRS_E_UNSUPPORTED, "no tuned GEMV for %s + %s", type_name(ta), type_name(tb));
+}
+
+int fast_gemv_grid(int cu_count, int rows, bool dual) {
+  const int g = (dual ? 2 : 1) * cu_count, quads = (rows + kR - 1) / kR;
+  return quads < g ? quads : g;
 }
 
 bool fast_gemv_supports_pair(uint32_t ta, uint32_t tb) {

@@ -63,7 +63,7 @@ struct llrs_kv {
   float *hidden = nullptr, *residual = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
         *attn = nullptr, *gate = nullptr, *up = nullptr, *act = nullptr, *logits = nullptr,
         *scores = nullptr, *rope = nullptr;  // scores: attention partials scratch
-  unsigned *attn_counters = nullptr;         // [nkv] chunk completion counters
+  unsigned *attn_counters = nullptr;         // [nh] chunk completion counters
   int *pos = nullptr;
   uint32_t *tok_by_pos = nullptr, *next_token = nullptr;
   unsigned long long *amax_key = nullptr;  // LM-head argmax accumulator (zero between steps)
@@ -342,10 +342,8 @@ static bool use_fast(llrs_model *m, size_t l, int which) {
   }
 }
 
-static int fast_grid(llrs_model *m, int rows) {
-  int g = 2 * m->b->cu_count;
-  int quads = (rows + 3) / 4;
-  return quads < g ? quads : g;
+static int fast_grid(llrs_model *m, int rows, bool dual = false) {
+  return fast_gemv_grid(m->b->cu_count, rows, dual);
 }
 
 static FastSeg seg_of(const llrs_tensor *t, const float *bias, float *out) {
@@ -429,7 +427,7 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
       a.rows = F;
       a.norm = L.ffn_norm;
       a.epi = kEpiSwiGlu;
-      return launch_gemv_fast(a, fast_grid(m, a.rows), s);
+      return launch_gemv_fast(a, fast_grid(m, a.rows, true), s);
     case P_DOWN:
       if (!fast) return launch_gemv_generic(L.down, kv->act, kv->residual, nullptr, true, s);
       a.seg[0] = seg_of(L.down, nullptr, kv->residual);
@@ -473,7 +471,7 @@ static int enqueue_step(llrs_model *m, llrs_kv *kv, int mode) {
   at.hd = (int)c.head_dim;
   at.max_seq = max_seq;
   at.max_chunks = attention_chunks(max_seq);
-  at.part_stride = (long)(at.nh / at.nkv) * at.hd + at.hd + 2 * (at.nh / at.nkv);
+  at.part_stride = attention_part_stride(at.hd);
   at.scale = 1.0f / sqrtf((float)c.head_dim);
   LLRS_TRY(launch_embed(m->embed, kv->tok_by_pos, kv->pos, max_seq, kv->residual, s));
   for (size_t l = 0; l < c.num_hidden_layers; l++) {
@@ -568,9 +566,8 @@ static int kv_create_impl(llrs_model *m, size_t max_seq, llrs_kv **out) {
       (rc = A((void **)&kv->gate, F * 4)) || (rc = A((void **)&kv->up, F * 4)) ||
       (rc = A((void **)&kv->act, F * 4)) || (rc = A((void **)&kv->logits, c.vocab_size * 4)) ||
       (rc = A((void **)&kv->scores, attention_scratch_floats((int)c.num_attention_heads,
-                                                             (int)c.num_key_value_heads,
                                                              (int)c.head_dim, (int)max_seq) * 4)) ||
-      (rc = A((void **)&kv->attn_counters, 4 * c.num_key_value_heads + 64)) ||
+      (rc = A((void **)&kv->attn_counters, 4 * c.num_attention_heads + 64)) ||
       (rc = A((void **)&kv->rope, max_seq * c.head_dim * 4)) || (rc = A((void **)&kv->pos, 64)) ||
       (rc = A((void **)&kv->tok_by_pos, (max_seq + 1) * 4)) || (rc = A((void **)&kv->next_token, 64)) ||
       (rc = A((void **)&kv->amax_key, 64)) || (rc = A((void **)&kv->done, 64))) {
@@ -596,7 +593,7 @@ static int kv_create_impl(llrs_model *m, size_t max_seq, llrs_kv **out) {
   if (e == hipSuccess) e = hipMemsetAsync(kv->pos, 0, 64, s);
   if (e == hipSuccess) e = hipMemsetAsync(kv->amax_key, 0, 64, s);
   if (e == hipSuccess) e = hipMemsetAsync(kv->done, 0, 64, s);
-  if (e == hipSuccess) e = hipMemsetAsync(kv->attn_counters, 0, 4 * c.num_key_value_heads + 64, s);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->attn_counters, 0, 4 * c.num_attention_heads + 64, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) {
     free_kv(kv);

@@ -78,6 +78,23 @@ def test_head_dim_64_and_gqa_7(llrs, backend, oracle, tmp_path):
     compare_run(llrs, backend, oracle, cfg, tmp_path / "h.gguf", prompt, 32, 96)
 
 
+def test_head_dim_128_long_context(llrs, backend, oracle, tmp_path):
+    """7B-like head_dim 128 over a 330-token context: six attention chunks,
+    the current position appended mid-chunk, partials merged across chunks."""
+    cfg = tiny_cfg(llrs, hidden_size=1024, num_attention_heads=8, num_key_value_heads=2,
+                   intermediate_size=1024, num_hidden_layers=1, vocab_size=600, seed=21)
+    prompt = np.random.default_rng(21).integers(0, cfg.vocab_size, 300).astype(np.uint32)
+    compare_run(llrs, backend, oracle, cfg, tmp_path / "l.gguf", prompt, 32, 512)
+
+
+def test_gqa_16_head_dim_32(llrs, backend, oracle, tmp_path):
+    """The widest supported group: 16 query heads on one KV head, head_dim 32."""
+    cfg = tiny_cfg(llrs, hidden_size=512, num_attention_heads=16, num_key_value_heads=1,
+                   intermediate_size=512, num_hidden_layers=2, vocab_size=500, seed=23)
+    prompt = np.random.default_rng(23).integers(0, cfg.vocab_size, 70).astype(np.uint32)
+    compare_run(llrs, backend, oracle, cfg, tmp_path / "g.gguf", prompt, 32, 128)
+
+
 def test_forward_token_matches_prefill(llrs, backend, oracle, tmp_path):
     cfg = tiny_cfg(llrs, seed=13)
     cfg.write_gguf(tmp_path / "f.gguf")
