@@ -79,7 +79,7 @@ def cpu_baseline(llrs, model, seconds: float, log_prefix="cpu") -> dict:
         t0 = time.perf_counter()
         om.forward_token(1, 0, True)
         first = time.perf_counter() - t0
-        n = int(max(2, min(32, seconds / max(first, 1e-3))))
+        n = int(max(2, min(128, seconds / max(first, 1e-3))))
         log(f"{log_prefix}: first token {first:.2f}s; timing {n} tokens on {threads} threads")
         tok = om.argmax()
         t0 = time.perf_counter()
@@ -98,6 +98,44 @@ def cpu_baseline(llrs, model, seconds: float, log_prefix="cpu") -> dict:
                       f"threads; the Rust reference itself cannot be built here"}
 
 
+COPY_BYTES = 256 << 20  # calibration copy: 256 MiB, 4 times
+
+
+def projection_only(llrs, be, model, which: str, iters: int) -> int:
+    """One projection's launches (every layer, `iters` times) plus a known-size
+    device copy, so that rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of the GEMV
+    kernel can be scaled by what the same counter reads for the copy."""
+    kv = llrs.KVCache(model, 64)
+    us, nb = model.profile_projection(kv, which, iters)
+    lib = llrs.lib()
+    import ctypes as C
+    src, dst = C.c_void_p(), C.c_void_p()
+    llrs._check(lib.llrs_device_alloc(be.handle, COPY_BYTES, C.byref(src)))
+    llrs._check(lib.llrs_device_alloc(be.handle, COPY_BYTES, C.byref(dst)))
+    try:
+        for _ in range(4):
+            llrs._check(lib.llrs_device_copy(be.handle, dst, src, COPY_BYTES))
+    finally:
+        lib.llrs_device_free(be.handle, src)
+        lib.llrs_device_free(be.handle, dst)
+    print(json.dumps({"projection": which, "avg_us": round(us, 2), "bytes": nb,
+                      "copy_bytes": COPY_BYTES, "copies": 4}), flush=True)
+    return 0
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration copy), or None."""
+    f = ROOT / "profiles" / "pmc_traffic_7b_q4km.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        parts = line.strip().strip("`").split()
+        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+            return int(parts[2])
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,6 +146,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-iters", type=int, default=5)
+    ap.add_argument("--projection-only", choices=["qkv", "o", "gate_up", "down", "lm_head"],
+                    help="only time this projection's launches over all layers and run the "
+                         "calibration copy (the workload of the rocprofv3 --pmc traffic runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -130,6 +171,9 @@ def main() -> int:
     mc = model.config()
     wbytes = model.weight_bytes()
     log(f"generated 7B q4km model in HBM in {gen_s:.1f}s: {wbytes / 1e9:.3f} GB of weights/token")
+
+    if args.projection_only:
+        return projection_only(llrs, be, model, args.projection_only, args.profile_iters)
 
     kv = llrs.KVCache(model, args.context)
     prompt = np.random.default_rng(5).integers(0, mc.vocab_size, args.prompt).astype(np.uint32)
@@ -168,7 +212,7 @@ def main() -> int:
     d = per[dom]
     achieved = d["bytes"] / d["avg_us"] / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": profiled_traffic(dom),
                 "kernel": f"{dom} projection GEMV ({d['bytes']} algorithmic weight bytes/launch)"}
 
     cpu = None

@@ -97,6 +97,11 @@ int llrs_device_alloc(llrs_backend *b, size_t nbytes, void **out_dev);
 int llrs_device_free(llrs_backend *b, void *dev);
 int llrs_copy_h2d(llrs_backend *b, void *dst_dev, const void *src, size_t nbytes);
 int llrs_copy_d2h(llrs_backend *b, void *dst, const void *src_dev, size_t nbytes);
+/* Device-to-device copy by a plain streaming kernel (16-byte aligned
+ * pointers, nbytes a multiple of 16); synchronous.  No counterpart in the
+ * reference: it is the known-size copy against which HBM traffic counters of
+ * the other kernels are calibrated. */
+int llrs_device_copy(llrs_backend *b, void *dst_dev, const void *src_dev, size_t nbytes);
 
 /* Host-side quantizers, QuantTensor::quantize_* (src/quant.rs:187-259,
  * 650-967) including their fallbacks (Q4_K -> Q5_0 -> F32, Q6_K -> Q8_0).
@@ -186,12 +191,14 @@ int llrs_read_logits(llrs_kv *kv, float *out, size_t n);
 int llrs_read_kv(llrs_kv *kv, size_t layer, int which /*0 = K, 1 = V*/, float *out, size_t n);
 
 /* Measurement hook (no reference counterpart; llama-bench times whole steps,
- * src/bin/llama-bench.rs:117-126): times the decode step's launch for one
- * projection with HIP events on the backend's stream.  `which`: 0 q, 1 k,
- * 2 v, 3 o, 4 gate, 5 up, 6 down, 7 LM head (LM head: one matrix; the others
- * rotate over every layer so each launch streams fresh weights).  Runs
- * `iters` rounds; returns the mean launch time in microseconds and the
- * matrix bytes one launch reads. */
+ * src/bin/llama-bench.rs:117-126): times the decode step's launch(es) for one
+ * projection group with HIP events on the backend's stream.  `which`: 0 q/k/v
+ * (RMSNorm fused), 1 o (+ residual), 2 gate/up (RMSNorm + SiLU*up fused),
+ * 3 down (+ residual), 4 LM head (RMSNorm + argmax fused).  The layer groups
+ * rotate over every layer so each launch streams its own weights; the LM
+ * head is one matrix.  Runs `iters` rounds and restores the position;
+ * returns the mean launch time in microseconds and the weight bytes one
+ * launch reads. */
 int llrs_profile_projection(llrs_model *m, llrs_kv *kv, int which, int iters, double *avg_us,
                             size_t *bytes_per_launch);
 

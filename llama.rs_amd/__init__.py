@@ -99,6 +99,7 @@ SIGNATURES = [
     ("llrs_device_free", C.c_int, [P, P]),
     ("llrs_copy_h2d", C.c_int, [P, P, P, SZ]),
     ("llrs_copy_d2h", C.c_int, [P, P, P, SZ]),
+    ("llrs_device_copy", C.c_int, [P, P, P, SZ]),
     ("llrs_quantize", C.c_int, [C.c_uint32, F32P, SZ, SZ, P, SZ, C.POINTER(SZ), U32P]),
     ("llrs_gguf_read_tensor", C.c_int, [C.c_char_p, C.c_char_p, U32P, U32P, C.POINTER(SZ),
                                         C.POINTER(SZ), P, SZ, C.POINTER(SZ)]),

@@ -12,6 +12,7 @@
 #include <new>
 
 #include "common.h"
+#include "decode.h"
 #include "gemv.h"
 
 namespace llrs {
@@ -297,6 +298,19 @@ int llrs_copy_d2h(llrs_backend *b, void *dst, const void *src_dev, size_t nbytes
   if (!b) return set_error(LLRS_E_INVALID, "backend is NULL");
   LLRS_HIP(hipSetDevice(b->device));
   LLRS_HIP(hipMemcpyAsync(dst, src_dev, nbytes, hipMemcpyDeviceToHost, b->stream));
+  LLRS_HIP(hipStreamSynchronize(b->stream));
+  return LLRS_OK;
+}
+
+int llrs_device_copy(llrs_backend *b, void *dst_dev, const void *src_dev, size_t nbytes) {
+  clear_error();
+  if (!b) return set_error(LLRS_E_INVALID, "backend is NULL");
+  if (nbytes == 0) return LLRS_OK;
+  if (!dst_dev || !src_dev) return set_error(LLRS_E_INVALID, "NULL device pointer");
+  if ((reinterpret_cast<uintptr_t>(dst_dev) | reinterpret_cast<uintptr_t>(src_dev) | nbytes) & 15)
+    return set_error(LLRS_E_INVALID, "device copy needs 16-byte aligned pointers and length");
+  LLRS_HIP(hipSetDevice(b->device));
+  LLRS_TRY(launch_copy(dst_dev, src_dev, nbytes, b->cu_count, b->stream));
   LLRS_HIP(hipStreamSynchronize(b->stream));
   return LLRS_OK;
 }

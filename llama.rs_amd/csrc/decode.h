@@ -33,5 +33,7 @@ int launch_silu_mul(const float *g, const float *u, float *out, int n, hipStream
 int launch_argmax(const float *logits, int n, int *pos, int max_seq, uint32_t *tok_by_pos,
                   uint32_t *next_token, int advance, hipStream_t s);
 int launch_advance(int *pos, int max_seq, hipStream_t s);
+// dst = src over nbytes (16-byte aligned, a multiple of 16).
+int launch_copy(void *dst, const void *src, size_t nbytes, int cu_count, hipStream_t s);
 
 }  // namespace llrs

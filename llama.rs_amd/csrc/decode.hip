@@ -356,6 +356,13 @@ __global__ void advance_kernel(int *pos, int max_seq) {
   *pos = p > max_seq ? max_seq : p;
 }
 
+// Plain streaming copy (the calibration copy of llrs_device_copy).
+__global__ __launch_bounds__(256) void copy_kernel(uint4 *__restrict__ dst,
+                                                   const uint4 *__restrict__ src, size_t n16) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
 // ------------------------------------------------------------------ launchers
 
 int launch_embed(const llrs_tensor *emb, const uint32_t *tok_by_pos, const int *pos, int max_seq,
@@ -396,6 +403,18 @@ int launch_attention(const AttnArgs &args, hipStream_t s) {
     case 64: hipLaunchKernelGGL(attention_kernel<64>, grid, dim3(64), 0, s, args); break;
     default: hipLaunchKernelGGL(attention_kernel<128>, grid, dim3(64), 0, s, args); break;
   }
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+int launch_copy(void *dst, const void *src, size_t nbytes, int cu_count, hipStream_t s) {
+  const size_t n16 = nbytes / 16;
+  size_t grid = (n16 + 255) / 256;
+  const size_t cap = (size_t)cu_count * 8;
+  if (grid > cap) grid = cap;
+  if (grid == 0) return LLRS_OK;
+  hipLaunchKernelGGL(copy_kernel, dim3((unsigned)grid), dim3(256), 0, s, static_cast<uint4 *>(dst),
+                     static_cast<const uint4 *>(src), n16);
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;
 }

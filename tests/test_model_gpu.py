@@ -139,3 +139,32 @@ def test_config3_qwen05b_shape_greedy_parity(llrs, backend, oracle, tmp_path):
                      ("blk.0.attn_v.weight", QT.Q8_0), ("token_embd.weight", QT.Q8_0),
                      ("blk.0.ffn_down.weight", QT.Q6K)):
         assert llrs.gguf_read_tensor(tmp_path / "c3.gguf", name)[1].quant_type == qt, name
+
+
+def test_softmax_uniform_fallback_on_gpu(llrs, backend, oracle, tmp_path):
+    """A NaN query bias in layer 0 makes every score NaN: the GPU attention must
+    fall back to the plain V mean as softmax_inplace does (src/model.rs:305-312),
+    in the single-chunk case (one position) and across three merged chunks."""
+    cfg = tiny_cfg(llrs, seed=29, num_hidden_layers=2)
+    path = tmp_path / "n.gguf"
+    cfg.write_gguf(path)
+    _, bias = oracle.gguf_read_f32(path, "blk.0.attn_q.bias")
+    raw = bytearray(path.read_bytes())
+    old = bias.astype(np.float32).tobytes()
+    at = raw.find(old)
+    assert at > 0 and raw.find(old, at + 1) < 0
+    raw[at:at + len(old)] = np.full(bias.size, np.nan, np.float32).tobytes()
+    path.write_bytes(bytes(raw))
+    prompt = np.random.default_rng(29).integers(0, cfg.vocab_size, 70).astype(np.uint32)
+    model = llrs.ModelLoader.load_dynamic(path, backend)  # the patched file, not a rewrite
+    kv, om = llrs.KVCache(model, 128), oracle.load(path)
+    for n in (1, len(prompt)):
+        model.prefill(prompt[:n], 0, kv)
+        om.new_state(128)
+        om.prefill(prompt[:n], 0)
+        lg, lo = kv.logits(), om.logits()
+        assert np.isfinite(lo).all()
+        err = float(np.abs(lg - lo).max())
+        print(f"[model] nan-q prompt {n}: logits max-abs err {err:.3e}", flush=True)
+        assert err <= LOGIT_TOL
+        assert kv.argmax() == om.argmax()

@@ -217,3 +217,35 @@ def test_quantizer_fallbacks(llrs):
     assert llrs.QuantTensor.quantize(QT.Q5_0, np.zeros(30, np.float32), 3, 10).quant_type == QT.F32
     t = llrs.QuantTensor.quantize(QT.Q6K, np.zeros(256, np.float32), 1, 256)
     assert t.quant_type == QT.Q6K and t.data == bytes(210)  # all-zero block (src/quant.rs:682-685)
+
+
+def _total_cmp_key(a: np.ndarray) -> np.ndarray:
+    """f32::total_cmp as a signed integer order (IEEE 754 totalOrder):
+    -NaN < -inf < ... < -0 < +0 < ... < +inf < +NaN."""
+    b = a.astype(np.float32).view(np.int32).astype(np.int64)
+    return np.where(b < 0, b ^ 0x7FFFFFFF, b)
+
+
+def test_argmax_total_cmp_last_index_wins(oracle):
+    """argmax_current_logits (src/engine.rs:233-241): Iterator::max_by with
+    total_cmp keeps the LAST of equal maxima; NaNs order by sign."""
+    f32p = ctypes.POINTER(ctypes.c_float)
+
+    def am(v):
+        v = np.ascontiguousarray(v, np.float32)
+        return int(oracle.lib.oq_argmax(v.ctypes.data_as(f32p), v.size))
+
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    neg_nan = np.array([0xFFC00000], np.uint32).view(np.float32)[0]
+    assert am([1, 3, 3, 2]) == 2
+    assert am([-0.0, 0.0]) == 1 and am([0.0, -0.0]) == 0
+    assert am([1, nan, 5]) == 1
+    assert am([neg_nan, -inf]) == 1
+    assert am([inf, inf, 1]) == 1
+    rng = np.random.default_rng(12)
+    pool = np.array([-inf, -1.5, -0.0, 0.0, 0.25, 7.0, inf, nan, neg_nan], np.float32)
+    for _ in range(200):
+        v = pool[rng.integers(0, pool.size, rng.integers(1, 40))]
+        k = _total_cmp_key(v)
+        want = int(np.flatnonzero(k == k.max())[-1])
+        assert am(v) == want, v
