@@ -30,6 +30,7 @@ import numpy as np
 
 ROOT = pathlib.Path(__file__).resolve().parent
 PEAK_HBM_GBS = 8000.0
+PEAK_F16_FLOPS = 2.5e15  # dense f16 MFMA
 METRIC = "batch-1 decode tok/s + achieved HBM GB/s (% of peak), Qwen2.5-7B-shape Q4_K_M"
 
 
@@ -53,6 +54,17 @@ def host_threads() -> int:
     if env and env.isdigit() and int(env) > 0:
         n = min(n, int(env))
     return n
+
+
+def prefill_flops(cfg, n: int) -> float:
+    """Algorithmic FLOPs of an n-token prefill from position 0: 2 per weight per
+    token for every layer matrix, the LM head on the last token only, and the
+    causal attention products (q.k and p.v, 2 FLOPs per multiply-add)."""
+    H, F, KV, L = cfg.hidden_size, cfg.intermediate_size, cfg.kv_width, cfg.num_hidden_layers
+    per_layer = H * H + 2 * KV * H + H * H + 3 * F * H
+    linear = 2.0 * n * L * per_layer + 2.0 * cfg.vocab_size * H
+    attn = 2.0 * 2 * L * cfg.num_attention_heads * cfg.head_dim * (n * (n + 1) / 2)
+    return linear + attn
 
 
 def kv_bytes_per_token(cfg, pos: int) -> int:
@@ -181,7 +193,10 @@ def main() -> int:
     t0 = time.perf_counter()
     model.prefill(prompt, 0, kv)
     prefill_s = time.perf_counter() - t0
-    log(f"prefill {args.prompt} tokens in {prefill_s:.2f}s ({args.prompt / prefill_s:.1f} tok/s)")
+    pf_flops = prefill_flops(mc, args.prompt)
+    log(f"prefill {args.prompt} tokens in {prefill_s * 1e3:.1f} ms ({args.prompt / prefill_s:.1f} tok/s, "
+        f"{pf_flops / prefill_s / 1e12:.1f} TFLOP/s = {100 * pf_flops / prefill_s / PEAK_F16_FLOPS:.2f}% "
+        f"of the f16 MFMA peak)")
 
     start = args.prompt
     if args.warmup:
@@ -230,6 +245,10 @@ def main() -> int:
                    "context": args.context, "global_batch": 1, "parallelism": "none"},
         "hbm_gbps": round(hbm_gbs, 1), "hbm_pct_peak": round(100 * hbm_gbs / PEAK_HBM_GBS, 2),
         "bytes_per_token": int(bytes_tok), "prefill_tps": round(args.prompt / prefill_s, 2),
+        "prefill": {"tokens": args.prompt, "ms": round(prefill_s * 1e3, 2),
+                    "tflops": round(pf_flops / prefill_s / 1e12, 2),
+                    "mfma_util": round(pf_flops / prefill_s / PEAK_F16_FLOPS, 4),
+                    "peak": "2.5 PFLOP/s dense f16"},
         "model_gen_s": round(gen_s, 2), "roofline": roofline, "cpu_baseline": cpu,
         "projections": per,
     }

@@ -22,6 +22,7 @@
 #include "decode.h"
 #include "gemv.h"
 #include "gguf.h"
+#include "prefill.h"
 #include "quantize.h"
 #include "quant_encode.h"
 #include "synth.h"
@@ -72,6 +73,11 @@ struct llrs_kv {
   hipGraph_t graph[2] = {nullptr, nullptr};
   hipGraphExec_t exec[2] = {nullptr, nullptr};
   std::vector<void *> allocs;
+  // Multi-token prefill buffers (allocated on first use, pf_cap token rows).
+  size_t pf_cap = 0;
+  float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_g = nullptr,
+        *pf_u = nullptr;
+  llrs::f16 *pf_h = nullptr, *pf_hl = nullptr;  // GEMM inputs as f16 hi + lo pairs
 };
 
 namespace llrs {
@@ -614,6 +620,94 @@ static int stage_tokens(llrs_kv *kv, const uint32_t *tokens, size_t n, size_t po
   return LLRS_OK;
 }
 
+// Rows of one prefill chunk: bounds the prefill buffers (7B: ~114 MB).
+constexpr size_t kPrefillRows = 512;
+
+static bool prefill_tokenwise() {
+  const char *e = getenv("LLRS_PREFILL_TOKENWISE");
+  return e && *e && *e != '0';
+}
+
+static int prefill_buffers(llrs_kv *kv) {
+  if (kv->pf_cap) return LLRS_OK;
+  const llrs_model_config &c = kv->m->cfg;
+  const size_t T = kv->max_seq_len < kPrefillRows ? kv->max_seq_len : kPrefillRows;
+  const size_t H = c.hidden_size, F = c.intermediate_size, KV = c.kv_width;
+  auto A = [&](void **p, size_t bytes) { return dev_alloc(kv->allocs, p, bytes); };
+  LLRS_TRY(A((void **)&kv->pf_x, T * H * 4));
+  LLRS_TRY(A((void **)&kv->pf_q, T * H * 4));
+  LLRS_TRY(A((void **)&kv->pf_k, T * KV * 4));
+  LLRS_TRY(A((void **)&kv->pf_v, T * KV * 4));
+  LLRS_TRY(A((void **)&kv->pf_g, T * F * 4));
+  LLRS_TRY(A((void **)&kv->pf_u, T * F * 4));
+  LLRS_TRY(A((void **)&kv->pf_h, T * (H > F ? H : F) * 2));
+  LLRS_TRY(A((void **)&kv->pf_hl, T * (H > F ? H : F) * 2));
+  kv->pf_cap = T;
+  return LLRS_OK;
+}
+
+static int prefill_gemm(const llrs_tensor *w, const f16 *a, const f16 *a_lo, int lda, float *c,
+                        int ldc, const float *bias, int T, bool accumulate, hipStream_t s) {
+  PrefillGemmArgs g{};
+  g.a = a;
+  g.a_lo = a_lo;
+  g.lda = lda;
+  g.w = w->dev;
+  g.type = w->type;
+  g.row_bytes = (long)w->row_bytes;
+  g.n = (int)w->rows;
+  g.k = (int)w->cols;
+  g.c = c;
+  g.ldc = ldc;
+  g.bias = bias;
+  g.t = T;
+  g.accumulate = accumulate ? 1 : 0;
+  return launch_prefill_gemm(g, s);
+}
+
+// CausalModel::prefill (src/architecture.rs:60-77) with the prompt's rows
+// batched through each layer: MFMA dequant-GEMMs for the matrices, causal
+// attention over the cache, then the decode step's fused LM head on the last
+// row.  Tokens are staged in tok_by_pos[start, start + n); ends with *pos =
+// start + n and the greedy token of the last logits at tok_by_pos[start + n],
+// exactly as the token-by-token loop leaves them.
+static int prefill_batched(llrs_model *m, llrs_kv *kv, size_t start, size_t n) {
+  const llrs_model_config &c = m->cfg;
+  hipStream_t s = m->b->stream;
+  LLRS_TRY(prefill_buffers(kv));
+  const int H = (int)c.hidden_size, F = (int)c.intermediate_size, KV = (int)c.kv_width;
+  const int nh = (int)c.num_attention_heads, nkv = (int)c.num_key_value_heads, hd = (int)c.head_dim;
+  const float eps = c.rms_norm_eps, scale = 1.0f / sqrtf((float)hd);
+  const size_t layer_stride = kv->max_seq_len * c.kv_width;
+  size_t last_rows = 0;
+  for (size_t c0 = 0; c0 < n; c0 += kv->pf_cap) {
+    const int T = (int)(n - c0 < kv->pf_cap ? n - c0 : kv->pf_cap);
+    const int st = (int)(start + c0);
+    LLRS_TRY(launch_embed_rows(m->embed, kv->tok_by_pos + st, T, kv->pf_x, s));
+    for (size_t l = 0; l < c.num_hidden_layers; l++) {
+      const DevLayer &L = m->layers[l];
+      float *kc = kv->k_cache + l * layer_stride, *vc = kv->v_cache + l * layer_stride;
+      LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.attn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s));
+      LLRS_TRY(prefill_gemm(L.q, kv->pf_h, kv->pf_hl, H, kv->pf_q, H, L.bq, T, false, s));
+      LLRS_TRY(prefill_gemm(L.k, kv->pf_h, kv->pf_hl, H, kv->pf_k, KV, L.bk, T, false, s));
+      LLRS_TRY(prefill_gemm(L.v, kv->pf_h, kv->pf_hl, H, kv->pf_v, KV, L.bv, T, false, s));
+      LLRS_TRY(launch_rope_append(kv->pf_q, kv->pf_k, kv->pf_v, kv->rope, T, st, nh, nkv, hd, kc, vc, s));
+      LLRS_TRY(launch_attention_rows(kv->pf_q, kc, vc, T, st, nh, nkv, hd, scale, kv->pf_h, kv->pf_hl, s));
+      LLRS_TRY(prefill_gemm(L.o, kv->pf_h, kv->pf_hl, H, kv->pf_x, H, nullptr, T, true, s));
+      LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.ffn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s));
+      LLRS_TRY(prefill_gemm(L.gate, kv->pf_h, kv->pf_hl, H, kv->pf_g, F, nullptr, T, false, s));
+      LLRS_TRY(prefill_gemm(L.up, kv->pf_h, kv->pf_hl, H, kv->pf_u, F, nullptr, T, false, s));
+      LLRS_TRY(launch_swiglu_f16(kv->pf_g, kv->pf_u, kv->pf_h, kv->pf_hl, (size_t)T * F, s));
+      LLRS_TRY(prefill_gemm(L.down, kv->pf_h, kv->pf_hl, F, kv->pf_x, H, nullptr, T, true, s));
+    }
+    last_rows = (size_t)T;
+  }
+  LLRS_HIP(hipMemcpyAsync(kv->residual, kv->pf_x + (last_rows - 1) * H, (size_t)H * 4,
+                          hipMemcpyDeviceToDevice, s));
+  LLRS_TRY(launch_set_pos(kv->pos, (int)(start + n - 1), s));
+  return launch_projection(m, kv, 0, P_LM_HEAD, s);
+}
+
 }  // namespace llrs
 
 using namespace llrs;
@@ -803,8 +897,12 @@ int llrs_prefill(llrs_model *m, llrs_kv *kv, const uint32_t *tokens, size_t n, s
   }
   LLRS_HIP(hipSetDevice(m->b->device));
   LLRS_TRY(stage_tokens(kv, tokens, n, start_pos));
-  for (size_t i = 0; i < n; i++)
-    LLRS_TRY(run_step(m, kv, i + 1 == n ? LLRS_LOGITS_COMPUTE : LLRS_LOGITS_SKIP));
+  if (n >= 2 && !prefill_tokenwise()) {
+    LLRS_TRY(prefill_batched(m, kv, start_pos, n));
+  } else {
+    for (size_t i = 0; i < n; i++)
+      LLRS_TRY(run_step(m, kv, i + 1 == n ? LLRS_LOGITS_COMPUTE : LLRS_LOGITS_SKIP));
+  }
   LLRS_HIP(hipStreamSynchronize(m->b->stream));
   return LLRS_OK;
 }

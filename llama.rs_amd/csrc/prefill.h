@@ -1,0 +1,49 @@
+// Multi-token prefill (CausalModel::prefill, src/architecture.rs:60-77): the
+// prompt's tokens go through each layer together, the weight matrices as
+// MFMA dequant-GEMMs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace llrs {
+
+typedef _Float16 f16;
+
+// C[t][n] (=|+=) sum_k A[t][k] * W[n][k] (+ bias[n]) for t < T, n < rows(W).
+struct PrefillGemmArgs {
+  const f16 *a, *a_lo;  // [T][lda] activations as hi + lo f16 pairs
+  int lda;
+  const uint8_t *w;  // native GGUF rows
+  uint32_t type;
+  long row_bytes;
+  int n, k;       // rows and cols of W
+  float *c;       // [T][ldc]
+  int ldc;
+  const float *bias;  // [n] or null; ignored when accumulating
+  int t;
+  int accumulate;
+};
+
+int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s);
+
+// x[t][:] = embedding row of tok[t] (bit-exact dequant), t < T.
+int launch_embed_rows(const llrs_tensor *emb, const uint32_t *tok, int T, float *x, hipStream_t s);
+// out + out_lo [t][:] = x[t] * (1/sqrt(mean(x[t]^2) + eps) * w) as f16 pairs.
+int launch_rmsnorm_rows_f16(const float *x, const float *w, f16 *out, f16 *out_lo, int T, int H,
+                            float eps, hipStream_t s);
+// Split-half RoPE of q (in place) and k at positions start + t, and the K/V
+// cache rows of those positions.
+int launch_rope_append(float *q, const float *k, const float *v, const float *rope, int T, int start,
+                       int nh, int nkv, int hd, float *k_cache, float *v_cache, hipStream_t s);
+// Causal GQA attention of the T query rows (positions start + t) over the
+// cache, out + out_lo [T][nh*hd] (f16 pairs).
+int launch_attention_rows(const float *q, const float *k_cache, const float *v_cache, int T,
+                          int start, int nh, int nkv, int hd, float scale, f16 *out, f16 *out_lo,
+                          hipStream_t s);
+// out + out_lo [i] = silu(g[i]) * u[i] as f16 pairs, i < n.
+int launch_swiglu_f16(const float *g, const float *u, f16 *out, f16 *out_lo, size_t n, hipStream_t s);
+int launch_set_pos(int *pos, int value, hipStream_t s);
+
+}  // namespace llrs

@@ -1,0 +1,474 @@
+// Multi-token prefill kernels: the prompt goes through each layer as a
+// T-row batch (CausalModel::prefill, src/architecture.rs:60-77, computed the
+// way Qwen2Model::forward_impl, src/model.rs:135-271, computes one token).
+//
+// The weight matrices run as MFMA dequant-GEMMs: a workgroup owns a 64-token x
+// 64-row output tile.  It dequantizes its 64 weight rows 128 columns at a time
+// from the native GGUF blocks (value_at, src/quant.rs:349-456) into LDS,
+// stages the matching activation tile, and accumulates
+// v_mfma_f32_16x16x32_f16 products in f32.  Each wave holds a 32 x 32 quarter
+// of the tile (2 x 2 MFMA blocks).
+//
+// Precision: f32 operands are carried as f16 pairs, v = hi + lo with hi =
+// f16(v) and lo = f16(v - hi) (22 significant bits), and each product is
+// hi*hi + hi*lo + lo*hi (the lo*lo term is below f32 rounding of the sum), so
+// the GEMM is close to an f32 GEMM rather than an f16 one.
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "common.h"
+#include "prefill.h"
+#include "quant_dev.h"
+
+namespace llrs {
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 64, BN = 64, KC = 128, LS = KC + 8;  // LS: LDS row stride in halves
+
+// The 32 values of `row` at columns [k0, k0 + 32) (k0 a multiple of 32), as
+// value_at computes them.
+template <uint32_t TY> struct Deq {
+  static __device__ __forceinline__ void run(const uint8_t *row, uint32_t ty, int k0, float (&v)[32]) {
+#pragma unroll
+    for (int j = 0; j < 32; j++) v[j] = value_dev(row, ty, (uint32_t)(k0 + j));
+  }
+};
+
+template <> struct Deq<LLRS_Q4_K> {
+  static __device__ __forceinline__ void run(const uint8_t *row, uint32_t, int k0, float (&v)[32]) {
+#pragma clang fp contract(off)
+    const uint8_t *b = row + (size_t)(k0 >> 8) * 144;
+    const int g = (k0 & 255) >> 5;
+    int sc, mn;
+    scale_min_k4(g, b + 4, sc, mn);
+    const float ds = ld_f16(b) * (float)sc, dm = ld_f16(b + 2) * (float)mn;
+    const uint4 q0 = *reinterpret_cast<const uint4 *>(b + 16 + (g >> 1) * 32);
+    const uint4 q1 = *reinterpret_cast<const uint4 *>(b + 32 + (g >> 1) * 32);
+    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const int shift = (g & 1) * 4;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      const int q = (int)((w[j >> 2] >> (8 * (j & 3) + shift)) & 15);
+      v[j] = ds * (float)q - dm;
+    }
+  }
+};
+
+template <> struct Deq<LLRS_Q6_K> {
+  static __device__ __forceinline__ void run(const uint8_t *row, uint32_t, int k0, float (&v)[32]) {
+#pragma clang fp contract(off)
+    const uint8_t *b = row + (size_t)(k0 >> 8) * 210;
+    const int j0 = k0 & 255, half = j0 >> 7, quarter = (j0 >> 5) & 3;
+    uint32_t ql[9], qh[9], shl, shh;
+    load9(b + half * 64 + (quarter & 1) * 32, ql, shl);
+    load9(b + 128 + half * 32, qh, shh);
+    const uint16_t s2 = ld_u16(b + 192 + half * 8 + quarter * 2);
+    const float d = ld_f16(b + 208);
+    const float sc0 = d * (float)(int8_t)(s2 & 0xff), sc1 = d * (float)(int8_t)(s2 >> 8);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t l = realign(ql, k, shl), h = realign(qh, k, shh);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int lb = (int)((l >> (8 * e)) & 0xff);
+        const int lo = quarter < 2 ? (lb & 15) : (lb >> 4);
+        const int hi = (int)((h >> (8 * e + 2 * quarter)) & 3);
+        const int j = 4 * k + e;
+        v[j] = (j < 16 ? sc0 : sc1) * (float)((lo | (hi << 4)) - 32);
+      }
+    }
+  }
+};
+
+template <> struct Deq<LLRS_Q8_0> {
+  static __device__ __forceinline__ void run(const uint8_t *row, uint32_t, int k0, float (&v)[32]) {
+    const uint8_t *b = row + (size_t)(k0 >> 5) * 34;
+    uint32_t q[9], sh;
+    load9(b + 2, q, sh);
+    const float d = ld_f16(b);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t w = realign(q, k, sh);
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[4 * k + e] = d * (float)(int8_t)((w >> (8 * e)) & 0xff);
+    }
+  }
+};
+
+template <> struct Deq<LLRS_Q5_0> {
+  static __device__ __forceinline__ void run(const uint8_t *row, uint32_t, int k0, float (&v)[32]) {
+#pragma clang fp contract(off)
+    const uint8_t *b = row + (size_t)(k0 >> 5) * 22;
+    uint32_t r[9], sh;
+    load9(b + 2, r, sh);  // qh (4 bytes) then 16 bytes of nibbles
+    const uint32_t qh = realign(r, 0, sh);
+    const float d = ld_f16(b);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t w = realign(r, k + 1, sh);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int j = 4 * k + e;
+        const int lo = (int)((w >> (8 * e)) & 15), hi = (int)((w >> (8 * e + 4)) & 15);
+        v[j] = d * ((float)(lo | (int)(((qh >> j) & 1) << 4)) - 16.0f);
+        v[j + 16] = d * ((float)(hi | (int)(((qh >> (j + 16)) & 1) << 4)) - 16.0f);
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ void split_f16(float v, f16 &hi, f16 &lo) {
+  hi = (f16)v;
+  lo = (f16)(v - (float)hi);
+}
+
+template <uint32_t TY>
+__global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
+  extern __shared__ __align__(16) f16 lds[];
+  f16 *As = lds, *Al = As + BM * LS, *Ws = Al + BM * LS, *Wl = Ws + BN * LS;
+  const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int wr = tid >> 2, wsub = tid & 3;  // this thread's weight row and 32-column run
+  const bool wrow_ok = n0 + wr < g.n;
+  const uint8_t *wrow = g.w + (size_t)(wrow_ok ? n0 + wr : 0) * g.row_bytes;
+  for (int k0 = 0; k0 < g.k; k0 += KC) {
+    const int kc = min(KC, g.k - k0);  // a multiple of 32
+#pragma unroll
+    for (int q = 0; q < 4; q++) {  // activations: 64 rows x 16 chunks of 8 halves
+      const int i = tid + 256 * q, r = i >> 4, c8 = i & 15;
+      half8 hv = half8{0, 0, 0, 0, 0, 0, 0, 0}, lv = hv;
+      if (t0 + r < g.t && c8 * 8 < kc) {
+        const size_t off = (size_t)(t0 + r) * g.lda + k0 + c8 * 8;
+        hv = *reinterpret_cast<const half8 *>(g.a + off);
+        lv = *reinterpret_cast<const half8 *>(g.a_lo + off);
+      }
+      *reinterpret_cast<half8 *>(As + r * LS + c8 * 8) = hv;
+      *reinterpret_cast<half8 *>(Al + r * LS + c8 * 8) = lv;
+    }
+    {
+      const int kk = k0 + 32 * wsub;
+      float v[32];
+      if (wrow_ok && kk < g.k) {
+        Deq<TY>::run(wrow, g.type, kk, v);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 32; j++) v[j] = 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        half8 h, l;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          f16 a, b;
+          split_f16(v[8 * q + e], a, b);
+          h[e] = a;
+          l[e] = b;
+        }
+        *reinterpret_cast<half8 *>(Ws + wr * LS + 32 * wsub + 8 * q) = h;
+        *reinterpret_cast<half8 *>(Wl + wr * LS + 32 * wsub + 8 * q) = l;
+      }
+    }
+    __syncthreads();
+    for (int ks = 0; ks < kc; ks += 32) {
+      half8 af[2], al[2], bf[2], bl[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const int o = (wm * 32 + 16 * i + (lane & 15)) * LS + ks + 8 * (lane >> 4);
+        af[i] = *reinterpret_cast<const half8 *>(As + o);
+        al[i] = *reinterpret_cast<const half8 *>(Al + o);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int o = (wn * 32 + 16 * j + (lane & 15)) * LS + ks + 8 * (lane >> 4);
+        bf[j] = *reinterpret_cast<const half8 *>(Ws + o);
+        bl[j] = *reinterpret_cast<const half8 *>(Wl + o);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bl[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    __syncthreads();
+  }
+  // D layout: lane holds column (lane & 15) and rows 4 * (lane >> 4) + e.
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int n = n0 + wn * 32 + 16 * j + (lane & 15);
+      if (n >= g.n) continue;
+      const float bias = (!g.accumulate && g.bias) ? g.bias[n] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int t = t0 + wm * 32 + 16 * i + 4 * (lane >> 4) + e;
+        if (t >= g.t) continue;
+        float *c = g.c + (size_t)t * g.ldc + n;
+        *c = g.accumulate ? *c + acc[i][j][e] : acc[i][j][e] + bias;
+      }
+    }
+}
+
+__global__ void embed_rows_kernel(const uint8_t *__restrict__ emb, uint32_t ty, size_t row_bytes,
+                                  int H, uint32_t vocab, const uint32_t *__restrict__ tok, int T,
+                                  float *__restrict__ x) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  if (c >= H || t >= T) return;
+  uint32_t id = tok[t];
+  if (id >= vocab) id = vocab - 1;  // validated on the host; never read past the table
+  x[(size_t)t * H + c] = value_dev(emb + (size_t)id * row_bytes, ty, (uint32_t)c);
+}
+
+// RMSNorm::forward (src/model.rs:65-73) per token row, rounded to f16.
+__global__ __launch_bounds__(256) void rmsnorm_rows_f16_kernel(const float *__restrict__ x,
+                                                               const float *__restrict__ w,
+                                                               f16 *__restrict__ out,
+                                                               f16 *__restrict__ out_lo, int H,
+                                                               float eps) {
+#pragma clang fp contract(off)
+  __shared__ float red[4];
+  const float *xr = x + (size_t)blockIdx.x * H;
+  float s = 0.f;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) s += xr[i] * xr[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+  f16 *o = out + (size_t)blockIdx.x * H, *ol = out_lo + (size_t)blockIdx.x * H;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) split_f16(xr[i] * (inv * w[i]), o[i], ol[i]);
+}
+
+// Split-half RoPE (src/model.rs:87-95) of the row's query heads (in place)
+// and key heads, and the K/V cache rows of position start + t
+// (KVCache::update, src/cache.rs:38-53).
+__global__ __launch_bounds__(256) void rope_append_kernel(float *__restrict__ q,
+                                                          const float *__restrict__ k,
+                                                          const float *__restrict__ v,
+                                                          const float *__restrict__ rope, int start,
+                                                          int nh, int nkv, int hd,
+                                                          float *__restrict__ k_cache,
+                                                          float *__restrict__ v_cache) {
+  const int t = blockIdx.x, p = start + t, half = hd / 2, kvw = nkv * hd;
+  const float *cs = rope + (size_t)p * hd, *sn = cs + half;
+  float *qr = q + (size_t)t * nh * hd;
+  for (int i = threadIdx.x; i < nh * half; i += blockDim.x) {
+    const int h = i / half, j = i % half;
+    const float re = qr[h * hd + j], im = qr[h * hd + j + half];
+    qr[h * hd + j] = re * cs[j] - im * sn[j];
+    qr[h * hd + j + half] = re * sn[j] + im * cs[j];
+  }
+  const float *kr = k + (size_t)t * kvw;
+  float *kd = k_cache + (size_t)p * kvw;
+  for (int i = threadIdx.x; i < nkv * half; i += blockDim.x) {
+    const int h = i / half, j = i % half;
+    const float re = kr[h * hd + j], im = kr[h * hd + j + half];
+    kd[h * hd + j] = re * cs[j] - im * sn[j];
+    kd[h * hd + j + half] = re * sn[j] + im * cs[j];
+  }
+  const float *vr = v + (size_t)t * kvw;
+  float *vd = v_cache + (size_t)p * kvw;
+  for (int i = threadIdx.x; i < kvw; i += blockDim.x) vd[i] = vr[i];
+}
+
+// Causal GQA attention of one query row and head (src/model.rs:206-231,
+// softmax_inplace 298-313): one wave walks the positions 0..start+t in chunks
+// of 32 (lane = half of the head x position for the scores, VW dims per lane
+// for the values) and folds them with a running max; the uniform fallback
+// applies when no finite positive total remains.
+template <int HD>
+__global__ __launch_bounds__(64) void attention_rows_kernel(const float *__restrict__ q,
+                                                            const float *__restrict__ k_cache,
+                                                            const float *__restrict__ v_cache,
+                                                            int start, int nh, int nkv, float scale,
+                                                            f16 *__restrict__ out,
+                                                            f16 *__restrict__ out_lo) {
+  constexpr int KH = HD / 2, NK4 = KH / 4;
+  constexpr int VW = HD >= 64 ? HD / 64 : 1, VL = HD / VW, RV = 64 / VL, NVI = 32 / RV;
+  using VT = typename std::conditional<VW == 2, float2, float>::type;
+  const int t = blockIdx.x, h = blockIdx.y, G = nh / nkv, kvh = h / G, kvw = nkv * HD;
+  const int p = start + t;
+  const int lane = threadIdx.x, half = lane >> 5, pl = lane & 31;
+  const int vd = (lane % VL) * VW, vr0 = lane / VL;
+  float4 qr[NK4];
+  {
+    const float *qp = q + (size_t)t * nh * HD + h * HD + half * KH;
+#pragma unroll
+    for (int j = 0; j < NK4; j++) qr[j] = *reinterpret_cast<const float4 *>(qp + 4 * j);
+  }
+  const float *kc = k_cache + (size_t)kvh * HD, *vc = v_cache + (size_t)kvh * HD;
+  float M = -INFINITY, L = 0.f, O[VW], Vs[VW];
+#pragma unroll
+  for (int e = 0; e < VW; e++) O[e] = Vs[e] = 0.f;
+  for (int c0 = 0; c0 <= p; c0 += 32) {
+    const int c1 = min(c0 + 32, p + 1);
+    float4 kr[NK4];
+    {
+      const float *kp = kc + (size_t)(c0 + pl < c1 ? c0 + pl : c0) * kvw + half * KH;
+#pragma unroll
+      for (int j = 0; j < NK4; j++) kr[j] = *reinterpret_cast<const float4 *>(kp + 4 * j);
+    }
+    VT vv[NVI];
+#pragma unroll
+    for (int i = 0; i < NVI; i++) {
+      const int pp = c0 + i * RV + vr0;
+      vv[i] = *reinterpret_cast<const VT *>(vc + (size_t)(pp < c1 ? pp : c0) * kvw + vd);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NK4; j++)
+      s += qr[j].x * kr[j].x + qr[j].y * kr[j].y + qr[j].z * kr[j].z + qr[j].w * kr[j].w;
+    s += __shfl_xor(s, 32, 64);
+    const bool valid = c0 + pl < c1;
+    s = valid ? s * scale : -INFINITY;
+    float mc = s;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o, 64));
+    const float x = valid ? expf(s - mc) : 0.f;
+    float lc = x;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) lc += __shfl_xor(lc, o, 64);
+    float Oc[VW];
+#pragma unroll
+    for (int e = 0; e < VW; e++) Oc[e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NVI; i++) {
+      const int pp = i * RV + vr0;
+      float wp;
+      if constexpr (RV == 1)
+        wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i));
+      else
+        wp = __shfl(x, pp, 64);
+      const float in = c0 + pp < c1 ? 1.f : 0.f;
+      const float *ev = reinterpret_cast<const float *>(&vv[i]);
+#pragma unroll
+      for (int e = 0; e < VW; e++) {
+        Oc[e] += wp * ev[e];
+        Vs[e] += in * ev[e];
+      }
+    }
+#pragma unroll
+    for (int o = VL; o < 64; o <<= 1)
+#pragma unroll
+      for (int e = 0; e < VW; e++) Oc[e] += __shfl_xor(Oc[e], o, 64);
+    if (mc != -INFINITY) {
+      const float Mn = fmaxf(M, mc);
+      const float sa = expf(M - Mn), sb = expf(mc - Mn);
+      L = L * sa + lc * sb;
+#pragma unroll
+      for (int e = 0; e < VW; e++) O[e] = O[e] * sa + Oc[e] * sb;
+      M = Mn;
+    }
+  }
+#pragma unroll
+  for (int o = VL; o < 64; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < VW; e++) Vs[e] += __shfl_xor(Vs[e], o, 64);
+  if (lane < VL) {
+    const bool ok = isfinite(L) && L > 0.f;
+    const size_t at = (size_t)t * nh * HD + h * HD + vd;
+#pragma unroll
+    for (int e = 0; e < VW; e++)
+      split_f16(ok ? O[e] / L : Vs[e] / (float)(p + 1), out[at + e], out_lo[at + e]);
+  }
+}
+
+__global__ void swiglu_f16_kernel(const float *__restrict__ g, const float *__restrict__ u,
+                                  f16 *__restrict__ out, f16 *__restrict__ out_lo, size_t n) {
+#pragma clang fp contract(off)
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const float x = g[i];
+    split_f16((x / (1.0f + expf(-x))) * u[i], out[i], out_lo[i]);
+  }
+}
+
+__global__ void set_pos_kernel(int *pos, int value) { *pos = value; }
+
+}  // namespace
+
+int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
+  if (g.k % 32 || g.lda % 8 || g.n <= 0 || g.k <= 0 || g.t <= 0)
+    return set_error(LLRS_E_UNSUPPORTED, "prefill GEMM shape %d x %d (lda %d) is not supported", g.n,
+                     g.k, g.lda);
+  const dim3 grid((unsigned)((g.n + BN - 1) / BN), (unsigned)((g.t + BM - 1) / BM));
+  const size_t lds = (size_t)2 * (BM + BN) * LS * sizeof(f16);
+  switch (g.type) {
+    case LLRS_Q4_K: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q4_K>, grid, dim3(256), lds, s, g); break;
+    case LLRS_Q6_K: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q6_K>, grid, dim3(256), lds, s, g); break;
+    case LLRS_Q8_0: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q8_0>, grid, dim3(256), lds, s, g); break;
+    case LLRS_Q5_0: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q5_0>, grid, dim3(256), lds, s, g); break;
+    default: hipLaunchKernelGGL(prefill_gemm_kernel<0xffffffffu>, grid, dim3(256), lds, s, g); break;
+  }
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+int launch_embed_rows(const llrs_tensor *emb, const uint32_t *tok, int T, float *x, hipStream_t s) {
+  const int H = (int)emb->cols;
+  hipLaunchKernelGGL(embed_rows_kernel, dim3((H + 255) / 256, T), dim3(256), 0, s, emb->dev,
+                     emb->type, emb->row_bytes, H, (uint32_t)emb->rows, tok, T, x);
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+int launch_rmsnorm_rows_f16(const float *x, const float *w, f16 *out, f16 *out_lo, int T, int H,
+                            float eps, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_rows_f16_kernel, dim3(T), dim3(256), 0, s, x, w, out, out_lo, H, eps);
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+int launch_rope_append(float *q, const float *k, const float *v, const float *rope, int T, int start,
+                       int nh, int nkv, int hd, float *k_cache, float *v_cache, hipStream_t s) {
+  hipLaunchKernelGGL(rope_append_kernel, dim3(T), dim3(256), 0, s, q, k, v, rope, start, nh, nkv, hd,
+                     k_cache, v_cache);
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+int launch_attention_rows(const float *q, const float *k_cache, const float *v_cache, int T,
+                          int start, int nh, int nkv, int hd, float scale, f16 *out, f16 *out_lo,
+                          hipStream_t s) {
+  const dim3 grid((unsigned)T, (unsigned)nh);
+  switch (hd) {
+    case 16: hipLaunchKernelGGL(attention_rows_kernel<16>, grid, dim3(64), 0, s, q, k_cache, v_cache, start, nh, nkv, scale, out, out_lo); break;
+    case 32: hipLaunchKernelGGL(attention_rows_kernel<32>, grid, dim3(64), 0, s, q, k_cache, v_cache, start, nh, nkv, scale, out, out_lo); break;
+    case 64: hipLaunchKernelGGL(attention_rows_kernel<64>, grid, dim3(64), 0, s, q, k_cache, v_cache, start, nh, nkv, scale, out, out_lo); break;
+    case 128: hipLaunchKernelGGL(attention_rows_kernel<128>, grid, dim3(64), 0, s, q, k_cache, v_cache, start, nh, nkv, scale, out, out_lo); break;
+    default: return set_error(LLRS_E_UNSUPPORTED, "attention head_dim %d is not supported", hd);
+  }
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+int launch_swiglu_f16(const float *g, const float *u, f16 *out, f16 *out_lo, size_t n, hipStream_t s) {
+  hipLaunchKernelGGL(swiglu_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, u, out,
+                     out_lo, n);
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+int launch_set_pos(int *pos, int value, hipStream_t s) {
+  hipLaunchKernelGGL(set_pos_kernel, dim3(1), dim3(1), 0, s, pos, value);
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+}  // namespace llrs

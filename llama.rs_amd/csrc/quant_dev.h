@@ -105,4 +105,22 @@ __device__ inline float value_dev(const uint8_t *row, uint32_t ty, uint32_t col)
   }
 }
 
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// Nine dwords from the dword holding p (p 2-byte aligned): raw[0..8].
+__device__ __forceinline__ void load9(const uint8_t *p, uint32_t (&raw)[9], uint32_t &sh) {
+  // The aligned pointer is derived from p itself (not from an integer) so the
+  // compiler keeps it in the global address space: global_load, not flat_load.
+  sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3);  // byte shift for v_alignbyte_b32 (0 or 2)
+  const uint32_t *base = reinterpret_cast<const uint32_t *>(p - sh);
+  u32x4a4 v0 = *reinterpret_cast<const u32x4a4 *>(base);
+  u32x4a4 v1 = *reinterpret_cast<const u32x4a4 *>(base + 4);
+  raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
+  raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
+  raw[8] = base[8];
+}
+__device__ __forceinline__ uint32_t realign(const uint32_t (&raw)[9], int k, uint32_t sh) {
+  return __builtin_amdgcn_alignbyte(raw[k + 1], raw[k], sh);
+}
+
 }  // namespace llrs

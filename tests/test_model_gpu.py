@@ -95,17 +95,32 @@ def test_gqa_16_head_dim_32(llrs, backend, oracle, tmp_path):
     compare_run(llrs, backend, oracle, cfg, tmp_path / "g.gguf", prompt, 32, 128)
 
 
-def test_forward_token_matches_prefill(llrs, backend, oracle, tmp_path):
+def test_forward_token_matches_prefill(llrs, backend, oracle, tmp_path, monkeypatch):
+    """The batched (MFMA) prefill agrees with the token-by-token loop of
+    CausalModel::prefill (src/architecture.rs:60-77) within the logits bar;
+    the token-by-token prefill is bit-identical to forward_token calls."""
     cfg = tiny_cfg(llrs, seed=13)
     cfg.write_gguf(tmp_path / "f.gguf")
     model = llrs.ModelLoader.load_dynamic(tmp_path / "f.gguf", backend)
-    prompt = np.array([5, 17, 999, 0, 42], np.uint32)
-    kv1, kv2 = llrs.KVCache(model, 32), llrs.KVCache(model, 32)
+    prompt = np.array([5, 17, 999, 0, 42, 7, 7, 300], np.uint32)
+    kv1, kv2, kv3 = (llrs.KVCache(model, 32) for _ in range(3))
     model.prefill(prompt, 0, kv1)
     for i, t in enumerate(prompt):
         model.forward_token(int(t), i, kv2,
                             llrs.LogitsMode.COMPUTE if i + 1 == len(prompt) else llrs.LogitsMode.SKIP)
-    np.testing.assert_array_equal(kv1.logits(), kv2.logits())
+    monkeypatch.setenv("LLRS_PREFILL_TOKENWISE", "1")
+    model.prefill(prompt, 0, kv3)
+    np.testing.assert_array_equal(kv3.logits(), kv2.logits())
+    err = float(np.abs(kv1.logits() - kv2.logits()).max())
+    print(f"[model] batched vs token-by-token prefill logits max-abs {err:.3e}", flush=True)
+    assert err <= LOGIT_TOL
+    assert kv1.argmax() == kv2.argmax()
+    n = len(prompt)
+    for which in ("k", "v"):
+        a, b = kv1.layer(1, which, n), kv2.layer(1, which, n)
+        assert float(np.abs(a - b).max()) <= 1e-2 * max(1.0, float(np.abs(b).max()))
+    # Both leave the same device state for decoding on.
+    np.testing.assert_array_equal(model.decode_greedy(n, 8, kv1), model.decode_greedy(n, 8, kv2))
 
 
 def test_model_error_paths(llrs, backend, tmp_path):
