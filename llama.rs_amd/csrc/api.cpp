@@ -64,7 +64,7 @@ static int launch_matvec(llrs_backend *b, const llrs_tensor *w, const float *x, 
   a.cols = (int)w->cols;
   a.x = x;
   a.epi = kEpiStore;
-  return launch_gemv_fast(a, fast_gemv_grid(b->cu_count, a.rows, false), b->stream);
+  return launch_gemv_fast(a, fast_gemv_grid(b->cu_count, a.rows, a.cols, false, 0), b->stream);
 }
 
 // validate_matvec (src/quant.rs:303-318).

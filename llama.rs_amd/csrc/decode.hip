@@ -113,7 +113,8 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
   __shared__ __align__(16) float qs[HD], kn[HD];
 
   const int G = a.nh / a.nkv, kvw = a.nkv * HD;
-  const int h = blockIdx.y, kvh = h / G, chunk = blockIdx.x;
+  // Grid (head, chunk): the low chunks, the ones that run, are dispatched first.
+  const int h = blockIdx.x, kvh = h / G, chunk = blockIdx.y;
   const int pos = bounded_pos(a.pos, a.max_seq);
   const int c0 = chunk * kChunk;
   if (c0 > pos) return;
@@ -252,34 +253,54 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
   prev = __builtin_amdgcn_readfirstlane(prev);
   if (prev != (unsigned)(n_active - 1)) return;
 
-  // 6. Merge (last chunk of the head): the lane's VW dimensions, chunks
-  //    folded with a running max, eight at a time.
+  // 6. Merge (last chunk of the head).  Chunk statistics one per lane (64
+  //    chunks a round): the round's max by wave reduction, each chunk's weight
+  //    exp(m_c - M) in its lane, broadcast by readlane to weight the O
+  //    partials, which are loaded 32 chunks at a time.  Rounds fold with the
+  //    running-max rescaling; a chunk whose max is -inf weighs 0.
   const float *base = a.scratch + (size_t)h * a.max_chunks * a.part_stride;
   const long stride = a.part_stride;
   float M = -INFINITY, L = 0.f, R[VW];
 #pragma unroll
   for (int k = 0; k < VW; k++) R[k] = 0.f;
   const int d0 = (lane % VL) * VW;
-  for (int cb = 0; cb < n_active; cb += 8) {
-    float o[8][VW], mm[8], ll[8];
+  for (int cb = 0; cb < n_active; cb += 64) {
+    const int nc = min(64, n_active - cb);
+    const float *pcl = base + (size_t)(cb + min(lane, nc - 1)) * stride;
+    const float mm = load_dev(pcl + 2 * HD), ll = load_dev(pcl + 2 * HD + 1);
+    const bool in = lane < nc && mm != -INFINITY;
+    float Mr = in ? mm : -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const float *pc = base + (size_t)min(cb + j, n_active - 1) * stride;
+    for (int o = 32; o > 0; o >>= 1) Mr = fmaxf(Mr, __shfl_xor(Mr, o, 64));
+    const float w = in ? expf(mm - Mr) : 0.f;
+    float Lr = w * ll;
 #pragma unroll
-      for (int k = 0; k < VW; k++) o[j][k] = load_dev(pc + d0 + k);
-      mm[j] = load_dev(pc + 2 * HD);
-      ll[j] = load_dev(pc + 2 * HD + 1);
+    for (int o = 32; o > 0; o >>= 1) Lr += __shfl_xor(Lr, o, 64);
+    float Rr[VW];
+#pragma unroll
+    for (int k = 0; k < VW; k++) Rr[k] = 0.f;
+    for (int jb = 0; jb < nc; jb += 32) {
+      float ov[32][VW];
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        const float *pc = base + (size_t)(cb + min(jb + j, nc - 1)) * stride + d0;
+#pragma unroll
+        for (int k = 0; k < VW; k++) ov[j][k] = load_dev(pc + k);
+      }
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        if (jb + j >= nc) break;
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jb + j));
+#pragma unroll
+        for (int k = 0; k < VW; k++) Rr[k] += wj * ov[j][k];
+      }
     }
+    const float Mn = fmaxf(M, Mr);
+    const float sa = expf(M - Mn), sb = expf(Mr - Mn);
+    L = L * sa + Lr * sb;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      if (cb + j >= n_active || mm[j] == -INFINITY) continue;
-      const float Mn = fmaxf(M, mm[j]);
-      const float sa = expf(M - Mn), sb = expf(mm[j] - Mn);
-      L = L * sa + ll[j] * sb;
-#pragma unroll
-      for (int k = 0; k < VW; k++) R[k] = R[k] * sa + o[j][k] * sb;
-      M = Mn;
-    }
+    for (int k = 0; k < VW; k++) R[k] = R[k] * sa + Rr[k] * sb;
+    M = Mn;
   }
   if (lane < VL) {
     if (isfinite(L) && L > 0.f) {
@@ -396,7 +417,7 @@ int launch_attention(const AttnArgs &args, hipStream_t s) {
   if (args.part_stride != attention_part_stride(hd) || args.max_chunks != attention_chunks(args.max_seq))
     return set_error(LLRS_E_INVALID, "attention scratch geometry does not match head_dim %d, context %d",
                      hd, args.max_seq);
-  const dim3 grid((unsigned)args.max_chunks, (unsigned)args.nh);
+  const dim3 grid((unsigned)args.nh, (unsigned)args.max_chunks);
   switch (hd) {
     case 16: hipLaunchKernelGGL(attention_kernel<16>, grid, dim3(64), 0, s, args); break;
     case 32: hipLaunchKernelGGL(attention_kernel<32>, grid, dim3(64), 0, s, args); break;

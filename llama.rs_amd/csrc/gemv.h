@@ -47,6 +47,9 @@ struct FastGemvArgs {
   uint32_t *tok_by_pos;  // max_pos + 1 entries
   uint32_t *next_token;
   int max_pos;           // the context length: positions past it are never written
+  int part;              // rows per partition unit: 4 (0 = default) or 16 with dig_out
+  uint8_t *dig_out;      // when set: the output is also written digitised here
+  const uint8_t *dig_in; // when set: x arrives digitised (x and norm are unused)
 };
 
 bool fast_gemv_supports(uint32_t type, size_t cols);
@@ -54,11 +57,12 @@ bool fast_gemv_supports(uint32_t type, size_t cols);
 // has a tuned instantiation.
 bool fast_gemv_supports_pair(uint32_t ta, uint32_t tb);
 // Dynamic LDS of one workgroup: the digitised activation and its rows' results.
-size_t fast_gemv_lds_bytes(int cols, int rows, int grid);
+size_t fast_gemv_lds_bytes(int cols, int rows, int grid, int part);
+// Bytes of a digitised activation of n elements (dig_out / dig_in).
+inline size_t fast_gemv_digits_size(size_t n) { return 2 * n + (n / 16) * 8; }
 int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s);
-// Workgroups for a launch over `rows` output rows: one per CU (two for the
-// dual gate/up kernel, whose waves hold half the rows), never more than the
-// row quads.
-int fast_gemv_grid(int cu_count, int rows, bool dual);
+// Workgroups for a launch over `rows` x `cols`, never more than the
+// partition units (`part` rows each; 0 = row quads).
+int fast_gemv_grid(int cu_count, int rows, int cols, bool dual, int part);
 
 }  // namespace llrs

@@ -112,8 +112,11 @@ template <> struct Traits<LLRS_Q4_K> {
     // nibbles of scales[g+4] with the top two bits of scales[g-4] / scales[g].
     const int sh = (p & 1) * 16;
     const uint32_t Y = r.hdr.y >> sh, Z = r.hdr.z >> sh, W = r.hdr.w >> sh;
-    const uint32_t sc = p < 2 ? (Y & 0x3f3fu) : ((W & 0x0f0fu) | ((Y >> 2) & 0x3030u));
-    const uint32_t mn = p < 2 ? (Z & 0x3f3fu) : (((W >> 4) & 0x0f0fu) | ((Z >> 2) & 0x3030u));
+    // Both forms, blended by a lane mask (a branch here would run both sides
+    // under exec masking anyway).
+    const uint32_t hi_g = 0u - (uint32_t)(p >> 1);  // all ones for groups >= 4
+    const uint32_t sc = ((Y & 0x3f3fu) & ~hi_g) | (((W & 0x0f0fu) | ((Y >> 2) & 0x3030u)) & hi_g);
+    const uint32_t mn = ((Z & 0x3f3fu) & ~hi_g) | ((((W >> 4) & 0x0f0fu) | ((Z >> 2) & 0x3030u)) & hi_g);
     // Blocks: group 2p = low nibbles of q0 then q1, group 2p+1 = high nibbles.
     const uint32_t m4 = 0x0f0f0f0fu;
     const int a0 = block_dot(r.q0.x & m4, r.q0.y & m4, r.q0.z & m4, r.q0.w & m4, D.g[0]);
@@ -274,6 +277,53 @@ __device__ __forceinline__ float wave_sum4(const float (&v)[4], int lane) {
   return k;
 }
 
+// The two digit planes of one 16-element block, its scale s_b / 128 and the
+// integer sum of X = 128 d1 + d2.
+__device__ __forceinline__ void digit_block(const float (&v)[16], uint4 &d1, uint4 &d2, float &scale,
+                                            int &sum) {
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; j++) m = fmaxf(m, fabsf(v[j]));
+  uint32_t p1[4] = {0, 0, 0, 0}, p2[4] = {0, 0, 0, 0};
+  sum = 0;
+  scale = 0.f;
+  if (m > 0.f) {
+    float is = 127.0f / m;
+    scale = (m / 127.0f) * (1.0f / 128.0f);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      float t = v[j] * is;
+      float a1 = rintf(t);
+      float a2 = rintf((t - a1) * 128.0f);
+      int i1 = (int)a1, i2 = (int)a2;
+      sum += i1 * 128 + i2;
+      p1[j >> 2] |= (uint32_t)(i1 & 0xff) << (8 * (j & 3));
+      p2[j >> 2] |= (uint32_t)(i2 & 0xff) << (8 * (j & 3));
+    }
+  }
+  d1 = make_uint4(p1[0], p1[1], p1[2], p1[3]);
+  d2 = make_uint4(p2[0], p2[1], p2[2], p2[3]);
+}
+
+// An activation digitised by the kernel that produced it (layout of the LDS
+// image below: [2][cols] digit planes, xs[nb], sx[nb], all in slot order),
+// copied to LDS; the per-32 sums follow from xs and sx.
+__device__ void load_digits(const uint8_t *__restrict__ src, int cols, uint8_t *smem) {
+  const int nb = cols >> 4, nb4 = nb >> 2;
+  const int n16 = (2 * cols + 8 * nb) >> 4;  // 16-byte chunks (cols is a multiple of 64)
+  for (int i = threadIdx.x; i < n16; i += blockDim.x)
+    reinterpret_cast<uint4 *>(smem)[i] = reinterpret_cast<const uint4 *>(src)[i];
+  __syncthreads();
+  const float *xs = reinterpret_cast<const float *>(smem + 2 * cols);
+  const int *sx = reinterpret_cast<const int *>(xs + nb);
+  float *xsum32 = reinterpret_cast<float *>(smem + 2 * cols + 8 * nb);
+  for (int g = threadIdx.x; g < (nb >> 1); g += blockDim.x) {
+    const int s0 = slot(2 * g, nb4), s1 = slot(2 * g + 1, nb4);
+    xsum32[g] = xs[s0] * (float)sx[s0] + xs[s1] * (float)sx[s1];
+  }
+  __syncthreads();
+}
+
 // x (times the RMSNorm gain when given) as digits in LDS; returns
 // 1/sqrt(mean(x^2) + eps) with a gain, 1 without.  One pass over x.
 __device__ float digitize(const float *__restrict__ x, const float *__restrict__ gain, float eps,
@@ -302,29 +352,13 @@ __device__ float digitize(const float *__restrict__ x, const float *__restrict__
         v[4 * q] *= g.x; v[4 * q + 1] *= g.y; v[4 * q + 2] *= g.z; v[4 * q + 3] *= g.w;
       }
     }
-    float m = 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; j++) m = fmaxf(m, fabsf(v[j]));
-    uint32_t p1[4] = {0, 0, 0, 0}, p2[4] = {0, 0, 0, 0};
-    int sum = 0;
-    float scale = 0.f;
-    if (m > 0.f) {
-      float is = 127.0f / m;
-      scale = (m / 127.0f) * (1.0f / 128.0f);
-#pragma unroll
-      for (int j = 0; j < 16; j++) {
-        float t = v[j] * is;
-        float a1 = rintf(t);
-        float a2 = rintf((t - a1) * 128.0f);
-        int i1 = (int)a1, i2 = (int)a2;
-        sum += i1 * 128 + i2;
-        p1[j >> 2] |= (uint32_t)(i1 & 0xff) << (8 * (j & 3));
-        p2[j >> 2] |= (uint32_t)(i2 & 0xff) << (8 * (j & 3));
-      }
-    }
+    uint4 d1, d2;
+    float scale;
+    int sum;
+    digit_block(v, d1, d2, scale, sum);
     int s = slot(b, nb4);
-    *reinterpret_cast<uint4 *>(dig + s * 16) = make_uint4(p1[0], p1[1], p1[2], p1[3]);
-    *reinterpret_cast<uint4 *>(dig + cols + s * 16) = make_uint4(p2[0], p2[1], p2[2], p2[3]);
+    *reinterpret_cast<uint4 *>(dig + s * 16) = d1;
+    *reinterpret_cast<uint4 *>(dig + cols + s * 16) = d2;
     xs[s] = scale;
     sx[s] = sum;
     float part = scale * (float)sum;
@@ -380,18 +414,18 @@ struct SegStream {
   int row_lo, row_hi, first, stride, units, iters, steps, lane;
   typename T::Raw cur[R], nxt[R], cu[DUAL ? R : 1], nu[DUAL ? R : 1];
 
-  __device__ __forceinline__ int rowof(int step, int i) const {
-    return row_lo + (first + (step / iters) * stride) * R + i;
-  }
+  // First row of this wave's g-th row group.
+  __device__ __forceinline__ int group_row(int g) const { return row_lo + (first + g * stride) * R; }
   // Loads are branch-free (indices past the segment are clamped onto its last
   // row and unit and their products discarded), so the compiler can count the
   // outstanding loads statically and wait only for the current step's.
-  __device__ __forceinline__ void load(int step, typename T::Raw (&dst)[R],
+  __device__ __forceinline__ void load(int g, int it, typename T::Raw (&dst)[R],
                                        typename T::Raw (&dstu)[DUAL ? R : 1]) {
-    const int u = min((step % iters) * 64 + lane, units - 1);
+    const int u = min(it * 64 + lane, units - 1);
+    const int r0 = group_row(g);
 #pragma unroll
     for (int i = 0; i < R; i++) {
-      const int r = min(rowof(step, i), row_hi - 1) - row_lo;
+      const int r = min(r0 + i, row_hi - 1) - row_lo;
       T::load(S.w + (size_t)r * S.row_bytes, u, dst[i]);
       if constexpr (DUAL) T::load(U.w + (size_t)r * U.row_bytes, u, dstu[i]);
     }
@@ -410,7 +444,7 @@ struct SegStream {
     const int ngroups = (row_hi - row_lo + R - 1) / R;
     int nmine = first < ngroups ? (ngroups - first + stride - 1) / stride : 0;
     steps = __builtin_amdgcn_readfirstlane(nmine) * iters;
-    if (steps > 0) load(0, cur, cu);
+    if (steps > 0) load(0, 0, cur, cu);
   }
   template <class Emit>
   __device__ __forceinline__ void run(const Lds &L, Emit &&emit);
@@ -424,16 +458,23 @@ __device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&em
   float acc[R], acc2[R];
 #pragma unroll
   for (int i = 0; i < R; i++) acc[i] = acc2[i] = 0.f;
+  int g = 0, it = 0;  // the current step's row group and unit iteration
   // One step on buffers (c, cu_) while the next step's loads go to (n, nu_).
-  auto step = [&](int s, Raw (&c)[R], Raw (&cu_)[RU], Raw (&n)[R], Raw (&nu_)[RU]) {
-    load(s + 1, n, nu_);  // past the last step: a clamped, unused reload
-    const int u0 = (s % iters) * 64 + lane;
+  auto step = [&](Raw (&c)[R], Raw (&cu_)[RU], Raw (&n)[R], Raw (&nu_)[RU]) {
+    int gn = g, itn = it + 1;
+    if (itn == iters) {
+      itn = 0;
+      gn = g + 1;
+    }
+    load(gn, itn, n, nu_);  // past the last step: a clamped, unused reload
+    const int u0 = it * 64 + lane;
     const int u = min(u0, units - 1);
+    const int r0 = group_row(g);
     typename T::Dig D;
     T::digits(L, u, D);
 #pragma unroll
     for (int i = 0; i < R; i++) {
-      const bool live = u0 < units && rowof(s, i) < row_hi;
+      const bool live = u0 < units && r0 + i < row_hi;
       float d = T::dot(c[i], u, D);
       acc[i] += live ? d : 0.f;
       if constexpr (DUAL) {
@@ -441,38 +482,40 @@ __device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&em
         acc2[i] += live ? d2 : 0.f;
       }
     }
-    if (s % iters == iters - 1) {
+    if (itn == 0) {  // the row group is complete
       if constexpr (DUAL) {
         // rows 0, 1 of gate and of up: gate sums land in lanes 0/16, up in 32/48.
         float v[4] = {acc[0], acc[1], acc2[0], acc2[1]};
         float t = wave_sum4(v, lane);
         float up = __shfl_xor(t, 32, 64);
         if ((lane & 47) == 0) {  // lanes 0 and 16
-          int r = rowof(s, (lane >> 4) & 1);
+          int r = r0 + ((lane >> 4) & 1);
           if (r < row_hi) emit(r - row_lo, t, up);
         }
       } else if constexpr (R == 4) {
         float t = wave_sum4(acc, lane);
         if ((lane & 15) == 0) {
-          int r = rowof(s, ((lane >> 5) << 1) | ((lane >> 4) & 1));
+          int r = r0 + (((lane >> 5) << 1) | ((lane >> 4) & 1));
           if (r < row_hi) emit(r - row_lo, t, 0.f);
         }
       } else {
         float t = wave_sum2(acc[0], acc[1], lane);
         if ((lane & 31) == 0) {
-          int r = rowof(s, lane >> 5);
+          int r = r0 + (lane >> 5);
           if (r < row_hi) emit(r - row_lo, t, 0.f);
         }
       }
 #pragma unroll
       for (int i = 0; i < R; i++) acc[i] = acc2[i] = 0.f;
     }
+    g = gn;
+    it = itn;
   };
   // Unrolled by two with the buffers swapping roles: no register copies, so
   // the in-flight loads never have to be waited for early.
   for (int s = 0; s < steps; s += 2) {
-    step(s, cur, cu, nxt, nu);
-    if (s + 1 < steps) step(s + 1, nxt, nu, cur, cu);
+    step(cur, cu, nxt, nu);
+    if (s + 1 < steps) step(nxt, nu, cur, cu);
   }
 }
 
@@ -484,13 +527,16 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
   __shared__ float red[16];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
-  // Whole row quads per workgroup (segment row counts are multiples of 4).
-  const int quads = (a.rows + kR - 1) / kR;
-  const int wq0 = (int)((long)blockIdx.x * quads / gridDim.x);
-  const int wq1 = (int)((long)(blockIdx.x + 1) * quads / gridDim.x);
+  // Whole partition units (row quads, or 16-row blocks when the output is
+  // digitised here) per workgroup; segment row counts are multiples of 4.
+  const int part = a.part ? a.part : kR;
+  const int nunits = (a.rows + part - 1) / part;
+  const int wq0 = (int)((long)blockIdx.x * nunits / gridDim.x);
+  const int wq1 = (int)((long)(blockIdx.x + 1) * nunits / gridDim.x);
+  const int wrow0 = wq0 * part, wrow1 = min(wq1 * part, a.rows);
   auto seg_range = [&](int s, int base, int &lo, int &hi) {
-    lo = max(wq0 * kR, base);
-    hi = min(min(wq1 * kR, a.rows), base + a.seg[s].rows);
+    lo = max(wrow0, base);
+    hi = min(wrow1, base + a.seg[s].rows);
   };
   auto shifted = [](FastSeg X, int rows) {
     X.w += (size_t)rows * X.row_bytes;
@@ -500,7 +546,7 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
   // The workgroup's first segment; when it streams with type TA its first
   // weight loads are issued now, so HBM latency overlaps the prologue.
   int s0 = 0, base0 = 0;
-  while (s0 + 1 < a.nseg && wq0 * kR >= base0 + a.seg[s0].rows) base0 += a.seg[s0++].rows;
+  while (s0 + 1 < a.nseg && wrow0 >= base0 + a.seg[s0].rows) base0 += a.seg[s0++].rows;
   const bool s0_is_ta = DUAL || TA == TB || s0 + 1 < a.nseg;
   SegStream<TA, DUAL> A;
   if (s0_is_ta) {
@@ -511,7 +557,11 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
     A.begin(Sw, Uw, lo, max(lo, hi), wave, nw, a.cols, lane);
   }
 
-  const float inv = digitize(a.x, a.norm, a.eps, a.cols, smem, red);
+  float inv = 1.0f;
+  if (a.dig_in)
+    load_digits(a.dig_in, a.cols, smem);
+  else
+    inv = digitize(a.x, a.norm, a.eps, a.cols, smem, red);
   Lds L;
   L.cols = a.cols;
   L.nb4 = a.cols >> 6;
@@ -523,7 +573,6 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
   // Row results wait in LDS (x inv_rms, SiLU(gate)*up applied) until the
   // streaming is over, so no epilogue memory access stalls the weight loads.
   float *ybuf = reinterpret_cast<float *>(smem + fast_gemv_digit_bytes(a.cols));
-  const int wrow0 = wq0 * kR;
   auto emitter = [&](int lo) {
     return [&, lo](int r, float v, float v2) {
       v *= inv;
@@ -566,7 +615,6 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
 
   // Epilogue over the workgroup's rows, coalesced.
   unsigned long long best = 0;
-  const int wrow1 = min(wq1 * kR, a.rows);
   for (int g = wrow0 + (int)threadIdx.x; g < wrow1; g += blockDim.x) {
     int s = 0, rs = g;
     while (s + 1 < a.nseg && rs >= a.seg[s].rows) rs -= a.seg[s++].rows;
@@ -581,6 +629,26 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
         unsigned long long key = ((unsigned long long)total_order_key(v) << 32) | (uint32_t)rs;
         best = key > best ? key : best;
       }
+    }
+  }
+  if (a.dig_out) {
+    // The consumer's activation, digitised once here: this workgroup owns
+    // whole 16-row blocks of the output (part == 16).
+    __syncthreads();
+    const int nb = a.rows >> 4, nb4 = nb >> 2, b0 = wrow0 >> 4;
+    for (int t = threadIdx.x; t < ((wrow1 - wrow0) >> 4); t += blockDim.x) {
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 16; j++) v[j] = ybuf[16 * t + j];
+      uint4 d1, d2;
+      float scale;
+      int sum;
+      digit_block(v, d1, d2, scale, sum);
+      const int sl = slot(b0 + t, nb4);
+      *reinterpret_cast<uint4 *>(a.dig_out + sl * 16) = d1;
+      *reinterpret_cast<uint4 *>(a.dig_out + a.rows + sl * 16) = d2;
+      reinterpret_cast<float *>(a.dig_out + 2 * a.rows)[sl] = scale;
+      reinterpret_cast<int *>(a.dig_out + 2 * a.rows + 4 * nb)[sl] = sum;
     }
   }
   if (a.epi == kEpiLogits) {
@@ -615,9 +683,10 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
   }
 }
 
-size_t fast_gemv_lds_bytes(int cols, int rows, int grid) {
-  const size_t quads = ((size_t)rows + kR - 1) / kR;
-  const size_t rows_per_wg = (quads + grid - 1) / grid * kR;
+size_t fast_gemv_lds_bytes(int cols, int rows, int grid, int part) {
+  if (part <= 0) part = kR;
+  const size_t units = ((size_t)rows + part - 1) / part;
+  const size_t rows_per_wg = (units + grid - 1) / grid * part;
   return fast_gemv_digit_bytes(cols) + rows_per_wg * sizeof(float);
 }
 
@@ -637,7 +706,11 @@ static void launch_one(const FastGemvArgs &args, int grid, size_t lds, hipStream
 
 int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
   if (grid <= 0) return set_error(LLRS_E_INVALID, "GEMV grid must be positive");
-  size_t lds = fast_gemv_lds_bytes(args.cols, args.rows, grid);
+  if (args.dig_out && (args.part != 16 || args.rows % 64))
+    return set_error(LLRS_E_INVALID, "a digitised output needs 16-row partitions of a multiple of 64 rows");
+  if (args.part && args.part != kR && args.part != 16)
+    return set_error(LLRS_E_INVALID, "GEMV partition of %d rows is not supported", args.part);
+  size_t lds = fast_gemv_lds_bytes(args.cols, args.rows, grid, args.part);
   if (lds > kMaxLds) return set_error(LLRS_E_UNSUPPORTED, "GEMV needs %zu bytes of LDS (cols %d, rows %d, grid %d)", lds, args.cols, args.rows, grid);
   uint32_t ta = args.seg[0].type, tb = args.seg[args.nseg - 1].type;
   for (int i = 0; i + 1 < args.nseg; i++)
@@ -667,9 +740,14 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
   return set_error(LLRS_E_UNSUPPORTED, "no tuned GEMV for %s + %s", type_name(ta), type_name(tb));
 }
 
-int fast_gemv_grid(int cu_count, int rows, bool dual) {
-  const int g = (dual ? 2 : 1) * cu_count, quads = (rows + kR - 1) / kR;
-  return quads < g ? quads : g;
+int fast_gemv_grid(int cu_count, int rows, int cols, bool dual, int part) {
+  // Measured on the decode shapes: one workgroup per CU for rows of <= 8K
+  // columns, two for longer rows (more loads in flight per row), three for the
+  // dual gate/up kernel.
+  const int per_cu = dual ? 3 : (cols > 8192 ? 2 : 1);
+  if (part <= 0) part = kR;
+  const int g = per_cu * cu_count, units = (rows + part - 1) / part;
+  return units < g ? units : g;
 }
 
 bool fast_gemv_supports_pair(uint32_t ta, uint32_t tb) {

@@ -69,6 +69,7 @@ struct llrs_kv {
   uint32_t *tok_by_pos = nullptr, *next_token = nullptr;
   unsigned long long *amax_key = nullptr;  // LM-head argmax accumulator (zero between steps)
   unsigned *done = nullptr;                // LM-head block completion counter
+  uint8_t *act_dig = nullptr;              // SiLU*up digitised by gate/up for ffn_down
   uint32_t *pinned = nullptr;  // host staging, max_seq_len + 2 words
   hipGraph_t graph[2] = {nullptr, nullptr};
   hipGraphExec_t exec[2] = {nullptr, nullptr};
@@ -348,8 +349,8 @@ static bool use_fast(llrs_model *m, size_t l, int which) {
   }
 }
 
-static int fast_grid(llrs_model *m, int rows, bool dual = false) {
-  return fast_gemv_grid(m->b->cu_count, rows, dual);
+static int fast_grid(llrs_model *m, const FastGemvArgs &a, bool dual = false) {
+  return fast_gemv_grid(m->b->cu_count, a.rows, a.cols, dual, a.part);
 }
 
 static FastSeg seg_of(const llrs_tensor *t, const float *bias, float *out) {
@@ -392,7 +393,7 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
     a.tok_by_pos = kv->tok_by_pos;
     a.next_token = kv->next_token;
     a.max_pos = (int)kv->max_seq_len;
-    return launch_gemv_fast(a, fast_grid(m, a.rows), s);
+    return launch_gemv_fast(a, fast_grid(m, a), s);
   }
   DevLayer &L = m->layers[l];
   switch (which) {
@@ -410,7 +411,7 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
       a.rows = (int)(L.q->rows + L.k->rows + L.v->rows);
       a.norm = L.attn_norm;
       a.epi = kEpiStore;
-      return launch_gemv_fast(a, fast_grid(m, a.rows), s);
+      return launch_gemv_fast(a, fast_grid(m, a), s);
     case P_O:
       if (!fast) return launch_gemv_generic(L.o, kv->attn, kv->residual, nullptr, true, s);
       a.seg[0] = seg_of(L.o, nullptr, kv->residual);
@@ -418,7 +419,7 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
       a.rows = H;
       a.x = kv->attn;
       a.epi = kEpiAdd;
-      return launch_gemv_fast(a, fast_grid(m, a.rows), s);
+      return launch_gemv_fast(a, fast_grid(m, a), s);
     case P_GATE_UP:
       if (!fast) {
         LLRS_TRY(launch_rmsnorm(kv->residual, L.ffn_norm, kv->hidden, H, eps, s));
@@ -433,7 +434,12 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
       a.rows = F;
       a.norm = L.ffn_norm;
       a.epi = kEpiSwiGlu;
-      return launch_gemv_fast(a, fast_grid(m, a.rows, true), s);
+      if (use_fast(m, l, P_DOWN) && F % 64 == 0) {
+        // SiLU*up leaves digitised for ffn_down: workgroups own 16-row blocks.
+        a.part = 16;
+        a.dig_out = kv->act_dig;
+      }
+      return launch_gemv_fast(a, fast_grid(m, a, true), s);
     case P_DOWN:
       if (!fast) return launch_gemv_generic(L.down, kv->act, kv->residual, nullptr, true, s);
       a.seg[0] = seg_of(L.down, nullptr, kv->residual);
@@ -442,7 +448,8 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
       a.cols = F;
       a.x = kv->act;
       a.epi = kEpiAdd;
-      return launch_gemv_fast(a, fast_grid(m, a.rows), s);
+      if (use_fast(m, l, P_GATE_UP) && F % 64 == 0) a.dig_in = kv->act_dig;
+      return launch_gemv_fast(a, fast_grid(m, a), s);
     default: return set_error(LLRS_E_INVALID, "unknown projection %d", which);
   }
 }
@@ -576,7 +583,8 @@ static int kv_create_impl(llrs_model *m, size_t max_seq, llrs_kv **out) {
       (rc = A((void **)&kv->attn_counters, 4 * c.num_attention_heads + 64)) ||
       (rc = A((void **)&kv->rope, max_seq * c.head_dim * 4)) || (rc = A((void **)&kv->pos, 64)) ||
       (rc = A((void **)&kv->tok_by_pos, (max_seq + 1) * 4)) || (rc = A((void **)&kv->next_token, 64)) ||
-      (rc = A((void **)&kv->amax_key, 64)) || (rc = A((void **)&kv->done, 64))) {
+      (rc = A((void **)&kv->amax_key, 64)) || (rc = A((void **)&kv->done, 64)) ||
+      (rc = A((void **)&kv->act_dig, fast_gemv_digits_size(F)))) {
     free_kv(kv);
     return rc;
   }
@@ -599,6 +607,7 @@ static int kv_create_impl(llrs_model *m, size_t max_seq, llrs_kv **out) {
   if (e == hipSuccess) e = hipMemsetAsync(kv->pos, 0, 64, s);
   if (e == hipSuccess) e = hipMemsetAsync(kv->amax_key, 0, 64, s);
   if (e == hipSuccess) e = hipMemsetAsync(kv->done, 0, 64, s);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->act_dig, 0, fast_gemv_digits_size(F), s);
   if (e == hipSuccess) e = hipMemsetAsync(kv->attn_counters, 0, 4 * c.num_attention_heads + 64, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) {
