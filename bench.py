@@ -117,8 +117,14 @@ def projection_only(llrs, be, model, which: str, iters: int) -> int:
     """One projection's launches (every layer, `iters` times) plus a known-size
     device copy, so that rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of the GEMV
     kernel can be scaled by what the same counter reads for the copy."""
-    kv = llrs.KVCache(model, 64)
-    us, nb = model.profile_projection(kv, which, iters)
+    if which == "layers":
+        # The persistent kernel at a decode-like position (520 cached rows).
+        kv = llrs.KVCache(model, 1024)
+        model.prefill(np.arange(520, dtype=np.uint32) * 7 % model.config().vocab_size, 0, kv)
+        us, nb = model.profile_layers(kv, iters)
+    else:
+        kv = llrs.KVCache(model, 64)
+        us, nb = model.profile_projection(kv, which, iters)
     lib = llrs.lib()
     import ctypes as C
     src, dst = C.c_void_p(), C.c_void_p()
@@ -158,7 +164,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-iters", type=int, default=5)
-    ap.add_argument("--projection-only", choices=["qkv", "o", "gate_up", "down", "lm_head"],
+    ap.add_argument("--projection-only", choices=["qkv", "o", "gate_up", "down", "lm_head", "layers"],
                     help="only time this projection's launches over all layers and run the "
                          "calibration copy (the workload of the rocprofv3 --pmc traffic runs)")
     args = ap.parse_args()
@@ -223,12 +229,30 @@ def main() -> int:
         per[which] = {"avg_us": round(us, 2), "bytes": nb, "gbs": round(nb / us / 1e3, 1),
                       "us_per_token": round(us * launches, 1)}
         log(f"  {which:8s} {us:8.2f} us/launch  {nb / 1e6:8.2f} MB  {nb / us / 1e3:7.1f} GB/s")
-    dom = max(per, key=lambda k: per[k]["us_per_token"])
-    d = per[dom]
-    achieved = d["bytes"] / d["avg_us"] / 1e3
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": profiled_traffic(dom),
-                "kernel": f"{dom} projection GEMV ({d['bytes']} algorithmic weight bytes/launch)"}
+    if kv.persistent:
+        # The dominant kernel is the persistent one (every layer in one launch):
+        # weights of all layers plus the KV rows its attention reads and writes.
+        pos_now = pos0 + args.steps
+        us, wb = model.profile_layers(kv, args.profile_iters)
+        kvb = kv_bytes_per_token(mc, pos_now)
+        per["layers"] = {"avg_us": round(us, 2), "bytes": wb + kvb,
+                         "gbs": round((wb + kvb) / us / 1e3, 1), "us_per_token": round(us, 1)}
+        log(f"  layers   {us:8.2f} us/launch  {(wb + kvb) / 1e6:8.2f} MB  {(wb + kvb) / us / 1e3:7.1f} GB/s "
+            f"(persistent kernel, position {pos_now})")
+        achieved = (wb + kvb) / us / 1e3
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                    "traffic": profiled_traffic("decode_persistent_kernel"),
+                    "kernel": f"decode_persistent_kernel: all {mc.num_hidden_layers} layers in one "
+                              f"launch ({wb} weight bytes + {kvb} KV bytes at position {pos_now})"}
+    else:
+        dom = max(per, key=lambda k: per[k]["us_per_token"])
+        d = per[dom]
+        achieved = d["bytes"] / d["avg_us"] / 1e3
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                    "traffic": profiled_traffic(dom),
+                    "kernel": f"{dom} projection GEMV ({d['bytes']} algorithmic weight bytes/launch)"}
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -171,6 +171,12 @@ int llrs_kv_create(llrs_model *m, size_t max_seq_len, llrs_kv **out);
 void llrs_kv_free(llrs_kv *kv);
 /* KVCache::reset (src/cache.rs:55-57): a no-op, positions are overwritten before read. */
 int llrs_kv_reset(llrs_kv *kv);
+/* Which implementation runs this state's decode steps: 1 = one persistent
+ * launch for all layers (chosen at llrs_kv_create when the model's weight
+ * types and head_dim have an instantiation and LLRS_NO_PERSISTENT is unset),
+ * 0 = one launch per phase.  Both compute the same values.  No counterpart
+ * in the reference (its decode step has one implementation). */
+int llrs_kv_decode_path(const llrs_kv *kv);
 
 /* CausalModel::forward_token (src/architecture.rs:47-54; src/model.rs:135-271).
  * Fails if token >= vocab or pos >= max_seq_len (src/model.rs:145-153). */
@@ -194,11 +200,13 @@ int llrs_read_kv(llrs_kv *kv, size_t layer, int which /*0 = K, 1 = V*/, float *o
  * src/bin/llama-bench.rs:117-126): times the decode step's launch(es) for one
  * projection group with HIP events on the backend's stream.  `which`: 0 q/k/v
  * (RMSNorm fused), 1 o (+ residual), 2 gate/up (RMSNorm + SiLU*up fused),
- * 3 down (+ residual), 4 LM head (RMSNorm + argmax fused).  The layer groups
- * rotate over every layer so each launch streams its own weights; the LM
- * head is one matrix.  Runs `iters` rounds and restores the position;
- * returns the mean launch time in microseconds and the weight bytes one
- * launch reads. */
+ * 3 down (+ residual), 4 LM head (RMSNorm + argmax fused), 5 every layer of
+ * the step (the persistent kernel when llrs_kv_decode_path is 1, else the
+ * per-phase launches; the embedding runs untimed before each round).  The
+ * layer groups rotate over every layer so each launch streams its own
+ * weights; the LM head is one matrix.  Runs `iters` rounds and restores the
+ * position; returns the mean launch (5: round) time in microseconds and the
+ * weight bytes one launch reads. */
 int llrs_profile_projection(llrs_model *m, llrs_kv *kv, int which, int iters, double *avg_us,
                             size_t *bytes_per_launch);
 

@@ -113,6 +113,7 @@ SIGNATURES = [
     ("llrs_kv_create", C.c_int, [P, SZ, C.POINTER(P)]),
     ("llrs_kv_free", None, [P]),
     ("llrs_kv_reset", C.c_int, [P]),
+    ("llrs_kv_decode_path", C.c_int, [P]),
     ("llrs_forward_token", C.c_int, [P, P, C.c_uint32, SZ, C.c_int]),
     ("llrs_prefill", C.c_int, [P, P, U32P, SZ, SZ]),
     ("llrs_decode_greedy", C.c_int, [P, P, SZ, SZ, U32P]),

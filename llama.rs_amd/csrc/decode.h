@@ -22,8 +22,9 @@ struct AttnArgs {
   float scale;               // 1/sqrt(hd)
 };
 
+// Also zeroes clear[0 .. nclear) (the persistent kernel's barrier counters).
 int launch_embed(const llrs_tensor *emb, const uint32_t *tok_by_pos, const int *pos, int max_seq,
-                 float *out, hipStream_t s);
+                 float *out, hipStream_t s, unsigned *clear = nullptr, int nclear = 0);
 int launch_rmsnorm(const float *in, const float *w, float *out, int n, float eps, hipStream_t s);
 long attention_part_stride(int hd);
 size_t attention_scratch_floats(int nh, int hd, int max_seq);

@@ -13,6 +13,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "attention_dev.h"
 #include "decode.h"
 #include "quant_dev.h"
 
@@ -41,16 +42,14 @@ __device__ float block_sum(float v, float *sh) {
   return t;
 }
 
-__device__ __forceinline__ int bounded_pos(const int *pos, int max_seq) {
-  int p = *pos;
-  return p < 0 ? 0 : p >= max_seq ? max_seq - 1 : p;
-}
 
 // embed_tokens.row_into(token) (src/model.rs:170-171): bit-exact dequant.
 __global__ void embed_kernel(const uint8_t *__restrict__ emb, uint32_t ty, size_t row_bytes, int H,
                              uint32_t vocab, const uint32_t *__restrict__ tok_by_pos,
-                             const int *__restrict__ pos, int max_seq, float *__restrict__ out) {
+                             const int *__restrict__ pos, int max_seq, float *__restrict__ out,
+                             unsigned *__restrict__ clear, int nclear) {
   int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c < nclear) clear[c] = 0u;  // the step's barrier counters start at zero
   if (c >= H) return;
   uint32_t tok = tok_by_pos[bounded_pos(pos, max_seq)];
   if (tok >= vocab) tok = vocab - 1;  // tokens are validated on the host; never read past the table
@@ -70,254 +69,11 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *__restrict__
   for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = in[i] * (inv * w[i]);
 }
 
-// ------------------------------------------------------------------ attention
-//
-// One wave per (query head, chunk of kChunk positions); chunks past the
-// current position exit at once, so one grid (sized for the whole context)
-// serves every position of a captured graph.  Per chunk: split-half RoPE
-// (src/model.rs:87-95) on the head's query, scores q.k * 1/sqrt(hd), softmax
-// partials (max, sum of exp) and exp-weighted V sums (src/model.rs:206-231,
-// softmax_inplace 298-313).  The chunk holding the current position also
-// rotates the new key, and the group's first head appends key and value to
-// the cache (KVCache::update, src/cache.rs:38-53).
-//
-// Decode attention moves a few MB per layer, so latency bounds it: each wave
-// issues all its K and V loads first, works without workgroup barriers, and
-// the chunks of a head meet through device-scope atomics only.  Partials are
-// stored write-through (device-scope relaxed atomic stores), the wave waits
-// for them to complete, then bumps the head's counter; the last chunk reads
-// them back with device-scope loads and folds them with the running-max
-// rescaling of flash decoding.  No cache write-back fence is needed.  A chunk
-// whose scores are all -inf contributes exp(-inf) = 0; without a finite
-// positive total the weights fall back to uniform, as softmax_inplace does.
-
-constexpr int kChunk = 32;  // positions per wave: lane = (half of the head, position)
-
-__device__ __forceinline__ void store_dev(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_dev(const float *p) {
-  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <int HD>
 __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
-  constexpr int KH = HD / 2;              // dimensions per score lane
-  constexpr int NK4 = KH / 4;             // their float4s
-  constexpr int VW = HD >= 64 ? HD / 64 : 1;  // V floats per lane
-  constexpr int VL = HD / VW;             // lanes covering one V row
-  constexpr int RV = 64 / VL;             // V rows per load instruction
-  constexpr int NVI = kChunk / RV;        // V load instructions
-  static_assert(NK4 >= 1 && VW <= 2 && RV * VL == 64, "head_dim must be 16..128");
-  using VT = typename std::conditional<VW == 2, float2, float>::type;
   __shared__ __align__(16) float qs[HD], kn[HD];
-
-  const int G = a.nh / a.nkv, kvw = a.nkv * HD;
   // Grid (head, chunk): the low chunks, the ones that run, are dispatched first.
-  const int h = blockIdx.x, kvh = h / G, chunk = blockIdx.y;
-  const int pos = bounded_pos(a.pos, a.max_seq);
-  const int c0 = chunk * kChunk;
-  if (c0 > pos) return;
-  const int n_active = pos / kChunk + 1;
-  const int c1 = min(c0 + kChunk, pos + 1);  // exclusive
-  const bool owns_new = pos < c1;
-  const int lane = threadIdx.x, half = lane >> 5, pl = lane & 31;
-  const float *kc = a.k_cache + (size_t)kvh * HD, *vc = a.v_cache + (size_t)kvh * HD;
-
-  // 1. Loads, all issued up front: this lane's query and new-key pair
-  //    (i, i + KH) with its RoPE factors and its dimensions of the new value;
-  //    then the chunk's keys (lane = half x position, KH dims) and values
-  //    (lane = VW consecutive dims of row lane / VL, RV rows per load).  Rows
-  //    past the chunk's end are clamped onto its first row and masked later.
-  const int ri = lane & (KH - 1);
-  const float *cs = a.rope + (size_t)pos * HD, *sn = cs + KH;
-  const float *qx = a.q + (size_t)h * HD, *kx = a.k + kvh * HD, *vx = a.v + kvh * HD;
-  const float q_re = qx[ri], q_im = qx[ri + KH], k_re = kx[ri], k_im = kx[ri + KH];
-  const float rc = cs[ri], rs = sn[ri];
-  const int vd = (lane % VL) * VW, vr0 = lane / VL;
-  const VT vnew = *reinterpret_cast<const VT *>(vx + vd);
-  float4 kr[NK4];
-  {
-    const float *kp = kc + (size_t)(c0 + pl < c1 ? c0 + pl : c0) * kvw + half * KH;
-#pragma unroll
-    for (int j = 0; j < NK4; j++) kr[j] = *reinterpret_cast<const float4 *>(kp + 4 * j);
-  }
-  VT vv[NVI];
-#pragma unroll
-  for (int i = 0; i < NVI; i++) {
-    const int p = c0 + i * RV + vr0;
-    vv[i] = *reinterpret_cast<const VT *>(vc + (size_t)(p < c1 ? p : c0) * kvw + vd);
-  }
-
-  // 2. Rotated query and new key in LDS; the group's first head appends the
-  //    new key and value to the cache.
-  if (lane < KH) {
-    qs[ri] = q_re * rc - q_im * rs;
-    qs[ri + KH] = q_re * rs + q_im * rc;
-    const float r0 = k_re * rc - k_im * rs, r1 = k_re * rs + k_im * rc;
-    kn[ri] = r0;
-    kn[ri + KH] = r1;
-    if (owns_new && h % G == 0) {
-      float *krow = a.k_cache + (size_t)pos * kvw + kvh * HD;
-      krow[ri] = r0;
-      krow[ri + KH] = r1;
-    }
-  }
-  if (owns_new && h % G == 0 && lane < VL)
-    *reinterpret_cast<VT *>(a.v_cache + (size_t)pos * kvw + kvh * HD + vd) = vnew;
-  __syncthreads();  // one wave: orders the LDS writes before the reads below
-  if (owns_new) {
-    if (c0 + pl == pos) {
-#pragma unroll
-      for (int j = 0; j < NK4; j++) kr[j] = *reinterpret_cast<const float4 *>(kn + half * KH + 4 * j);
-    }
-#pragma unroll
-    for (int i = 0; i < NVI; i++)
-      if (c0 + i * RV + vr0 == pos) vv[i] = vnew;
-  }
-
-  // 3. Score of position pl (both halves end with the full dot), softmax partials.
-  float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < NK4; j++) {
-    const float4 q4 = *reinterpret_cast<const float4 *>(qs + half * KH + 4 * j);
-    s += q4.x * kr[j].x + q4.y * kr[j].y + q4.z * kr[j].z + q4.w * kr[j].w;
-  }
-  s += __shfl_xor(s, 32, 64);
-  const bool valid = c0 + pl < c1;
-  s = valid ? s * a.scale : -INFINITY;
-  float m = s;
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  const float x = valid ? expf(s - m) : 0.f;
-  float l = x;
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-
-  // 4. Exp-weighted and plain V sums of the lane's VW dimensions.
-  float O[VW], Vs[VW];
-#pragma unroll
-  for (int k = 0; k < VW; k++) O[k] = Vs[k] = 0.f;
-#pragma unroll
-  for (int i = 0; i < NVI; i++) {
-    const int p = i * RV + vr0;  // position within the chunk
-    float wp;  // exp weight of position p, held by lane p
-    if constexpr (RV == 1)
-      wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i));
-    else
-      wp = __shfl(x, p, 64);
-    const float in = c0 + p < c1 ? 1.f : 0.f;
-    const float *e = reinterpret_cast<const float *>(&vv[i]);
-#pragma unroll
-    for (int k = 0; k < VW; k++) {
-      O[k] += wp * e[k];
-      Vs[k] += in * e[k];
-    }
-  }
-#pragma unroll
-  for (int o = VL; o < 64; o <<= 1) {
-#pragma unroll
-    for (int k = 0; k < VW; k++) {
-      O[k] += __shfl_xor(O[k], o, 64);
-      Vs[k] += __shfl_xor(Vs[k], o, 64);
-    }
-  }
-
-  float *out = a.out + (size_t)h * HD;
-  if (n_active == 1) {  // the only chunk: finish here
-    if (lane < VL) {
-      const bool ok = isfinite(l) && l > 0.f;
-#pragma unroll
-      for (int k = 0; k < VW; k++) out[vd + k] = ok ? O[k] / l : Vs[k] / (float)(pos + 1);
-    }
-    return;
-  }
-
-  // 5. Publish the partial: [HD] O sums, [HD] V sums, max, sum.
-  float *part = a.scratch + ((size_t)h * a.max_chunks + chunk) * a.part_stride;
-  if (lane < VL) {
-#pragma unroll
-    for (int k = 0; k < VW; k++) {
-      store_dev(part + vd + k, O[k]);
-      store_dev(part + HD + vd + k, Vs[k]);
-    }
-  }
-  if (lane == 0) {
-    store_dev(part + 2 * HD, m);
-    store_dev(part + 2 * HD + 1, l);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial is written through
-  unsigned prev = 0;
-  if (lane == 0)
-    prev = __hip_atomic_fetch_add(a.counters + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  prev = __builtin_amdgcn_readfirstlane(prev);
-  if (prev != (unsigned)(n_active - 1)) return;
-
-  // 6. Merge (last chunk of the head).  Chunk statistics one per lane (64
-  //    chunks a round): the round's max by wave reduction, each chunk's weight
-  //    exp(m_c - M) in its lane, broadcast by readlane to weight the O
-  //    partials, which are loaded 32 chunks at a time.  Rounds fold with the
-  //    running-max rescaling; a chunk whose max is -inf weighs 0.
-  const float *base = a.scratch + (size_t)h * a.max_chunks * a.part_stride;
-  const long stride = a.part_stride;
-  float M = -INFINITY, L = 0.f, R[VW];
-#pragma unroll
-  for (int k = 0; k < VW; k++) R[k] = 0.f;
-  const int d0 = (lane % VL) * VW;
-  for (int cb = 0; cb < n_active; cb += 64) {
-    const int nc = min(64, n_active - cb);
-    const float *pcl = base + (size_t)(cb + min(lane, nc - 1)) * stride;
-    const float mm = load_dev(pcl + 2 * HD), ll = load_dev(pcl + 2 * HD + 1);
-    const bool in = lane < nc && mm != -INFINITY;
-    float Mr = in ? mm : -INFINITY;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) Mr = fmaxf(Mr, __shfl_xor(Mr, o, 64));
-    const float w = in ? expf(mm - Mr) : 0.f;
-    float Lr = w * ll;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) Lr += __shfl_xor(Lr, o, 64);
-    float Rr[VW];
-#pragma unroll
-    for (int k = 0; k < VW; k++) Rr[k] = 0.f;
-    for (int jb = 0; jb < nc; jb += 32) {
-      float ov[32][VW];
-#pragma unroll
-      for (int j = 0; j < 32; j++) {
-        const float *pc = base + (size_t)(cb + min(jb + j, nc - 1)) * stride + d0;
-#pragma unroll
-        for (int k = 0; k < VW; k++) ov[j][k] = load_dev(pc + k);
-      }
-#pragma unroll
-      for (int j = 0; j < 32; j++) {
-        if (jb + j >= nc) break;
-        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jb + j));
-#pragma unroll
-        for (int k = 0; k < VW; k++) Rr[k] += wj * ov[j][k];
-      }
-    }
-    const float Mn = fmaxf(M, Mr);
-    const float sa = expf(M - Mn), sb = expf(Mr - Mn);
-    L = L * sa + Lr * sb;
-#pragma unroll
-    for (int k = 0; k < VW; k++) R[k] = R[k] * sa + Rr[k] * sb;
-    M = Mn;
-  }
-  if (lane < VL) {
-    if (isfinite(L) && L > 0.f) {
-#pragma unroll
-      for (int k = 0; k < VW; k++) out[d0 + k] = R[k] / L;
-    } else {
-      float V[VW];
-#pragma unroll
-      for (int k = 0; k < VW; k++) V[k] = 0.f;
-      for (int c = 0; c < n_active; c++)
-#pragma unroll
-        for (int k = 0; k < VW; k++) V[k] += load_dev(base + (size_t)c * stride + HD + d0 + k);
-#pragma unroll
-      for (int k = 0; k < VW; k++) out[d0 + k] = V[k] / (float)(pos + 1);
-    }
-  }
-  if (lane == 0) __hip_atomic_store(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  attention_item<HD, false>(a, blockIdx.x, blockIdx.y, bounded_pos(a.pos, a.max_seq), qs, kn);
 }
 
 // silu(gate) * up (src/model.rs:251-254).
@@ -387,10 +143,12 @@ __global__ __launch_bounds__(256) void copy_kernel(uint4 *__restrict__ dst,
 // ------------------------------------------------------------------ launchers
 
 int launch_embed(const llrs_tensor *emb, const uint32_t *tok_by_pos, const int *pos, int max_seq,
-                 float *out, hipStream_t s) {
+                 float *out, hipStream_t s, unsigned *clear, int nclear) {
   int H = (int)emb->cols;
-  hipLaunchKernelGGL(embed_kernel, dim3((H + 255) / 256), dim3(256), 0, s, emb->dev, emb->type,
-                     emb->row_bytes, H, (uint32_t)emb->rows, tok_by_pos, pos, max_seq, out);
+  int n = H > nclear ? H : nclear;
+  hipLaunchKernelGGL(embed_kernel, dim3((n + 255) / 256), dim3(256), 0, s, emb->dev, emb->type,
+                     emb->row_bytes, H, (uint32_t)emb->rows, tok_by_pos, pos, max_seq, out, clear,
+                     nclear);
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;
 }

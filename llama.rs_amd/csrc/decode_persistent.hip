@@ -1,0 +1,169 @@
+// The persistent decode kernel: one launch runs every layer of a token's
+// step (Qwen2Model::forward_impl, src/model.rs:173-261) with one workgroup
+// per CU, all co-resident.  Per layer the phases are those of the
+// kernel-per-phase path, with the same arithmetic: RMSNorm + Q/K/V (+bias),
+// RoPE + KV append + attention, o_proj (+residual), RMSNorm + gate/up +
+// SiLU*up, ffn_down (+residual).  A device-wide barrier separates the phases.
+//
+// Why: a separate launch per phase pays the ramp-up of its first weight
+// loads and the drain of its last workgroups every time.  Here a workgroup
+// issues the first weight loads of its next phase (they depend on nothing the
+// current phase writes) before it waits at the barrier, so the wait overlaps
+// HBM latency.
+//
+// Barrier: one device-scope counter that every workgroup increments (an
+// atomic without return, so arriving costs no round trip) and thread 0 of
+// each workgroup polls.  The writer waits for its stores (device-scope
+// stores) before arriving.  Every wait is bounded in time: on expiry the
+// kernel sets *err (reported to the host as an error) and runs on rather than
+// hang.
+#include <hip/hip_runtime.h>
+
+#include "attention_dev.h"
+#include "common.h"
+#include "decode_persistent.h"
+#include "gemv_dev.h"
+
+namespace llrs {
+
+namespace {
+
+__device__ __forceinline__ unsigned ld_u32_dev(unsigned *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The workgroup's stores are complete, then its arrival at the next barrier.
+__device__ void bar_arrive(unsigned *bar) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Until every workgroup has arrived at barrier k (k >= 1), or ~20 ms passed.
+__device__ void bar_wait(unsigned *bar, unsigned *err, int nwg, unsigned k) {
+  if (threadIdx.x == 0) {
+    const unsigned target = k * (unsigned)nwg;
+    const unsigned long long t0 = wall_clock64();
+    while (ld_u32_dev(bar) < target) {
+      __builtin_amdgcn_s_sleep(1);
+      if (wall_clock64() - t0 > 2000000ull) {  // the 100 MHz wall clock: 20 ms
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+typedef const __attribute__((address_space(4))) PersistentLayer ConstLayer;
+
+template <uint32_t TQ, uint32_t TV, uint32_t TO, uint32_t TGU, uint32_t TD, int HD>
+__global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(PersistentArgs p) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float red[16];
+  __shared__ __align__(16) float aqs[kPersistentThreads / 64][HD], akn[kPersistentThreads / 64][HD];
+  const int wg = blockIdx.x, nwg = gridDim.x;
+  const int wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  const int pos = bounded_pos(p.attn.pos, p.attn.max_seq);
+  const int n_items = p.attn.nh * (pos / kChunk + 1);
+  unsigned k = 0;
+  for (int l = 0; l < p.nlayers; l++) {
+    // Through the constant address space: the arguments are never written
+    // during the launch, so they load through the scalar cache.
+    const PersistentLayer &L = *(const PersistentLayer *)(ConstLayer *)((uintptr_t)(p.layers + l));
+    // The phase objects are value-initialised: a member that one path leaves
+    // unset would otherwise be carried in registers from the previous layer.
+    {  // RMSNorm + Q/K/V (+ bias)
+      GemvPhase<TQ, TV, false, true> ph{};
+      ph.prefetch(L.qkv, wg, nwg);
+      if (k) bar_wait(p.bar, p.err, nwg, k);
+      ph.finish(L.qkv, smem, red);
+      bar_arrive(p.bar);
+      k++;
+    }
+    {  // RoPE, KV append, attention: one (head, chunk) item per wave
+      AttnArgs a = p.attn;
+      a.q += l * p.act_stride;
+      a.k += l * p.act_stride;
+      a.v += l * p.act_stride;
+      a.out += l * p.act_stride;
+      a.k_cache += l * p.cache_stride;
+      a.v_cache += l * p.cache_stride;
+      bar_wait(p.bar, p.err, nwg, k);
+      for (int it = wave * nwg + wg; it < n_items; it += nwg * nwv)
+        attention_item<HD, true>(a, it % a.nh, it / a.nh, pos, aqs[wave], akn[wave]);
+      bar_arrive(p.bar);
+      k++;
+    }
+    {  // o_proj (+ residual)
+      GemvPhase<TO, TO, false, true> ph{};
+      ph.prefetch(L.o, wg, nwg);
+      bar_wait(p.bar, p.err, nwg, k);
+      ph.finish(L.o, smem, red);
+      bar_arrive(p.bar);
+      k++;
+    }
+    {  // RMSNorm + gate/up + SiLU*up
+      GemvPhase<TGU, TGU, true, true> ph{};
+      ph.prefetch(L.gate_up, wg, nwg);
+      bar_wait(p.bar, p.err, nwg, k);
+      ph.finish(L.gate_up, smem, red);
+      bar_arrive(p.bar);
+      k++;
+    }
+    {  // ffn_down (+ residual)
+      GemvPhase<TD, TD, false, true> ph{};
+      ph.prefetch(L.down, wg, nwg);
+      bar_wait(p.bar, p.err, nwg, k);
+      ph.finish(L.down, smem, red);
+      bar_arrive(p.bar);
+      k++;
+    }
+  }
+}
+
+template <uint32_t TQ, uint32_t TV, uint32_t TO, uint32_t TGU, uint32_t TD>
+int launch_types(const PersistentArgs &p, int head_dim, int grid, size_t lds, hipStream_t s) {
+  const dim3 g((unsigned)grid), b(kPersistentThreads);
+  switch (head_dim) {
+    case 64: hipLaunchKernelGGL((decode_persistent_kernel<TQ, TV, TO, TGU, TD, 64>), g, b, lds, s, p); break;
+    case 128: hipLaunchKernelGGL((decode_persistent_kernel<TQ, TV, TO, TGU, TD, 128>), g, b, lds, s, p); break;
+    default: return set_error(LLRS_E_UNSUPPORTED, "persistent decode: head_dim %d", head_dim);
+  }
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+}  // namespace
+
+// The instantiated type sets: the q4km recipe at hidden sizes that are
+// multiples of 256 (Q4_K, Q8_0 V, Q6_K down) and not (Q5_0 fallback), and
+// the uniform q4k recipe.
+bool decode_persistent_supports(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, uint32_t t_gu,
+                                uint32_t t_down, int head_dim) {
+  if (head_dim != 64 && head_dim != 128) return false;
+  const bool q4km = t_qkv == LLRS_Q4_K && t_v == LLRS_Q8_0 && t_o == LLRS_Q4_K && t_gu == LLRS_Q4_K &&
+                    t_down == LLRS_Q6_K;
+  const bool q4km_q5 = t_qkv == LLRS_Q5_0 && t_v == LLRS_Q8_0 && t_o == LLRS_Q5_0 &&
+                       t_gu == LLRS_Q5_0 && t_down == LLRS_Q6_K;
+  const bool q4k = t_qkv == LLRS_Q4_K && t_v == LLRS_Q4_K && t_o == LLRS_Q4_K && t_gu == LLRS_Q4_K &&
+                   t_down == LLRS_Q4_K;
+  return q4km || q4km_q5 || q4k;
+}
+
+int launch_decode_persistent(const PersistentArgs &p, uint32_t t_qkv, uint32_t t_v, uint32_t t_o,
+                             uint32_t t_gu, uint32_t t_down, int head_dim, int grid, size_t lds,
+                             hipStream_t s) {
+  if (grid < 1) return set_error(LLRS_E_INVALID, "persistent decode: grid %d", grid);
+  if (lds + persistent_static_lds(head_dim) > kCuLds)
+    return set_error(LLRS_E_UNSUPPORTED, "persistent decode needs %zu bytes of LDS", lds);
+  if (t_qkv == LLRS_Q4_K && t_v == LLRS_Q8_0 && t_down == LLRS_Q6_K)
+    return launch_types<LLRS_Q4_K, LLRS_Q8_0, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q6_K>(p, head_dim, grid, lds, s);
+  if (t_qkv == LLRS_Q5_0)
+    return launch_types<LLRS_Q5_0, LLRS_Q8_0, LLRS_Q5_0, LLRS_Q5_0, LLRS_Q6_K>(p, head_dim, grid, lds, s);
+  if (t_qkv == LLRS_Q4_K && t_v == LLRS_Q4_K)
+    return launch_types<LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K>(p, head_dim, grid, lds, s);
+  return set_error(LLRS_E_UNSUPPORTED, "persistent decode: no instantiation for these weight types");
+}
+
+}  // namespace llrs

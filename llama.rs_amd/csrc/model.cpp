@@ -10,6 +10,7 @@
 //                          (src/engine.rs:205-216) + argmax (233-241)
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -20,6 +21,7 @@
 
 #include "common.h"
 #include "decode.h"
+#include "decode_persistent.h"
 #include "gemv.h"
 #include "gguf.h"
 #include "prefill.h"
@@ -70,6 +72,15 @@ struct llrs_kv {
   unsigned long long *amax_key = nullptr;  // LM-head argmax accumulator (zero between steps)
   unsigned *done = nullptr;                // LM-head block completion counter
   uint8_t *act_dig = nullptr;              // SiLU*up digitised by gate/up for ffn_down
+  // Persistent decode (one launch for every layer), when the model's weight
+  // types have an instantiation: per-layer arguments, barrier words, error flag.
+  llrs::PersistentLayer *p_layers = nullptr;
+  unsigned *p_bar = nullptr, *p_err = nullptr;
+  llrs::AttnArgs p_attn{};  // layer 0's attention (per-layer buffers act_stride floats apart)
+  long p_act_stride = 0;
+  int p_grid = 0;
+  size_t p_lds = 0;
+  uint32_t p_types[5] = {};
   uint32_t *pinned = nullptr;  // host staging, max_seq_len + 2 words
   hipGraph_t graph[2] = {nullptr, nullptr};
   hipGraphExec_t exec[2] = {nullptr, nullptr};
@@ -329,6 +340,9 @@ static int synth_config_to_model(const llrs_synth_config &s, llrs_model_config &
 // Projection groups of the decode step: each is one launch on the tuned path
 // (fused RMSNorm prologue / epilogues), or the generic sequence otherwise.
 enum Proj { P_QKV = 0, P_O, P_GATE_UP, P_DOWN, P_LM_HEAD, P_COUNT };
+// Profiling only: every layer of the step (the persistent kernel, or the
+// per-phase launches), embedding and LM head excluded.
+constexpr int P_LAYERS = P_COUNT;
 
 static bool fast_ok(const llrs_tensor *t) {
   return t->rows % 4 == 0 && t->rows <= INT32_MAX && fast_gemv_supports(t->type, t->cols);
@@ -364,24 +378,17 @@ static FastSeg seg_of(const llrs_tensor *t, const float *bias, float *out) {
   return s;
 }
 
-// The decode step's launch(es) for projection group `which` of layer `l`; the
-// bench's per-kernel timing calls this same function.
-static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hipStream_t s) {
+// The tuned GEMV's arguments for projection group `which` of layer `l` (the
+// caller has checked use_fast); shared by the per-phase launches and the
+// persistent decode kernel.
+static FastGemvArgs projection_args(llrs_model *m, llrs_kv *kv, size_t l, int which) {
   const llrs_model_config &c = m->cfg;
   const int H = (int)c.hidden_size, F = (int)c.intermediate_size;
-  const float eps = c.rms_norm_eps;
-  const bool fast = use_fast(m, l, which);
   FastGemvArgs a{};
-  a.eps = eps;
+  a.eps = c.rms_norm_eps;
   a.cols = H;
   a.x = kv->residual;
   if (which == P_LM_HEAD) {
-    if (!fast) {
-      LLRS_TRY(launch_rmsnorm(kv->residual, m->norm, kv->hidden, H, eps, s));
-      LLRS_TRY(launch_gemv_generic(m->lm_head, kv->hidden, kv->logits, nullptr, false, s));
-      return launch_argmax(kv->logits, (int)c.vocab_size, kv->pos, (int)kv->max_seq_len,
-                           kv->tok_by_pos, kv->next_token, 1, s);
-    }
     a.seg[0] = seg_of(m->lm_head, nullptr, kv->logits);
     a.nseg = 1;
     a.rows = (int)c.vocab_size;
@@ -393,17 +400,11 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
     a.tok_by_pos = kv->tok_by_pos;
     a.next_token = kv->next_token;
     a.max_pos = (int)kv->max_seq_len;
-    return launch_gemv_fast(a, fast_grid(m, a), s);
+    return a;
   }
   DevLayer &L = m->layers[l];
   switch (which) {
     case P_QKV:
-      if (!fast) {
-        LLRS_TRY(launch_rmsnorm(kv->residual, L.attn_norm, kv->hidden, H, eps, s));
-        LLRS_TRY(launch_gemv_generic(L.q, kv->hidden, kv->q, L.bq, false, s));
-        LLRS_TRY(launch_gemv_generic(L.k, kv->hidden, kv->k, L.bk, false, s));
-        return launch_gemv_generic(L.v, kv->hidden, kv->v, L.bv, false, s);
-      }
       a.seg[0] = seg_of(L.q, L.bq, kv->q);
       a.seg[1] = seg_of(L.k, L.bk, kv->k);
       a.seg[2] = seg_of(L.v, L.bv, kv->v);
@@ -411,22 +412,15 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
       a.rows = (int)(L.q->rows + L.k->rows + L.v->rows);
       a.norm = L.attn_norm;
       a.epi = kEpiStore;
-      return launch_gemv_fast(a, fast_grid(m, a), s);
+      break;
     case P_O:
-      if (!fast) return launch_gemv_generic(L.o, kv->attn, kv->residual, nullptr, true, s);
       a.seg[0] = seg_of(L.o, nullptr, kv->residual);
       a.nseg = 1;
       a.rows = H;
       a.x = kv->attn;
       a.epi = kEpiAdd;
-      return launch_gemv_fast(a, fast_grid(m, a), s);
+      break;
     case P_GATE_UP:
-      if (!fast) {
-        LLRS_TRY(launch_rmsnorm(kv->residual, L.ffn_norm, kv->hidden, H, eps, s));
-        LLRS_TRY(launch_gemv_generic(L.gate, kv->hidden, kv->gate, nullptr, false, s));
-        LLRS_TRY(launch_gemv_generic(L.up, kv->hidden, kv->up, nullptr, false, s));
-        return launch_silu_mul(kv->gate, kv->up, kv->act, F, s);
-      }
       a.seg[0] = seg_of(L.gate, nullptr, kv->gate);
       a.seg[1] = seg_of(L.up, nullptr, kv->up);
       a.seg[2] = seg_of(L.gate, nullptr, kv->act);
@@ -439,9 +433,8 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
         a.part = 16;
         a.dig_out = kv->act_dig;
       }
-      return launch_gemv_fast(a, fast_grid(m, a, true), s);
-    case P_DOWN:
-      if (!fast) return launch_gemv_generic(L.down, kv->act, kv->residual, nullptr, true, s);
+      break;
+    default:  // P_DOWN
       a.seg[0] = seg_of(L.down, nullptr, kv->residual);
       a.nseg = 1;
       a.rows = H;
@@ -449,13 +442,54 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
       a.x = kv->act;
       a.epi = kEpiAdd;
       if (use_fast(m, l, P_GATE_UP) && F % 64 == 0) a.dig_in = kv->act_dig;
-      return launch_gemv_fast(a, fast_grid(m, a), s);
-    default: return set_error(LLRS_E_INVALID, "unknown projection %d", which);
+      break;
+  }
+  return a;
+}
+
+// The decode step's launch(es) for projection group `which` of layer `l`; the
+// bench's per-kernel timing calls this same function.
+static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hipStream_t s) {
+  const llrs_model_config &c = m->cfg;
+  const int H = (int)c.hidden_size, F = (int)c.intermediate_size;
+  const float eps = c.rms_norm_eps;
+  if (which < 0 || which >= P_COUNT) return set_error(LLRS_E_INVALID, "unknown projection %d", which);
+  if (use_fast(m, l, which)) {
+    const FastGemvArgs a = projection_args(m, kv, l, which);
+    return launch_gemv_fast(a, fast_grid(m, a, which == P_GATE_UP), s);
+  }
+  if (which == P_LM_HEAD) {
+    LLRS_TRY(launch_rmsnorm(kv->residual, m->norm, kv->hidden, H, eps, s));
+    LLRS_TRY(launch_gemv_generic(m->lm_head, kv->hidden, kv->logits, nullptr, false, s));
+    return launch_argmax(kv->logits, (int)c.vocab_size, kv->pos, (int)kv->max_seq_len,
+                         kv->tok_by_pos, kv->next_token, 1, s);
+  }
+  DevLayer &L = m->layers[l];
+  switch (which) {
+    case P_QKV:
+      LLRS_TRY(launch_rmsnorm(kv->residual, L.attn_norm, kv->hidden, H, eps, s));
+      LLRS_TRY(launch_gemv_generic(L.q, kv->hidden, kv->q, L.bq, false, s));
+      LLRS_TRY(launch_gemv_generic(L.k, kv->hidden, kv->k, L.bk, false, s));
+      return launch_gemv_generic(L.v, kv->hidden, kv->v, L.bv, false, s);
+    case P_O: return launch_gemv_generic(L.o, kv->attn, kv->residual, nullptr, true, s);
+    case P_GATE_UP:
+      LLRS_TRY(launch_rmsnorm(kv->residual, L.ffn_norm, kv->hidden, H, eps, s));
+      LLRS_TRY(launch_gemv_generic(L.gate, kv->hidden, kv->gate, nullptr, false, s));
+      LLRS_TRY(launch_gemv_generic(L.up, kv->hidden, kv->up, nullptr, false, s));
+      return launch_silu_mul(kv->gate, kv->up, kv->act, F, s);
+    default: return launch_gemv_generic(L.down, kv->act, kv->residual, nullptr, true, s);
   }
 }
 
 static size_t projection_bytes(llrs_model *m, int which) {
   if (which == P_LM_HEAD) return m->lm_head->nbytes;
+  if (which == P_LAYERS) {
+    size_t b = 0;
+    for (const DevLayer &L : m->layers)
+      b += L.q->nbytes + L.k->nbytes + L.v->nbytes + L.o->nbytes + L.gate->nbytes + L.up->nbytes +
+           L.down->nbytes;
+    return b;
+  }
   const DevLayer &L = m->layers[0];
   switch (which) {
     case P_QKV: return L.q->nbytes + L.k->nbytes + L.v->nbytes;
@@ -465,37 +499,70 @@ static size_t projection_bytes(llrs_model *m, int which) {
   }
 }
 
-static int enqueue_step(llrs_model *m, llrs_kv *kv, int mode) {
+// The attention launch of layer l: GQA over the layer's cache at *pos.
+static AttnArgs attention_args(llrs_model *m, llrs_kv *kv, size_t l) {
   const llrs_model_config &c = m->cfg;
-  hipStream_t s = m->b->stream;
-  const int max_seq = (int)kv->max_seq_len;
-  size_t layer_stride = kv->max_seq_len * c.kv_width;
+  const size_t layer_stride = kv->max_seq_len * c.kv_width;
   AttnArgs at{};
   at.q = kv->q;
   at.k = kv->k;
   at.v = kv->v;
   at.rope = kv->rope;
   at.pos = kv->pos;
+  at.k_cache = kv->k_cache + l * layer_stride;
+  at.v_cache = kv->v_cache + l * layer_stride;
   at.out = kv->attn;
   at.scratch = kv->scores;
   at.counters = kv->attn_counters;
   at.nh = (int)c.num_attention_heads;
   at.nkv = (int)c.num_key_value_heads;
   at.hd = (int)c.head_dim;
-  at.max_seq = max_seq;
-  at.max_chunks = attention_chunks(max_seq);
+  at.max_seq = (int)kv->max_seq_len;
+  at.max_chunks = attention_chunks(at.max_seq);
   at.part_stride = attention_part_stride(at.hd);
   at.scale = 1.0f / sqrtf((float)c.head_dim);
-  LLRS_TRY(launch_embed(m->embed, kv->tok_by_pos, kv->pos, max_seq, kv->residual, s));
+  return at;
+}
+
+// The step's layers: one persistent launch, or five launches per layer.
+static int enqueue_layers(llrs_model *m, llrs_kv *kv) {
+  const llrs_model_config &c = m->cfg;
+  hipStream_t s = m->b->stream;
+  if (kv->p_layers) {
+    PersistentArgs p{};
+    p.layers = kv->p_layers;
+    p.nlayers = (int)c.num_hidden_layers;
+    p.attn = kv->p_attn;
+    p.act_stride = kv->p_act_stride;
+    p.cache_stride = (long)(kv->max_seq_len * c.kv_width);
+    p.bar = kv->p_bar;
+    p.err = kv->p_err;
+    const uint32_t *t = kv->p_types;
+    return launch_decode_persistent(p, t[0], t[1], t[2], t[3], t[4], (int)c.head_dim, kv->p_grid,
+                                    kv->p_lds, s);
+  }
   for (size_t l = 0; l < c.num_hidden_layers; l++) {
-    at.k_cache = kv->k_cache + l * layer_stride;
-    at.v_cache = kv->v_cache + l * layer_stride;
     LLRS_TRY(launch_projection(m, kv, l, P_QKV, s));
-    LLRS_TRY(launch_attention(at, s));
+    LLRS_TRY(launch_attention(attention_args(m, kv, l), s));
     LLRS_TRY(launch_projection(m, kv, l, P_O, s));
     LLRS_TRY(launch_projection(m, kv, l, P_GATE_UP, s));
     LLRS_TRY(launch_projection(m, kv, l, P_DOWN, s));
   }
+  return LLRS_OK;
+}
+
+// The embedding of tok_by_pos[*pos] (which also zeroes the persistent
+// kernel's barrier counter).
+static int enqueue_embed(llrs_model *m, llrs_kv *kv) {
+  return launch_embed(m->embed, kv->tok_by_pos, kv->pos, (int)kv->max_seq_len, kv->residual,
+                      m->b->stream, kv->p_bar, kv->p_bar ? kPersistentBarWords : 0);
+}
+
+static int enqueue_step(llrs_model *m, llrs_kv *kv, int mode) {
+  hipStream_t s = m->b->stream;
+  const int max_seq = (int)kv->max_seq_len;
+  LLRS_TRY(enqueue_embed(m, kv));
+  LLRS_TRY(enqueue_layers(m, kv));
   if (mode == LLRS_LOGITS_COMPUTE) {
     LLRS_TRY(launch_projection(m, kv, 0, P_LM_HEAD, s));
   } else {
@@ -543,6 +610,105 @@ static void rope_table(float *dst, size_t max_seq, size_t hd, float theta) {
       dst[p * hd + i] = cosf(a);
       dst[p * hd + half + i] = sinf(a);
     }
+}
+
+static bool persistent_disabled() {
+  const char *e = getenv("LLRS_NO_PERSISTENT");
+  return e && *e && *e != '0';
+}
+
+// Chooses the persistent decode kernel when every layer runs the tuned GEMV
+// with one set of weight types that has an instantiation, and uploads the
+// per-layer arguments it reads.
+static int setup_persistent(llrs_model *m, llrs_kv *kv) {
+  const llrs_model_config &c = m->cfg;
+  if (persistent_disabled() || c.intermediate_size % 64) return LLRS_OK;
+  const size_t nl = c.num_hidden_layers;
+  uint32_t t[5] = {};
+  for (size_t l = 0; l < nl; l++) {
+    for (int w = P_QKV; w <= P_DOWN; w++)
+      if (!use_fast(m, l, w)) return LLRS_OK;
+    const DevLayer &L = m->layers[l];
+    const uint32_t tl[5] = {L.q->type, L.v->type, L.o->type, L.gate->type, L.down->type};
+    if (l == 0) memcpy(t, tl, sizeof t);
+    if (memcmp(t, tl, sizeof t)) return LLRS_OK;
+  }
+  if (!decode_persistent_supports(t[0], t[1], t[2], t[3], t[4], (int)c.head_dim)) return LLRS_OK;
+  const int grid = m->b->cu_count;
+  // Per-layer activation buffers (each slice 256-byte aligned, so no cache
+  // line holds two buffers): q|k|v, attention output, residual after o_proj
+  // and after ffn_down, SiLU*up digits.  The last layer's ffn_down writes
+  // the shared residual the LM head reads.
+  const size_t H = c.hidden_size, KV = c.kv_width, F = c.intermediate_size;
+  auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+  const size_t sz_qkv = al((H + 2 * KV) * 4), sz_h = al(H * 4), sz_dig = al(fast_gemv_digits_size(F));
+  const size_t per_layer = sz_qkv + 3 * sz_h + sz_dig;
+  uint8_t *act = nullptr;
+  LLRS_TRY(dev_alloc(kv->allocs, (void **)&act, nl * per_layer));
+  std::vector<PersistentLayer> host(nl);
+  size_t lds = 0;
+  const float *x_in = kv->residual;
+  for (size_t l = 0; l < nl; l++) {
+    uint8_t *b = act + l * per_layer;
+    float *q = (float *)b, *k = q + H, *v = k + KV;
+    float *attn = (float *)(b + sz_qkv), *x_mid = (float *)(b + sz_qkv + sz_h);
+    float *x_out = l + 1 == nl ? kv->residual : (float *)(b + sz_qkv + 2 * sz_h);
+    uint8_t *dig = b + sz_qkv + 3 * sz_h;
+    PersistentLayer &P = host[l];
+    P.qkv = projection_args(m, kv, l, P_QKV);
+    P.qkv.x = x_in;
+    P.qkv.seg[0].out = q;
+    P.qkv.seg[1].out = k;
+    P.qkv.seg[2].out = v;
+    if (l == 0) {
+      kv->p_attn = attention_args(m, kv, 0);
+      kv->p_attn.q = q;
+      kv->p_attn.k = k;
+      kv->p_attn.v = v;
+      kv->p_attn.out = attn;
+    }
+    P.o = projection_args(m, kv, l, P_O);
+    P.o.x = attn;
+    P.o.res_in = x_in;
+    P.o.seg[0].out = x_mid;
+    P.gate_up = projection_args(m, kv, l, P_GATE_UP);
+    P.gate_up.x = x_mid;
+    P.gate_up.dig_out = dig;
+    P.down = projection_args(m, kv, l, P_DOWN);
+    P.down.dig_in = dig;
+    P.down.res_in = x_mid;
+    P.down.seg[0].out = x_out;
+    if (!P.gate_up.dig_out || P.gate_up.part != 16) return LLRS_OK;
+    for (const FastGemvArgs *a : {&P.qkv, &P.o, &P.gate_up, &P.down})
+      lds = std::max(lds, fast_gemv_lds_bytes(*a, grid));
+    x_in = x_out;
+  }
+  // More than half a CU's LDS per workgroup: exactly one workgroup per CU.
+  lds = std::max(lds, kPersistentMinLds);
+  if (lds + persistent_static_lds((int)c.head_dim) > kCuLds) return LLRS_OK;
+  auto A = [&](void **p, size_t bytes) { return dev_alloc(kv->allocs, p, bytes); };
+  LLRS_TRY(A((void **)&kv->p_layers, nl * sizeof(PersistentLayer)));
+  LLRS_TRY(A((void **)&kv->p_bar, kPersistentBarWords * 4));
+  LLRS_TRY(A((void **)&kv->p_err, 64));
+  hipStream_t s = m->b->stream;
+  LLRS_HIP(hipMemcpyAsync(kv->p_layers, host.data(), nl * sizeof(PersistentLayer), hipMemcpyHostToDevice, s));
+  LLRS_HIP(hipMemsetAsync(kv->p_bar, 0, kPersistentBarWords * 4, s));
+  LLRS_HIP(hipMemsetAsync(kv->p_err, 0, 64, s));
+  LLRS_HIP(hipStreamSynchronize(s));
+  memcpy(kv->p_types, t, sizeof t);
+  kv->p_act_stride = (long)(per_layer / 4);
+  kv->p_grid = grid;
+  kv->p_lds = lds;
+  return LLRS_OK;
+}
+
+// Reports a persistent-decode barrier wait that gave up (the stream is idle).
+static int check_persistent(llrs_kv *kv) {
+  if (!kv->p_err) return LLRS_OK;
+  unsigned err = 0;
+  LLRS_HIP(hipMemcpy(&err, kv->p_err, 4, hipMemcpyDeviceToHost));
+  if (err) return set_error(LLRS_E_HIP, "persistent decode: a device-wide barrier timed out");
+  return LLRS_OK;
 }
 
 static void free_kv(llrs_kv *kv) {
@@ -613,6 +779,10 @@ static int kv_create_impl(llrs_model *m, size_t max_seq, llrs_kv **out) {
   if (e != hipSuccess) {
     free_kv(kv);
     return set_error(LLRS_E_HIP, "KV cache init failed: %s", hipGetErrorString(e));
+  }
+  if ((rc = setup_persistent(m, kv)) != LLRS_OK) {
+    free_kv(kv);
+    return rc;
   }
   *out = kv;
   return LLRS_OK;
@@ -875,6 +1045,8 @@ int llrs_kv_reset(llrs_kv *kv) {
   return kv ? LLRS_OK : set_error(LLRS_E_INVALID, "kv is NULL");
 }
 
+int llrs_kv_decode_path(const llrs_kv *kv) { return kv && kv->p_layers ? 1 : 0; }
+
 int llrs_forward_token(llrs_model *m, llrs_kv *kv, uint32_t token, size_t pos, int logits_mode) {
   clear_error();
   if (!m || !kv || kv->m != m) return set_error(LLRS_E_INVALID, "model/kv mismatch");
@@ -889,7 +1061,7 @@ int llrs_forward_token(llrs_model *m, llrs_kv *kv, uint32_t token, size_t pos, i
   LLRS_TRY(stage_tokens(kv, &token, 1, pos));
   LLRS_TRY(run_step(m, kv, logits_mode));
   LLRS_HIP(hipStreamSynchronize(m->b->stream));
-  return LLRS_OK;
+  return check_persistent(kv);
 }
 
 int llrs_prefill(llrs_model *m, llrs_kv *kv, const uint32_t *tokens, size_t n, size_t start_pos) {
@@ -913,7 +1085,7 @@ int llrs_prefill(llrs_model *m, llrs_kv *kv, const uint32_t *tokens, size_t n, s
       LLRS_TRY(run_step(m, kv, i + 1 == n ? LLRS_LOGITS_COMPUTE : LLRS_LOGITS_SKIP));
   }
   LLRS_HIP(hipStreamSynchronize(m->b->stream));
-  return LLRS_OK;
+  return check_persistent(kv);
 }
 
 int llrs_decode_greedy(llrs_model *m, llrs_kv *kv, size_t start_pos, size_t n_steps,
@@ -935,7 +1107,7 @@ int llrs_decode_greedy(llrs_model *m, llrs_kv *kv, size_t start_pos, size_t n_st
                           hipMemcpyDeviceToHost, s));
   LLRS_HIP(hipStreamSynchronize(s));
   memcpy(out_tokens, kv->pinned, n_steps * 4);
-  return LLRS_OK;
+  return check_persistent(kv);
 }
 
 int llrs_argmax(llrs_kv *kv, uint32_t *out_token) {
@@ -988,7 +1160,7 @@ int llrs_profile_projection(llrs_model *m, llrs_kv *kv, int which, int iters, do
                             size_t *bytes_per_launch) {
   clear_error();
   if (!m || !kv || kv->m != m || !avg_us) return set_error(LLRS_E_INVALID, "bad arguments");
-  if (which < 0 || which >= P_COUNT) return set_error(LLRS_E_INVALID, "unknown projection %d", which);
+  if (which < 0 || which > P_LAYERS) return set_error(LLRS_E_INVALID, "unknown projection %d", which);
   if (iters < 1) return set_error(LLRS_E_INVALID, "iters must be positive");
   LLRS_HIP(hipSetDevice(m->b->device));
   hipStream_t s = m->b->stream;
@@ -1004,6 +1176,37 @@ int llrs_profile_projection(llrs_model *m, llrs_kv *kv, int which, int iters, do
       (void)hipMemcpy(kv->pos, &pos, 4, hipMemcpyHostToDevice);
     }
   } restore{kv, saved_pos};
+  if (which == P_LAYERS) {
+    // Each round: the embedding (outside the timed span), then the layers
+    // between two events.  Rounds recompute the same position, so they are
+    // idempotent.
+    std::vector<hipEvent_t> ev(2 * (size_t)iters + 2, nullptr);
+    int rc = LLRS_OK;
+    hipError_t e = hipSuccess;
+    for (auto &x : ev)
+      if (e == hipSuccess) e = hipEventCreate(&x);
+    for (int it = -1; it < iters && rc == LLRS_OK && e == hipSuccess; it++) {  // round -1 warms
+      rc = enqueue_embed(m, kv);
+      if (rc == LLRS_OK) e = hipEventRecord(ev[2 * (it + 1)], s);
+      if (rc == LLRS_OK && e == hipSuccess) rc = enqueue_layers(m, kv);
+      if (rc == LLRS_OK && e == hipSuccess) e = hipEventRecord(ev[2 * (it + 1) + 1], s);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    double total = 0;
+    for (int it = 0; it < iters && e == hipSuccess; it++) {
+      float ms = 0.f;
+      e = hipEventElapsedTime(&ms, ev[2 * (it + 1)], ev[2 * (it + 1) + 1]);
+      total += ms;
+    }
+    for (auto &x : ev)
+      if (x) (void)hipEventDestroy(x);
+    LLRS_TRY(rc);
+    if (e != hipSuccess) return set_error(LLRS_E_HIP, "event timing failed: %s", hipGetErrorString(e));
+    LLRS_TRY(check_persistent(kv));
+    *avg_us = 1000.0 * total / iters;
+    if (bytes_per_launch) *bytes_per_launch = projection_bytes(m, which);
+    return LLRS_OK;
+  }
   size_t layers = which == P_LM_HEAD ? 1 : m->cfg.num_hidden_layers;
   hipEvent_t e0, e1;
   LLRS_HIP(hipEventCreate(&e0));

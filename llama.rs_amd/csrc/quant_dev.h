@@ -12,6 +12,16 @@
 
 namespace llrs {
 
+// threadIdx.x, read afresh at each call.  The persistent decode kernel runs
+// every phase of a layer inside one loop over the layers; values derived from
+// the (loop-invariant) thread index would otherwise be hoisted out of that
+// loop and held in registers for all phases at once.
+__device__ __forceinline__ int thread_x() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
   // v_cvt_f32_f16: exact widening, f16 subnormals preserved (gfx9 default mode).
   return (float)__builtin_bit_cast(_Float16, h);
@@ -102,6 +112,51 @@ __device__ inline float value_dev(const uint8_t *row, uint32_t ty, uint32_t col)
       return ld_f16(b + 208) * scale * q;
     }
     default: return 0.0f;
+  }
+}
+
+// Loads and stores of activations.  With COH (the persistent decode kernel,
+// where producer and consumer run in the same launch on different XCDs) they
+// are device-scope relaxed atomics, which go through to memory; otherwise
+// plain accesses (kernel boundaries order them).
+template <bool COH> __device__ __forceinline__ float ld_act(const float *p) {
+  if constexpr (COH)
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    return *p;
+}
+template <bool COH> __device__ __forceinline__ void st_act(float *p, float v) {
+  if constexpr (COH)
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *p = v;
+}
+template <bool COH> __device__ __forceinline__ float4 ld_act4(const float *p) {
+  if constexpr (COH)
+    return make_float4(ld_act<true>(p), ld_act<true>(p + 1), ld_act<true>(p + 2), ld_act<true>(p + 3));
+  else
+    return *reinterpret_cast<const float4 *>(p);
+}
+template <bool COH> __device__ __forceinline__ uint4 ld_u4(const uint8_t *p) {
+  if constexpr (COH) {
+    uint32_t *q = reinterpret_cast<uint32_t *>(const_cast<uint8_t *>(p));
+    return make_uint4(__hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                      __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                      __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                      __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  } else {
+    return *reinterpret_cast<const uint4 *>(p);
+  }
+}
+template <bool COH> __device__ __forceinline__ void st_u4(uint8_t *p, uint4 v) {
+  if constexpr (COH) {
+    uint32_t *q = reinterpret_cast<uint32_t *>(p);
+    __hip_atomic_store(q, v.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, v.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 2, v.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 3, v.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *reinterpret_cast<uint4 *>(p) = v;
   }
 }
 

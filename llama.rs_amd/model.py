@@ -127,6 +127,14 @@ class HipQwen2Model:
                                              C.byref(nb)))
         return us.value, nb.value
 
+    def profile_layers(self, kv_cache: "KVCache", iters: int = 10):
+        """(mean time in us, weight bytes) of every layer of one decode step: the
+        persistent kernel when kv_cache.persistent, else the per-phase launches."""
+        us, nb = C.c_double(), SZ()
+        _check(lib().llrs_profile_projection(self.handle, kv_cache.handle, len(self.PROJECTIONS),
+                                             iters, C.byref(us), C.byref(nb)))
+        return us.value, nb.value
+
     def __del__(self):
         h = getattr(self, "handle", None)
         if h and lib is not None:
@@ -146,6 +154,11 @@ class KVCache:
 
     def reset(self) -> None:
         _check(lib().llrs_kv_reset(self.handle))
+
+    @property
+    def persistent(self) -> bool:
+        """Whether decode steps run as one persistent launch for all layers."""
+        return lib().llrs_kv_decode_path(self.handle) == 1
 
     def logits(self) -> np.ndarray:
         out = np.empty(self.model.config().vocab_size, dtype=np.float32)

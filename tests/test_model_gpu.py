@@ -123,6 +123,45 @@ def test_forward_token_matches_prefill(llrs, backend, oracle, tmp_path, monkeypa
     np.testing.assert_array_equal(model.decode_greedy(n, 8, kv1), model.decode_greedy(n, 8, kv2))
 
 
+@pytest.mark.parametrize("geom", [
+    dict(),                                                   # Q4_K / Q8_0 V / Q6_K down, head_dim 64
+    dict(hidden_size=512, intermediate_size=1024, seed=3),    # head_dim 128
+    dict(hidden_size=384, num_attention_heads=6, intermediate_size=1024, seed=5),  # Q5_0 fallback
+    dict(recipe=None, seed=9),                                # uniform Q4_K
+], ids=["q4km_hd64", "q4km_hd128", "q4km_q5_0", "q4k"])
+def test_persistent_decode_matches_per_phase(llrs, backend, tmp_path, monkeypatch, geom):
+    """The persistent decode kernel (every layer in one launch, device-wide
+    barriers between phases) computes bit-identical logits, tokens and KV
+    rows to the launch-per-phase path: the same per-row arithmetic, only
+    scheduled differently."""
+    if geom.get("recipe", 0) is None:
+        geom = dict(geom, recipe=llrs.LoadQuantization.Q4K)
+    cfg = tiny_cfg(llrs, **geom)
+    cfg.write_gguf(tmp_path / "p.gguf")
+    model = llrs.ModelLoader.load_dynamic(tmp_path / "p.gguf", backend)
+    ctx = 96
+    kv_p = llrs.KVCache(model, ctx)
+    monkeypatch.setenv("LLRS_NO_PERSISTENT", "1")
+    kv_s = llrs.KVCache(model, ctx)
+    monkeypatch.delenv("LLRS_NO_PERSISTENT")
+    assert kv_p.persistent and not kv_s.persistent
+    prompt = np.array([3, 77, 512, 9, 1, 640], np.uint32)
+    for i, t in enumerate(prompt):  # token-wise: every step through the decode kernels
+        for kv in (kv_p, kv_s):
+            model.forward_token(int(t), i, kv, llrs.LogitsMode.COMPUTE)
+        np.testing.assert_array_equal(kv_p.logits(), kv_s.logits())
+    # 40 greedy steps cross the 32-position attention chunk boundary.
+    got = model.decode_greedy(len(prompt), 40, kv_p)
+    want = model.decode_greedy(len(prompt), 40, kv_s)
+    print(f"[persistent] tokens {got[:8].tolist()}...", flush=True)
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(kv_p.logits(), kv_s.logits())
+    n = len(prompt) + 40
+    for layer in (0, cfg.num_hidden_layers - 1):
+        for which in ("k", "v"):
+            np.testing.assert_array_equal(kv_p.layer(layer, which, n), kv_s.layer(layer, which, n))
+
+
 def test_model_error_paths(llrs, backend, tmp_path):
     cfg = tiny_cfg(llrs, seed=17)
     cfg.write_gguf(tmp_path / "e.gguf")
