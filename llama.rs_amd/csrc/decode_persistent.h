@@ -27,11 +27,13 @@ struct PersistentArgs {
   // the attention's pointers stay in scalar registers).
   AttnArgs attn;
   long act_stride, cache_stride;
-  unsigned *bar;  // barrier counter, zero at launch (the embedding kernel clears it)
+  unsigned *bar;  // kPersistentBarWords words of barrier counters, zero at launch (the embedding kernel clears them)
   unsigned *err;  // set when a barrier wait gives up; never cleared by the kernel
 };
 
-constexpr int kPersistentBarWords = 16;
+// Barrier counters, each on its own 128-byte line.
+constexpr int kBarCounters = 16, kBarStride = 32;
+constexpr int kPersistentBarWords = kBarCounters * kBarStride;
 constexpr int kPersistentThreads = 512;
 constexpr size_t kCuLds = 160 * 1024;  // LDS per CU on gfx950
 // The dynamic LDS request is at least this, so no CU holds two workgroups.
