@@ -75,7 +75,14 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
   const int wg = blockIdx.x, nwg = gridDim.x;
   const int wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
   const int pos = bounded_pos(p.attn.pos, p.attn.max_seq);
-  const int n_items = p.attn.nh * (pos / kChunk + 1);
+  // Attention items: the G query heads that share a (KV head, chunk) run on
+  // workgroups of one XCD (workgroup w sits on XCD w % 8), so the chunk's keys
+  // and values come from HBM once and from that XCD's L2 for the other heads.
+  // Item i: XCD x = i % 8, r = i / 8, head j = r % G of pair q * 8 + x with
+  // q = r / G; pair = chunk * nkv + kv head.
+  const int G = p.attn.nh / p.attn.nkv;
+  const int n_pairs = p.attn.nkv * (pos / kChunk + 1);
+  const int n_items = (n_pairs + 7) / 8 * 8 * G;
   unsigned k = 0;
   for (int l = 0; l < p.nlayers; l++) {
     // Through the constant address space: the arguments are never written
@@ -100,8 +107,12 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
       a.k_cache += l * p.cache_stride;
       a.v_cache += l * p.cache_stride;
       bar_wait(p.bar, p.err, nwg, k);
-      for (int it = wave * nwg + wg; it < n_items; it += nwg * nwv)
-        attention_item<HD, true>(a, it % a.nh, it / a.nh, pos, aqs[wave], akn[wave]);
+      for (int it = wave * nwg + wg; it < n_items; it += nwg * nwv) {
+        const int r = it >> 3, pair = (r / G) * 8 + (it & 7);
+        if (pair < n_pairs)
+          attention_item<HD, true>(a, (pair % a.nkv) * G + r % G, pair / a.nkv, pos, aqs[wave],
+                                   akn[wave]);
+      }
       bar_arrive(p.bar, wg);
       k++;
     }

@@ -80,10 +80,12 @@ def test_head_dim_64_and_gqa_7(llrs, backend, oracle, tmp_path):
 
 def test_head_dim_128_long_context(llrs, backend, oracle, tmp_path):
     """7B-like head_dim 128 over a 330-token context: six attention chunks,
-    the current position appended mid-chunk, partials merged across chunks."""
+    the current position appended mid-chunk, partials merged across chunks.
+    (Seed 24: the oracle's top-2 logit gap stays above 6e-3 on every step, far
+    above the logit error, so greedy ties cannot flip a token.)"""
     cfg = tiny_cfg(llrs, hidden_size=1024, num_attention_heads=8, num_key_value_heads=2,
-                   intermediate_size=1024, num_hidden_layers=1, vocab_size=600, seed=21)
-    prompt = np.random.default_rng(21).integers(0, cfg.vocab_size, 300).astype(np.uint32)
+                   intermediate_size=1024, num_hidden_layers=1, vocab_size=600, seed=24)
+    prompt = np.random.default_rng(24).integers(0, cfg.vocab_size, 300).astype(np.uint32)
     compare_run(llrs, backend, oracle, cfg, tmp_path / "l.gguf", prompt, 32, 512)
 
 
