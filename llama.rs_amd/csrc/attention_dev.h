@@ -221,6 +221,14 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
   const int d0 = (lane % VL) * VW;
   for (int cb = 0; cb < n_active; cb += 64) {
     const int nc = min(64, n_active - cb);
+    // The round's statistics and its first 32 O partials load together.
+    float ov[32][VW];
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      const float *pc = base + (size_t)(cb + min(j, nc - 1)) * stride + d0;
+#pragma unroll
+      for (int k = 0; k < VW; k++) ov[j][k] = load_dev(pc + k);
+    }
     const float *pcl = base + (size_t)(cb + min(lane, nc - 1)) * stride;
     const float mm = load_dev(pcl + 2 * HD), ll = load_dev(pcl + 2 * HD + 1);
     const bool in = lane < nc && mm != -INFINITY;
@@ -235,12 +243,13 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
 #pragma unroll
     for (int k = 0; k < VW; k++) Rr[k] = 0.f;
     for (int jb = 0; jb < nc; jb += 32) {
-      float ov[32][VW];
+      if (jb > 0) {
 #pragma unroll
-      for (int j = 0; j < 32; j++) {
-        const float *pc = base + (size_t)(cb + min(jb + j, nc - 1)) * stride + d0;
+        for (int j = 0; j < 32; j++) {
+          const float *pc = base + (size_t)(cb + min(jb + j, nc - 1)) * stride + d0;
 #pragma unroll
-        for (int k = 0; k < VW; k++) ov[j][k] = load_dev(pc + k);
+          for (int k = 0; k < VW; k++) ov[j][k] = load_dev(pc + k);
+        }
       }
 #pragma unroll
       for (int j = 0; j < 32; j++) {
