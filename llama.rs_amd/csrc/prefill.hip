@@ -3,11 +3,13 @@
 // way Qwen2Model::forward_impl, src/model.rs:135-271, computes one token).
 //
 // The weight matrices run as MFMA dequant-GEMMs: a workgroup owns a 64-token x
-// 64-row output tile.  It dequantizes its 64 weight rows 128 columns at a time
-// from the native GGUF blocks (value_at, src/quant.rs:349-456) into LDS,
+// 128-row output tile.  It dequantizes its 128 weight rows 64 columns at a
+// time from the native GGUF blocks (value_at, src/quant.rs:349-456) into LDS,
 // stages the matching activation tile, and accumulates
-// v_mfma_f32_16x16x32_f16 products in f32.  Each wave holds a 32 x 32 quarter
-// of the tile (2 x 2 MFMA blocks).
+// v_mfma_f32_16x16x32_f16 products in f32.  Each wave holds a 32 x 64 quarter
+// of the tile (2 x 4 MFMA blocks).  The raw weight blocks and activations of
+// the next 64 columns are loaded into registers before the current ones are
+// multiplied, so the loads' latency hides behind the MFMAs.
 //
 // Precision: f32 operands are carried as f16 pairs, v = hi + lo with hi =
 // f16(v) and lo = f16(v - hi) (22 significant bits), and each product is
@@ -28,28 +30,50 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 64, BN = 64, KC = 128, LS = KC + 8;  // LS: LDS row stride in halves
+constexpr int BM = 64, BN = 128, KC = 64, LS = KC + 8;  // LS: LDS row stride in halves
 
 // The 32 values of `row` at columns [k0, k0 + 32) (k0 a multiple of 32), as
-// value_at computes them.
+// value_at computes them, in two stages: load() issues the loads of the raw
+// block bytes, decode() turns them into values once they have arrived.
 template <uint32_t TY> struct Deq {
-  static __device__ __forceinline__ void run(const uint8_t *row, uint32_t ty, int k0, float (&v)[32]) {
+  struct Raw { const uint8_t *row; uint32_t ty; };
+  static __device__ __forceinline__ void load(const uint8_t *row, uint32_t ty, int, Raw &r) {
+    r.row = row;
+    r.ty = ty;
+  }
+  static __device__ __forceinline__ void decode(const Raw &r, int k0, float (&v)[32]) {
 #pragma unroll
-    for (int j = 0; j < 32; j++) v[j] = value_dev(row, ty, (uint32_t)(k0 + j));
+    for (int j = 0; j < 32; j++) v[j] = value_dev(r.row, r.ty, (uint32_t)(k0 + j));
   }
 };
 
+// Byte i of the little-endian words w.
+__device__ __forceinline__ int byte_of(const uint32_t *w, int i) { return (int)((w[i >> 2] >> (8 * (i & 3))) & 0xff); }
+
 template <> struct Deq<LLRS_Q4_K> {
-  static __device__ __forceinline__ void run(const uint8_t *row, uint32_t, int k0, float (&v)[32]) {
-#pragma clang fp contract(off)
+  struct Raw { uint4 hdr, q0, q1; };  // d, dmin, 12 scale bytes; the sub-block's 32 quant bytes
+  static __device__ __forceinline__ void load(const uint8_t *row, uint32_t, int k0, Raw &r) {
     const uint8_t *b = row + (size_t)(k0 >> 8) * 144;
     const int g = (k0 & 255) >> 5;
-    int sc, mn;
-    scale_min_k4(g, b + 4, sc, mn);
-    const float ds = ld_f16(b) * (float)sc, dm = ld_f16(b + 2) * (float)mn;
-    const uint4 q0 = *reinterpret_cast<const uint4 *>(b + 16 + (g >> 1) * 32);
-    const uint4 q1 = *reinterpret_cast<const uint4 *>(b + 32 + (g >> 1) * 32);
-    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    r.hdr = *reinterpret_cast<const uint4 *>(b);
+    r.q0 = *reinterpret_cast<const uint4 *>(b + 16 + (g >> 1) * 32);
+    r.q1 = *reinterpret_cast<const uint4 *>(b + 32 + (g >> 1) * 32);
+  }
+  static __device__ __forceinline__ void decode(const Raw &r, int k0, float (&v)[32]) {
+#pragma clang fp contract(off)
+    const int g = (k0 & 255) >> 5;
+    const uint32_t s[3] = {r.hdr.y, r.hdr.z, r.hdr.w};
+    int sc, mn;  // scale_min_k4 (src/quant.rs:338-347) on the scale bytes in registers
+    if (g < 4) {
+      sc = byte_of(s, g) & 63;
+      mn = byte_of(s, g + 4) & 63;
+    } else {
+      sc = (byte_of(s, g + 4) & 0x0f) | ((byte_of(s, g - 4) >> 6) << 4);
+      mn = (byte_of(s, g + 4) >> 4) | ((byte_of(s, g) >> 6) << 4);
+    }
+    const float ds = f16_bits_to_f32((uint16_t)(r.hdr.x & 0xffff)) * (float)sc;
+    const float dm = f16_bits_to_f32((uint16_t)(r.hdr.x >> 16)) * (float)mn;
+    const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
     const int shift = (g & 1) * 4;
 #pragma unroll
     for (int j = 0; j < 32; j++) {
@@ -60,19 +84,23 @@ template <> struct Deq<LLRS_Q4_K> {
 };
 
 template <> struct Deq<LLRS_Q6_K> {
-  static __device__ __forceinline__ void run(const uint8_t *row, uint32_t, int k0, float (&v)[32]) {
-#pragma clang fp contract(off)
+  struct Raw { uint32_t ql[9], qh[9], shl, shh; uint16_t s2, d; };
+  static __device__ __forceinline__ void load(const uint8_t *row, uint32_t, int k0, Raw &r) {
     const uint8_t *b = row + (size_t)(k0 >> 8) * 210;
     const int j0 = k0 & 255, half = j0 >> 7, quarter = (j0 >> 5) & 3;
-    uint32_t ql[9], qh[9], shl, shh;
-    load9(b + half * 64 + (quarter & 1) * 32, ql, shl);
-    load9(b + 128 + half * 32, qh, shh);
-    const uint16_t s2 = ld_u16(b + 192 + half * 8 + quarter * 2);
-    const float d = ld_f16(b + 208);
-    const float sc0 = d * (float)(int8_t)(s2 & 0xff), sc1 = d * (float)(int8_t)(s2 >> 8);
+    load9(b + half * 64 + (quarter & 1) * 32, r.ql, r.shl);
+    load9(b + 128 + half * 32, r.qh, r.shh);
+    r.s2 = ld_u16(b + 192 + half * 8 + quarter * 2);
+    r.d = ld_u16(b + 208);
+  }
+  static __device__ __forceinline__ void decode(const Raw &r, int k0, float (&v)[32]) {
+#pragma clang fp contract(off)
+    const int quarter = (k0 >> 5) & 3;
+    const float d = f16_bits_to_f32(r.d);
+    const float sc0 = d * (float)(int8_t)(r.s2 & 0xff), sc1 = d * (float)(int8_t)(r.s2 >> 8);
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-      const uint32_t l = realign(ql, k, shl), h = realign(qh, k, shh);
+      const uint32_t l = realign(r.ql, k, r.shl), h = realign(r.qh, k, r.shh);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int lb = (int)((l >> (8 * e)) & 0xff);
@@ -86,14 +114,17 @@ template <> struct Deq<LLRS_Q6_K> {
 };
 
 template <> struct Deq<LLRS_Q8_0> {
-  static __device__ __forceinline__ void run(const uint8_t *row, uint32_t, int k0, float (&v)[32]) {
+  struct Raw { uint32_t q[9], sh; uint16_t d; };
+  static __device__ __forceinline__ void load(const uint8_t *row, uint32_t, int k0, Raw &r) {
     const uint8_t *b = row + (size_t)(k0 >> 5) * 34;
-    uint32_t q[9], sh;
-    load9(b + 2, q, sh);
-    const float d = ld_f16(b);
+    load9(b + 2, r.q, r.sh);
+    r.d = ld_u16(b);
+  }
+  static __device__ __forceinline__ void decode(const Raw &r, int, float (&v)[32]) {
+    const float d = f16_bits_to_f32(r.d);
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-      const uint32_t w = realign(q, k, sh);
+      const uint32_t w = realign(r.q, k, r.sh);
 #pragma unroll
       for (int e = 0; e < 4; e++) v[4 * k + e] = d * (float)(int8_t)((w >> (8 * e)) & 0xff);
     }
@@ -101,16 +132,19 @@ template <> struct Deq<LLRS_Q8_0> {
 };
 
 template <> struct Deq<LLRS_Q5_0> {
-  static __device__ __forceinline__ void run(const uint8_t *row, uint32_t, int k0, float (&v)[32]) {
-#pragma clang fp contract(off)
+  struct Raw { uint32_t r[9], sh; uint16_t d; };  // qh (4 bytes) then 16 bytes of nibbles
+  static __device__ __forceinline__ void load(const uint8_t *row, uint32_t, int k0, Raw &r) {
     const uint8_t *b = row + (size_t)(k0 >> 5) * 22;
-    uint32_t r[9], sh;
-    load9(b + 2, r, sh);  // qh (4 bytes) then 16 bytes of nibbles
-    const uint32_t qh = realign(r, 0, sh);
-    const float d = ld_f16(b);
+    load9(b + 2, r.r, r.sh);
+    r.d = ld_u16(b);
+  }
+  static __device__ __forceinline__ void decode(const Raw &r, int, float (&v)[32]) {
+#pragma clang fp contract(off)
+    const uint32_t qh = realign(r.r, 0, r.sh);
+    const float d = f16_bits_to_f32(r.d);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      const uint32_t w = realign(r, k + 1, sh);
+      const uint32_t w = realign(r.r, k + 1, r.sh);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int j = 4 * k + e;
@@ -132,57 +166,72 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
   extern __shared__ __align__(16) f16 lds[];
   f16 *As = lds, *Al = As + BM * LS, *Ws = Al + BM * LS, *Wl = Ws + BN * LS;
   const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM;
+  // This workgroup's K range (split K: whole KC chunks per split).
+  const int per = ((g.k + KC - 1) / KC + g.ksplit - 1) / g.ksplit * KC;
+  const int kb = blockIdx.z * per, ke = min(g.k, kb + per);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  f32x4 acc[2][2];
+  const int wm = wave >> 1, wn = wave & 1;  // the wave's 32-token x 64-row quarter
+  f32x4 acc[2][4];
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int wr = tid >> 2, wsub = tid & 3;  // this thread's weight row and 32-column run
-  const bool wrow_ok = n0 + wr < g.n;
-  const uint8_t *wrow = g.w + (size_t)(wrow_ok ? n0 + wr : 0) * g.row_bytes;
-  for (int k0 = 0; k0 < g.k; k0 += KC) {
-    const int kc = min(KC, g.k - k0);  // a multiple of 32
+  // Staging roles: activations 64 rows x 4 runs of 16 halves, weights 128
+  // rows x 2 runs of 32 values.  Rows past the tile's end read row 0 and are
+  // zeroed on their way into LDS.
+  const int ar = tid >> 2, ac = (tid & 3) * 16;
+  const int wr = tid >> 1, wc = (tid & 1) * 32;
+  const bool a_ok = t0 + ar < g.t, w_ok = n0 + wr < g.n;
+  const size_t aoff = (size_t)(a_ok ? t0 + ar : 0) * g.lda + ac;
+  const uint8_t *wrow = g.w + (size_t)(w_ok ? n0 + wr : 0) * g.row_bytes;
+  half8 ah[2], alo[2];
+  typename Deq<TY>::Raw raw;
+  auto load_chunk = [&](int k0) {
+    const int kk = min(k0 + ac, ke - 16);  // columns past the range: a valid read, zeroed below
 #pragma unroll
-    for (int q = 0; q < 4; q++) {  // activations: 64 rows x 16 chunks of 8 halves
-      const int i = tid + 256 * q, r = i >> 4, c8 = i & 15;
-      half8 hv = half8{0, 0, 0, 0, 0, 0, 0, 0}, lv = hv;
-      if (t0 + r < g.t && c8 * 8 < kc) {
-        const size_t off = (size_t)(t0 + r) * g.lda + k0 + c8 * 8;
-        hv = *reinterpret_cast<const half8 *>(g.a + off);
-        lv = *reinterpret_cast<const half8 *>(g.a_lo + off);
+    for (int h = 0; h < 2; h++) {
+      ah[h] = *reinterpret_cast<const half8 *>(g.a + aoff - ac + kk + 8 * h);
+      alo[h] = *reinterpret_cast<const half8 *>(g.a_lo + aoff - ac + kk + 8 * h);
+    }
+    Deq<TY>::load(wrow, g.type, min(k0 + wc, ke - 32), raw);
+  };
+  if (kb >= ke) return;
+  load_chunk(kb);
+  for (int k0 = kb; k0 < ke; k0 += KC) {
+    const int kc = min(KC, ke - k0);  // 32 or 64
+    __syncthreads();  // the previous chunk's MFMAs have read LDS
+    {
+      const bool in = a_ok && ac < kc;
+      const half8 z = half8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        *reinterpret_cast<half8 *>(As + ar * LS + ac + 8 * h) = in ? ah[h] : z;
+        *reinterpret_cast<half8 *>(Al + ar * LS + ac + 8 * h) = in ? alo[h] : z;
       }
-      *reinterpret_cast<half8 *>(As + r * LS + c8 * 8) = hv;
-      *reinterpret_cast<half8 *>(Al + r * LS + c8 * 8) = lv;
     }
     {
-      const int kk = k0 + 32 * wsub;
       float v[32];
-      if (wrow_ok && kk < g.k) {
-        Deq<TY>::run(wrow, g.type, kk, v);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 32; j++) v[j] = 0.f;
-      }
+      Deq<TY>::decode(raw, min(k0 + wc, ke - 32), v);  // the columns load_chunk read
+      const bool in = w_ok && wc < kc;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         half8 h, l;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
           f16 a, b;
-          split_f16(v[8 * q + e], a, b);
+          split_f16(in ? v[8 * q + e] : 0.f, a, b);
           h[e] = a;
           l[e] = b;
         }
-        *reinterpret_cast<half8 *>(Ws + wr * LS + 32 * wsub + 8 * q) = h;
-        *reinterpret_cast<half8 *>(Wl + wr * LS + 32 * wsub + 8 * q) = l;
+        *reinterpret_cast<half8 *>(Ws + wr * LS + wc + 8 * q) = h;
+        *reinterpret_cast<half8 *>(Wl + wr * LS + wc + 8 * q) = l;
       }
     }
     __syncthreads();
+    if (k0 + KC < ke) load_chunk(k0 + KC);  // in flight during the MFMAs below
     for (int ks = 0; ks < kc; ks += 32) {
-      half8 af[2], al[2], bf[2], bl[2];
+      half8 af[2], al[2], bf[4], bl[4];
 #pragma unroll
       for (int i = 0; i < 2; i++) {
         const int o = (wm * 32 + 16 * i + (lane & 15)) * LS + ks + 8 * (lane >> 4);
@@ -190,28 +239,27 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
         al[i] = *reinterpret_cast<const half8 *>(Al + o);
       }
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const int o = (wn * 32 + 16 * j + (lane & 15)) * LS + ks + 8 * (lane >> 4);
+      for (int j = 0; j < 4; j++) {
+        const int o = (wn * 64 + 16 * j + (lane & 15)) * LS + ks + 8 * (lane >> 4);
         bf[j] = *reinterpret_cast<const half8 *>(Ws + o);
         bl[j] = *reinterpret_cast<const half8 *>(Wl + o);
       }
 #pragma unroll
       for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < 4; j++) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bf[j], acc[i][j], 0, 0, 0);
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bl[j], acc[i][j], 0, 0, 0);
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
     }
-    __syncthreads();
   }
   // D layout: lane holds column (lane & 15) and rows 4 * (lane >> 4) + e.
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int n = n0 + wn * 32 + 16 * j + (lane & 15);
+    for (int j = 0; j < 4; j++) {
+      const int n = n0 + wn * 64 + 16 * j + (lane & 15);
       if (n >= g.n) continue;
       const float bias = (!g.accumulate && g.bias) ? g.bias[n] : 0.f;
 #pragma unroll
@@ -219,7 +267,10 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
         const int t = t0 + wm * 32 + 16 * i + 4 * (lane >> 4) + e;
         if (t >= g.t) continue;
         float *c = g.c + (size_t)t * g.ldc + n;
-        *c = g.accumulate ? *c + acc[i][j][e] : acc[i][j][e] + bias;
+        if (g.ksplit > 1)
+          atomicAdd(c, acc[i][j][e]);
+        else
+          *c = g.accumulate ? *c + acc[i][j][e] : acc[i][j][e] + bias;
       }
     }
 }
@@ -407,14 +458,21 @@ int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
   if (g.k % 32 || g.lda % 8 || g.n <= 0 || g.k <= 0 || g.t <= 0)
     return set_error(LLRS_E_UNSUPPORTED, "prefill GEMM shape %d x %d (lda %d) is not supported", g.n,
                      g.k, g.lda);
-  const dim3 grid((unsigned)((g.n + BN - 1) / BN), (unsigned)((g.t + BM - 1) / BM));
+  PrefillGemmArgs a = g;
+  // Accumulating products (o_proj, ffn_down) with fewer tiles than two per CU
+  // split K over up to 4 workgroups that add into C atomically.
+  const int tiles = ((g.n + BN - 1) / BN) * ((g.t + BM - 1) / BM), chunks = (g.k + KC - 1) / KC;
+  a.ksplit = 1;
+  if (g.accumulate)
+    while (a.ksplit < 4 && tiles * a.ksplit < 512 && chunks >= 16 * a.ksplit * 2) a.ksplit *= 2;
+  const dim3 grid((unsigned)((g.n + BN - 1) / BN), (unsigned)((g.t + BM - 1) / BM), (unsigned)a.ksplit);
   const size_t lds = (size_t)2 * (BM + BN) * LS * sizeof(f16);
-  switch (g.type) {
-    case LLRS_Q4_K: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q4_K>, grid, dim3(256), lds, s, g); break;
-    case LLRS_Q6_K: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q6_K>, grid, dim3(256), lds, s, g); break;
-    case LLRS_Q8_0: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q8_0>, grid, dim3(256), lds, s, g); break;
-    case LLRS_Q5_0: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q5_0>, grid, dim3(256), lds, s, g); break;
-    default: hipLaunchKernelGGL(prefill_gemm_kernel<0xffffffffu>, grid, dim3(256), lds, s, g); break;
+  switch (a.type) {
+    case LLRS_Q4_K: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q4_K>, grid, dim3(256), lds, s, a); break;
+    case LLRS_Q6_K: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q6_K>, grid, dim3(256), lds, s, a); break;
+    case LLRS_Q8_0: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q8_0>, grid, dim3(256), lds, s, a); break;
+    case LLRS_Q5_0: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q5_0>, grid, dim3(256), lds, s, a); break;
+    default: hipLaunchKernelGGL(prefill_gemm_kernel<0xffffffffu>, grid, dim3(256), lds, s, a); break;
   }
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;
