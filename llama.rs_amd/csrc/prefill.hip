@@ -30,7 +30,7 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 64, BN = 128, KC = 64, LS = KC + 8;  // LS: LDS row stride in halves
+constexpr int BN = 128, KC = 64, LS = KC + 8;  // weight rows per tile; LS: LDS row stride in halves
 
 // The 32 values of `row` at columns [k0, k0 + 32) (k0 a multiple of 32), as
 // value_at computes them, in two stages: load() issues the loads of the raw
@@ -161,8 +161,12 @@ __device__ __forceinline__ void split_f16(float v, f16 &hi, f16 &lo) {
   lo = (f16)(v - (float)hi);
 }
 
-template <uint32_t TY>
+// BM tokens x BN weight rows per workgroup (BM = 64 or 128).
+template <uint32_t TY, int BM>
 __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
+  constexpr int MI = BM / 32;    // 16-token MFMA blocks per wave
+  constexpr int APT = BM / 4;    // activation halves per thread and plane
+  constexpr int TPR = 64 / APT;  // threads per activation row
   extern __shared__ __align__(16) f16 lds[];
   f16 *As = lds, *Al = As + BM * LS, *Ws = Al + BM * LS, *Wl = Ws + BN * LS;
   const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM;
@@ -170,27 +174,27 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
   const int per = ((g.k + KC - 1) / KC + g.ksplit - 1) / g.ksplit * KC;
   const int kb = blockIdx.z * per, ke = min(g.k, kb + per);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;  // the wave's 32-token x 64-row quarter
-  f32x4 acc[2][4];
+  const int wm = wave >> 1, wn = wave & 1;  // the wave's (BM/2)-token x 64-row quarter
+  f32x4 acc[MI][4];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < MI; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Staging roles: activations 64 rows x 4 runs of 16 halves, weights 128
+  // Staging roles: activations BM rows x TPR runs of APT halves, weights 128
   // rows x 2 runs of 32 values.  Rows past the tile's end read row 0 and are
   // zeroed on their way into LDS.
-  const int ar = tid >> 2, ac = (tid & 3) * 16;
+  const int ar = tid / TPR, ac = (tid % TPR) * APT;
   const int wr = tid >> 1, wc = (tid & 1) * 32;
   const bool a_ok = t0 + ar < g.t, w_ok = n0 + wr < g.n;
   const size_t aoff = (size_t)(a_ok ? t0 + ar : 0) * g.lda + ac;
   const uint8_t *wrow = g.w + (size_t)(w_ok ? n0 + wr : 0) * g.row_bytes;
-  half8 ah[2], alo[2];
+  half8 ah[APT / 8], alo[APT / 8];
   typename Deq<TY>::Raw raw;
   auto load_chunk = [&](int k0) {
-    const int kk = min(k0 + ac, ke - 16);  // columns past the range: a valid read, zeroed below
+    const int kk = min(k0 + ac, ke - APT);  // columns past the range: a valid read, zeroed below
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
+    for (int h = 0; h < APT / 8; h++) {
       ah[h] = *reinterpret_cast<const half8 *>(g.a + aoff - ac + kk + 8 * h);
       alo[h] = *reinterpret_cast<const half8 *>(g.a_lo + aoff - ac + kk + 8 * h);
     }
@@ -205,7 +209,7 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
       const bool in = a_ok && ac < kc;
       const half8 z = half8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
+      for (int h = 0; h < APT / 8; h++) {
         *reinterpret_cast<half8 *>(As + ar * LS + ac + 8 * h) = in ? ah[h] : z;
         *reinterpret_cast<half8 *>(Al + ar * LS + ac + 8 * h) = in ? alo[h] : z;
       }
@@ -231,10 +235,10 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
     __syncthreads();
     if (k0 + KC < ke) load_chunk(k0 + KC);  // in flight during the MFMAs below
     for (int ks = 0; ks < kc; ks += 32) {
-      half8 af[2], al[2], bf[4], bl[4];
+      half8 af[MI], al[MI], bf[4], bl[4];
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        const int o = (wm * 32 + 16 * i + (lane & 15)) * LS + ks + 8 * (lane >> 4);
+      for (int i = 0; i < MI; i++) {
+        const int o = (wm * (BM / 2) + 16 * i + (lane & 15)) * LS + ks + 8 * (lane >> 4);
         af[i] = *reinterpret_cast<const half8 *>(As + o);
         al[i] = *reinterpret_cast<const half8 *>(Al + o);
       }
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
         bl[j] = *reinterpret_cast<const half8 *>(Wl + o);
       }
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bf[j], acc[i][j], 0, 0, 0);
@@ -256,7 +260,7 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
   }
   // D layout: lane holds column (lane & 15) and rows 4 * (lane >> 4) + e.
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < MI; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int n = n0 + wn * 64 + 16 * j + (lane & 15);
@@ -264,7 +268,7 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
       const float bias = (!g.accumulate && g.bias) ? g.bias[n] : 0.f;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        const int t = t0 + wm * 32 + 16 * i + 4 * (lane >> 4) + e;
+        const int t = t0 + wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + e;
         if (t >= g.t) continue;
         float *c = g.c + (size_t)t * g.ldc + n;
         if (g.ksplit > 1)
@@ -459,21 +463,31 @@ int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
     return set_error(LLRS_E_UNSUPPORTED, "prefill GEMM shape %d x %d (lda %d) is not supported", g.n,
                      g.k, g.lda);
   PrefillGemmArgs a = g;
-  // Accumulating products (o_proj, ffn_down) with fewer tiles than two per CU
-  // split K over up to 4 workgroups that add into C atomically.
-  const int tiles = ((g.n + BN - 1) / BN) * ((g.t + BM - 1) / BM), chunks = (g.k + KC - 1) / KC;
+  // 128-token tiles when there are enough of them (the dequantized weight
+  // tile then serves twice the tokens), else 64.  Accumulating products
+  // (o_proj, ffn_down) with fewer tiles than two per CU split K over up to 4
+  // workgroups that add into C atomically.
+  const int ntiles = (g.n + BN - 1) / BN;
+  const int bm = (g.t >= 256 && ntiles >= 64) ? 128 : 64;
+  const int tiles = ntiles * ((g.t + bm - 1) / bm), chunks = (g.k + KC - 1) / KC;
   a.ksplit = 1;
   if (g.accumulate)
     while (a.ksplit < 4 && tiles * a.ksplit < 512 && chunks >= 16 * a.ksplit * 2) a.ksplit *= 2;
-  const dim3 grid((unsigned)((g.n + BN - 1) / BN), (unsigned)((g.t + BM - 1) / BM), (unsigned)a.ksplit);
-  const size_t lds = (size_t)2 * (BM + BN) * LS * sizeof(f16);
+  const dim3 grid((unsigned)ntiles, (unsigned)((g.t + bm - 1) / bm), (unsigned)a.ksplit);
+  const size_t lds = (size_t)2 * (bm + BN) * LS * sizeof(f16);
+#define GEMM(T)                                                                        \
+  if (bm == 128)                                                                       \
+    hipLaunchKernelGGL((prefill_gemm_kernel<T, 128>), grid, dim3(256), lds, s, a);     \
+  else                                                                                 \
+    hipLaunchKernelGGL((prefill_gemm_kernel<T, 64>), grid, dim3(256), lds, s, a);
   switch (a.type) {
-    case LLRS_Q4_K: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q4_K>, grid, dim3(256), lds, s, a); break;
-    case LLRS_Q6_K: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q6_K>, grid, dim3(256), lds, s, a); break;
-    case LLRS_Q8_0: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q8_0>, grid, dim3(256), lds, s, a); break;
-    case LLRS_Q5_0: hipLaunchKernelGGL(prefill_gemm_kernel<LLRS_Q5_0>, grid, dim3(256), lds, s, a); break;
-    default: hipLaunchKernelGGL(prefill_gemm_kernel<0xffffffffu>, grid, dim3(256), lds, s, a); break;
+    case LLRS_Q4_K: GEMM(LLRS_Q4_K) break;
+    case LLRS_Q6_K: GEMM(LLRS_Q6_K) break;
+    case LLRS_Q8_0: GEMM(LLRS_Q8_0) break;
+    case LLRS_Q5_0: GEMM(LLRS_Q5_0) break;
+    default: GEMM(0xffffffffu) break;
   }
+#undef GEMM
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;
 }

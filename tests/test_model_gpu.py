@@ -97,6 +97,15 @@ def test_gqa_16_head_dim_32(llrs, backend, oracle, tmp_path):
     compare_run(llrs, backend, oracle, cfg, tmp_path / "g.gguf", prompt, 32, 128)
 
 
+def test_prefill_128_token_tiles(llrs, backend, oracle, tmp_path):
+    """A 300-token prompt through FFN matrices of 8192 rows: the batched prefill
+    takes its 128-token GEMM tiles there (64-token tiles elsewhere) and still
+    matches the oracle."""
+    cfg = tiny_cfg(llrs, intermediate_size=8192, num_hidden_layers=1, seed=31)
+    prompt = np.random.default_rng(31).integers(0, cfg.vocab_size, 300).astype(np.uint32)
+    compare_run(llrs, backend, oracle, cfg, tmp_path / "w.gguf", prompt, 8, 320)
+
+
 def test_forward_token_matches_prefill(llrs, backend, oracle, tmp_path, monkeypatch):
     """The batched (MFMA) prefill agrees with the token-by-token loop of
     CausalModel::prefill (src/architecture.rs:60-77) within the logits bar;
