@@ -17,7 +17,6 @@
 // the GEMM is close to an f32 GEMM rather than an f16 one.
 #include <hip/hip_runtime.h>
 
-#include <type_traits>
 
 #include "common.h"
 #include "prefill.h"
@@ -342,105 +341,143 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float *__restrict__ q,
   for (int i = threadIdx.x; i < kvw; i += blockDim.x) vd[i] = vr[i];
 }
 
-// Causal GQA attention of one query row and head (src/model.rs:206-231,
-// softmax_inplace 298-313): one wave walks the positions 0..start+t in chunks
-// of 32 (lane = half of the head x position for the scores, VW dims per lane
-// for the values) and folds them with a running max; the uniform fallback
-// applies when no finite positive total remains.
+// Causal GQA attention (src/model.rs:206-231, softmax_inplace 298-313) for a
+// tile of 16 query rows of one head, on f32 matrix cores: fp32 products and
+// sums as the scalar loop has them, in another order.  The four waves take
+// every fourth 16-key block of the causal range and keep a running max;
+// their partial states are merged through LDS at the end.
+//
+// Both products keep the query index in lane % 16, so neither the scores nor
+// the weights move between lanes:
+//   S^T (keys x queries) = K Q^T     A = K rows, B = Q rows, contraction over
+//                                    the head dims (lane group g holds dims
+//                                    g*HD/4 ... g*HD/4 + HD/4 - 1)
+//   O^T (dims x queries) = V^T P^T   A = V, B = the lane's own weights (the
+//                                    score registers r = key 4g + r)
+// and O^T's rows come out as dims (4g + r) * HD/16 + t for tile t: each lane
+// ends with HD/4 consecutive dims of its query.  Keys past a query's position
+// weigh 0 and their V rows are clamped to rows the tile may read.  The
+// uniform fallback applies when no finite positive total remains.
 template <int HD>
-__global__ __launch_bounds__(64) void attention_rows_kernel(const float *__restrict__ q,
-                                                            const float *__restrict__ k_cache,
-                                                            const float *__restrict__ v_cache,
-                                                            int start, int nh, int nkv, float scale,
-                                                            f16 *__restrict__ out,
-                                                            f16 *__restrict__ out_lo) {
-  constexpr int KH = HD / 2, NK4 = KH / 4;
-  constexpr int VW = HD >= 64 ? HD / 64 : 1, VL = HD / VW, RV = 64 / VL, NVI = 32 / RV;
-  using VT = typename std::conditional<VW == 2, float2, float>::type;
-  const int t = blockIdx.x, h = blockIdx.y, G = nh / nkv, kvh = h / G, kvw = nkv * HD;
-  const int p = start + t;
-  const int lane = threadIdx.x, half = lane >> 5, pl = lane & 31;
-  const int vd = (lane % VL) * VW, vr0 = lane / VL;
-  float4 qr[NK4];
+__global__ __launch_bounds__(256) void attention_tile_kernel(const float *__restrict__ q,
+                                                             const float *__restrict__ k_cache,
+                                                             const float *__restrict__ v_cache,
+                                                             int T, int start, int nh, int nkv,
+                                                             float scale, f16 *__restrict__ out,
+                                                             f16 *__restrict__ out_lo) {
+  constexpr int DPL = HD / 4;  // head dims per lane in S (32 contraction steps at 128)
+  constexpr int NT = HD / 16;  // 16-dim output tiles of O^T
+  __shared__ float so[4][16][HD + 4];
+  __shared__ float sm[4][16], sl[4][16];
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * 16;  // the longest tiles start first
+  const int h = blockIdx.y, kvh = h / (nh / nkv), kvw = nkv * HD;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+  const int pmax = start + min(q0 + 15, T - 1);
+  const int pq = start + min(q0 + i, T - 1);  // rows past T mask as the last row
+  float qv[DPL];
   {
-    const float *qp = q + (size_t)t * nh * HD + h * HD + half * KH;
+    const float *qp = q + (size_t)min(q0 + i, T - 1) * nh * HD + h * HD + g * DPL;
 #pragma unroll
-    for (int j = 0; j < NK4; j++) qr[j] = *reinterpret_cast<const float4 *>(qp + 4 * j);
+    for (int d = 0; d < DPL; d += 4) *reinterpret_cast<float4 *>(qv + d) = *reinterpret_cast<const float4 *>(qp + d);
   }
-  const float *kc = k_cache + (size_t)kvh * HD, *vc = v_cache + (size_t)kvh * HD;
-  float M = -INFINITY, L = 0.f, O[VW], Vs[VW];
+  const float *kc = k_cache + (size_t)kvh * HD + g * DPL;
+  const float *vc = v_cache + (size_t)kvh * HD + i * NT;
+  f32x4 o[NT];
 #pragma unroll
-  for (int e = 0; e < VW; e++) O[e] = Vs[e] = 0.f;
-  for (int c0 = 0; c0 <= p; c0 += 32) {
-    const int c1 = min(c0 + 32, p + 1);
-    float4 kr[NK4];
+  for (int t = 0; t < NT; t++) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float M = -INFINITY, L = 0.f;
+  const int nb = pmax / 16 + 1;
+  for (int b = wave; b < nb; b += 4) {
+    const int key0 = b * 16;
+    float kk[DPL];
     {
-      const float *kp = kc + (size_t)(c0 + pl < c1 ? c0 + pl : c0) * kvw + half * KH;
+      const float *kp = kc + (size_t)min(key0 + i, pmax) * kvw;
 #pragma unroll
-      for (int j = 0; j < NK4; j++) kr[j] = *reinterpret_cast<const float4 *>(kp + 4 * j);
+      for (int d = 0; d < DPL; d += 4) *reinterpret_cast<float4 *>(kk + d) = *reinterpret_cast<const float4 *>(kp + d);
     }
-    VT vv[NVI];
+    float vv[4][NT];
 #pragma unroll
-    for (int i = 0; i < NVI; i++) {
-      const int pp = c0 + i * RV + vr0;
-      vv[i] = *reinterpret_cast<const VT *>(vc + (size_t)(pp < c1 ? pp : c0) * kvw + vd);
-    }
-    float s = 0.f;
+    for (int s = 0; s < 4; s++) {
+      const float *vp = vc + (size_t)min(key0 + 4 * g + s, pmax) * kvw;
 #pragma unroll
-    for (int j = 0; j < NK4; j++)
-      s += qr[j].x * kr[j].x + qr[j].y * kr[j].y + qr[j].z * kr[j].z + qr[j].w * kr[j].w;
-    s += __shfl_xor(s, 32, 64);
-    const bool valid = c0 + pl < c1;
-    s = valid ? s * scale : -INFINITY;
-    float mc = s;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o, 64));
-    const float x = valid ? expf(s - mc) : 0.f;
-    float lc = x;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) lc += __shfl_xor(lc, o, 64);
-    float Oc[VW];
-#pragma unroll
-    for (int e = 0; e < VW; e++) Oc[e] = 0.f;
-#pragma unroll
-    for (int i = 0; i < NVI; i++) {
-      const int pp = i * RV + vr0;
-      float wp;
-      if constexpr (RV == 1)
-        wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i));
-      else
-        wp = __shfl(x, pp, 64);
-      const float in = c0 + pp < c1 ? 1.f : 0.f;
-      const float *ev = reinterpret_cast<const float *>(&vv[i]);
-#pragma unroll
-      for (int e = 0; e < VW; e++) {
-        Oc[e] += wp * ev[e];
-        Vs[e] += in * ev[e];
+      for (int t = 0; t < NT; t += (NT >= 4 ? 4 : NT)) {
+        if constexpr (NT >= 4)
+          *reinterpret_cast<float4 *>(&vv[s][t]) = *reinterpret_cast<const float4 *>(vp + t);
+        else if constexpr (NT == 2)
+          *reinterpret_cast<float2 *>(&vv[s][t]) = *reinterpret_cast<const float2 *>(vp + t);
+        else
+          vv[s][t] = vp[t];
       }
     }
+    f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int o = VL; o < 64; o <<= 1)
+    for (int d = 0; d < DPL; d++) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[d], qv[d], st, 0, 0, 0);
+    float sc[4], mc = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < VW; e++) Oc[e] += __shfl_xor(Oc[e], o, 64);
-    if (mc != -INFINITY) {
-      const float Mn = fmaxf(M, mc);
-      const float sa = expf(M - Mn), sb = expf(mc - Mn);
-      L = L * sa + lc * sb;
+    for (int r = 0; r < 4; r++) {
+      sc[r] = key0 + 4 * g + r <= pq ? st[r] * scale : -INFINITY;
+      mc = fmaxf(mc, sc[r]);
+    }
+    mc = fmaxf(mc, __shfl_xor(mc, 16, 64));
+    mc = fmaxf(mc, __shfl_xor(mc, 32, 64));
+    const float Mn = fmaxf(M, mc);
+    const bool live = Mn != -INFINITY;
+    const float alpha = live ? expf(M - Mn) : 1.f;
+    float pw[4], ls = 0.f;
 #pragma unroll
-      for (int e = 0; e < VW; e++) O[e] = O[e] * sa + Oc[e] * sb;
-      M = Mn;
+    for (int r = 0; r < 4; r++) {
+      pw[r] = live ? expf(sc[r] - Mn) : 0.f;
+      ls += pw[r];
+    }
+    L = L * alpha + ls;
+    M = Mn;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      o[t] *= alpha;
+#pragma unroll
+      for (int s = 0; s < 4; s++) o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[s][t], pw[s], o[t], 0, 0, 0);
     }
   }
+  L += __shfl_xor(L, 16, 64);
+  L += __shfl_xor(L, 32, 64);
+  if (g == 0) {
+    sm[wave][i] = M;
+    sl[wave][i] = L;
+  }
 #pragma unroll
-  for (int o = VL; o < 64; o <<= 1)
+  for (int t = 0; t < NT; t++)
 #pragma unroll
-    for (int e = 0; e < VW; e++) Vs[e] += __shfl_xor(Vs[e], o, 64);
-  if (lane < VL) {
-    const bool ok = isfinite(L) && L > 0.f;
-    const size_t at = (size_t)t * nh * HD + h * HD + vd;
+    for (int r = 0; r < 4; r++) so[wave][i][(4 * g + r) * NT + t] = o[t][r];
+  __syncthreads();
+  // Merge: thread -> query qi, dims c*NT ... c*NT + NT - 1.
+  const int qi = threadIdx.x >> 4, c = threadIdx.x & 15;
+  if (q0 + qi >= T) return;
+  float Mt = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < VW; e++)
-      split_f16(ok ? O[e] / L : Vs[e] / (float)(p + 1), out[at + e], out_lo[at + e]);
+  for (int w = 0; w < 4; w++) Mt = fmaxf(Mt, sm[w][qi]);
+  float Lt = 0.f, acc[NT];
+#pragma unroll
+  for (int e = 0; e < NT; e++) acc[e] = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    const float mw = sm[w][qi];
+    const float f = mw == -INFINITY ? 0.f : expf(mw - Mt);
+    Lt += sl[w][qi] * f;
+#pragma unroll
+    for (int e = 0; e < NT; e++) acc[e] += so[w][qi][c * NT + e] * f;
+  }
+  const int p = start + q0 + qi;
+  const size_t at = (size_t)(q0 + qi) * nh * HD + h * HD + c * NT;
+  if (isfinite(Lt) && Lt > 0.f) {
+#pragma unroll
+    for (int e = 0; e < NT; e++) split_f16(acc[e] / Lt, out[at + e], out_lo[at + e]);
+  } else {
+    const float *vp = v_cache + (size_t)kvh * HD + c * NT;
+    for (int e = 0; e < NT; e++) {
+      float vs = 0.f;
+      for (int j = 0; j <= p; j++) vs += vp[(size_t)j * kvw + e];
+      split_f16(vs / (float)(p + 1), out[at + e], out_lo[at + e]);
+    }
   }
 }
 
@@ -518,14 +555,20 @@ int launch_rope_append(float *q, const float *k, const float *v, const float *ro
 int launch_attention_rows(const float *q, const float *k_cache, const float *v_cache, int T,
                           int start, int nh, int nkv, int hd, float scale, f16 *out, f16 *out_lo,
                           hipStream_t s) {
-  const dim3 grid((unsigned)T, (unsigned)nh);
+  if (T <= 0 || nkv <= 0 || nh % nkv)
+    return set_error(LLRS_E_UNSUPPORTED, "attention over %d rows with %d/%d heads", T, nh, nkv);
+  const dim3 grid((unsigned)((T + 15) / 16), (unsigned)nh);
+#define ATT(D)                                                                                   \
+  hipLaunchKernelGGL(attention_tile_kernel<D>, grid, dim3(256), 0, s, q, k_cache, v_cache, T, start, \
+                     nh, nkv, scale, out, out_lo)
   switch (hd) {
-    case 16: hipLaunchKernelGGL(attention_rows_kernel<16>, grid, dim3(64), 0, s, q, k_cache, v_cache, start, nh, nkv, scale, out, out_lo); break;
-    case 32: hipLaunchKernelGGL(attention_rows_kernel<32>, grid, dim3(64), 0, s, q, k_cache, v_cache, start, nh, nkv, scale, out, out_lo); break;
-    case 64: hipLaunchKernelGGL(attention_rows_kernel<64>, grid, dim3(64), 0, s, q, k_cache, v_cache, start, nh, nkv, scale, out, out_lo); break;
-    case 128: hipLaunchKernelGGL(attention_rows_kernel<128>, grid, dim3(64), 0, s, q, k_cache, v_cache, start, nh, nkv, scale, out, out_lo); break;
+    case 16: ATT(16); break;
+    case 32: ATT(32); break;
+    case 64: ATT(64); break;
+    case 128: ATT(128); break;
     default: return set_error(LLRS_E_UNSUPPORTED, "attention head_dim %d is not supported", hd);
   }
+#undef ATT
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;
 }
