@@ -32,22 +32,39 @@ __device__ __forceinline__ int bounded_pos(const int *pos, int max_seq) {
 // the cache (KVCache::update, src/cache.rs:38-53).
 //
 // Decode attention moves a few MB per layer, so latency bounds it: each wave
-// issues all its K and V loads first, works without workgroup barriers, and
-// the chunks of a head meet through device-scope atomics only.  Partials are
-// stored write-through (device-scope relaxed atomic stores), the wave waits
-// for them to complete, then bumps the head's counter; the last chunk reads
-// them back with device-scope loads and folds them with the running-max
-// rescaling of flash decoding.  No cache write-back fence is needed.  A chunk
-// whose scores are all -inf contributes exp(-inf) = 0; without a finite
-// positive total the weights fall back to uniform, as softmax_inplace does.
+// issues all its K and V loads first and works without workgroup barriers.
+// The chunks of a head meet without counters: every chunk but the last
+// publishes its partial with device-scope 64-bit stores that carry the
+// step's tag beside each value, and returns at once; the last chunk (the one
+// holding the current position) computes its own partial, then reads the
+// others' until every tag is this step's, and folds them with the running-max
+// rescaling of flash decoding.  One round trip on the merging path, none on
+// the others, no cache write-back.  A chunk whose scores are all -inf
+// contributes exp(-inf) = 0; without a finite positive total the weights fall
+// back to uniform, as softmax_inplace does.
 
 constexpr int kChunk = 32;  // positions per wave: lane = (half of the head, position)
 
-__device__ __forceinline__ void store_dev(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// A partial's value with its tag in one single-copy-atomic 64-bit word.
+__device__ __forceinline__ void store_tagged(unsigned long long *p, float v, unsigned tag) {
+  __hip_atomic_store(p, ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float load_dev(const float *p) {
-  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ float load_tagged(const unsigned long long *p, unsigned tag, bool &ok) {
+  const unsigned long long w =
+      __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  ok = ok && (unsigned)(w >> 32) == tag;
+  return __uint_as_float((unsigned)w);
+}
+
+// Whether a merge has waited ~20 ms (the 100 MHz wall clock) for partials
+// that never came; then *err is set and the merge goes on with what it read.
+__device__ __forceinline__ bool merge_wait_over(unsigned long long &t0, unsigned *err) {
+  const unsigned long long t = wall_clock64();
+  if (!t0) t0 = t;
+  if (t - t0 < 2000000ull) return false;
+  if (err && (thread_x() & 63) == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
 }
 
 // One (query head, chunk) item, run by one wave.  COH: the output is read by
@@ -161,12 +178,12 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
       wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i));
     else
       wp = __shfl(x, p, 64);
-    const float in = c0 + p < c1 ? 1.f : 0.f;
+    const bool in = c0 + p < c1;  // a clamped row adds nothing, whatever it holds
     const float *e = reinterpret_cast<const float *>(&vv[i]);
 #pragma unroll
     for (int k = 0; k < VW; k++) {
-      O[k] += wp * e[k];
-      Vs[k] += in * e[k];
+      O[k] += in ? wp * e[k] : 0.f;
+      Vs[k] += in ? e[k] : 0.f;
     }
   }
 #pragma unroll
@@ -188,49 +205,56 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
     return;
   }
 
-  // 5. Publish the partial: [HD] O sums, [HD] V sums, max, sum.
-  float *part = a.scratch + ((size_t)h * a.max_chunks + chunk) * a.part_stride;
-  if (lane < VL) {
-#pragma unroll
-    for (int k = 0; k < VW; k++) {
-      store_dev(part + vd + k, O[k]);
-      store_dev(part + HD + vd + k, Vs[k]);
-    }
-  }
-  if (lane == 0) {
-    store_dev(part + 2 * HD, m);
-    store_dev(part + 2 * HD + 1, l);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial is written through
-  unsigned prev = 0;
-  if (lane == 0)
-    prev = __hip_atomic_fetch_add(a.counters + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  prev = __builtin_amdgcn_readfirstlane(prev);
-  if (prev != (unsigned)(n_active - 1)) return;
-
-  // 6. Merge (last chunk of the head).  Chunk statistics one per lane (64
-  //    chunks a round): the round's max by wave reduction, each chunk's weight
-  //    exp(m_c - M) in its lane, broadcast by readlane to weight the O
-  //    partials, which are loaded 32 chunks at a time.  Rounds fold with the
-  //    running-max rescaling; a chunk whose max is -inf weighs 0.
-  const float *base = a.scratch + (size_t)h * a.max_chunks * a.part_stride;
+  // 5. Every chunk but the last publishes [HD] O sums, [HD] V sums, max, sum.
   const long stride = a.part_stride;
-  float M = -INFINITY, L = 0.f, R[VW];
+  unsigned long long *const base = a.scratch + (size_t)h * a.max_chunks * stride;
+  const unsigned tag = a.tag;
+  if (chunk != n_active - 1) {
+    unsigned long long *part = base + (size_t)chunk * stride;
+    if (lane < VL) {
 #pragma unroll
-  for (int k = 0; k < VW; k++) R[k] = 0.f;
-  const int d0 = (lane % VL) * VW;
-  for (int cb = 0; cb < n_active; cb += 64) {
-    const int nc = min(64, n_active - cb);
-    // The round's statistics and its first 32 O partials load together.
-    float ov[32][VW];
-#pragma unroll
-    for (int j = 0; j < 32; j++) {
-      const float *pc = base + (size_t)(cb + min(j, nc - 1)) * stride + d0;
-#pragma unroll
-      for (int k = 0; k < VW; k++) ov[j][k] = load_dev(pc + k);
+      for (int k = 0; k < VW; k++) {
+        store_tagged(part + vd + k, O[k], tag);
+        store_tagged(part + HD + vd + k, Vs[k], tag);
+      }
     }
-    const float *pcl = base + (size_t)(cb + min(lane, nc - 1)) * stride;
-    const float mm = load_dev(pcl + 2 * HD), ll = load_dev(pcl + 2 * HD + 1);
+    if (lane == 0) {
+      store_tagged(part + 2 * HD, m, tag);
+      store_tagged(part + 2 * HD + 1, l, tag);
+    }
+    return;
+  }
+
+  // 6. Merge (the last chunk), starting from its own partial.  The others'
+  //    statistics one per lane (64 chunks a round) load together with their
+  //    first OB O partials; a load round is repeated until every tag is this
+  //    step's.  The round's max by wave reduction, each chunk's weight
+  //    exp(m_c - M) in its lane, broadcast by readlane to weight the O
+  //    partials.  Rounds fold with the running-max rescaling; a chunk whose
+  //    max is -inf weighs 0.
+  constexpr int OB = 32 / VW;  // O partials per load round
+  const int np = n_active - 1;
+  float M = m, L = l, R[VW];
+#pragma unroll
+  for (int k = 0; k < VW; k++) R[k] = O[k];
+  unsigned long long t0 = 0;
+  for (int cb = 0; cb < np; cb += 64) {
+    const int nc = min(64, np - cb);
+    float ov[OB][VW], mm, ll;
+    const unsigned long long *pcl = base + (size_t)(cb + min(lane, nc - 1)) * stride;
+    while (true) {
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < OB; j++) {
+        const unsigned long long *pc = base + (size_t)(cb + min(j, nc - 1)) * stride + vd;
+#pragma unroll
+        for (int k = 0; k < VW; k++) ov[j][k] = load_tagged(pc + k, tag, ok);
+      }
+      mm = load_tagged(pcl + 2 * HD, tag, ok);
+      ll = load_tagged(pcl + 2 * HD + 1, tag, ok);
+      if (__all(ok) || merge_wait_over(t0, a.err)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
     const bool in = lane < nc && mm != -INFINITY;
     float Mr = in ? mm : -INFINITY;
 #pragma unroll
@@ -242,46 +266,61 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
     float Rr[VW];
 #pragma unroll
     for (int k = 0; k < VW; k++) Rr[k] = 0.f;
-    for (int jb = 0; jb < nc; jb += 32) {
+    for (int jb = 0; jb < nc; jb += OB) {
       if (jb > 0) {
+        while (true) {
+          bool ok = true;
 #pragma unroll
-        for (int j = 0; j < 32; j++) {
-          const float *pc = base + (size_t)(cb + min(jb + j, nc - 1)) * stride + d0;
+          for (int j = 0; j < OB; j++) {
+            const unsigned long long *pc = base + (size_t)(cb + min(jb + j, nc - 1)) * stride + vd;
 #pragma unroll
-          for (int k = 0; k < VW; k++) ov[j][k] = load_dev(pc + k);
+            for (int k = 0; k < VW; k++) ov[j][k] = load_tagged(pc + k, tag, ok);
+          }
+          if (__all(ok) || merge_wait_over(t0, a.err)) break;
+          __builtin_amdgcn_s_sleep(1);
         }
       }
 #pragma unroll
-      for (int j = 0; j < 32; j++) {
+      for (int j = 0; j < OB; j++) {
         if (jb + j >= nc) break;
         const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jb + j));
 #pragma unroll
         for (int k = 0; k < VW; k++) Rr[k] += wj * ov[j][k];
       }
     }
-    const float Mn = fmaxf(M, Mr);
-    const float sa = expf(M - Mn), sb = expf(Mr - Mn);
-    L = L * sa + Lr * sb;
+    if (Mr != -INFINITY) {
+      const float Mn = fmaxf(M, Mr);
+      const float sa = M == -INFINITY ? 0.f : expf(M - Mn), sb = expf(Mr - Mn);
+      L = L * sa + Lr * sb;
 #pragma unroll
-    for (int k = 0; k < VW; k++) R[k] = R[k] * sa + Rr[k] * sb;
-    M = Mn;
+      for (int k = 0; k < VW; k++) R[k] = R[k] * sa + Rr[k] * sb;
+      M = Mn;
+    }
   }
   if (lane < VL) {
     if (isfinite(L) && L > 0.f) {
 #pragma unroll
-      for (int k = 0; k < VW; k++) st_act<COH>(out + d0 + k, R[k] / L);
+      for (int k = 0; k < VW; k++) st_act<COH>(out + vd + k, R[k] / L);
     } else {
       float V[VW];
 #pragma unroll
-      for (int k = 0; k < VW; k++) V[k] = 0.f;
-      for (int c = 0; c < n_active; c++)
+      for (int k = 0; k < VW; k++) V[k] = Vs[k];
+      for (int c = 0; c < np; c++) {
+        float vc[VW];
+        while (true) {
+          bool ok = true;
 #pragma unroll
-        for (int k = 0; k < VW; k++) V[k] += load_dev(base + (size_t)c * stride + HD + d0 + k);
+          for (int k = 0; k < VW; k++) vc[k] = load_tagged(base + (size_t)c * stride + HD + vd + k, tag, ok);
+          if (ok || merge_wait_over(t0, a.err)) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
 #pragma unroll
-      for (int k = 0; k < VW; k++) st_act<COH>(out + d0 + k, V[k] / (float)(pos + 1));
+        for (int k = 0; k < VW; k++) V[k] += vc[k];
+      }
+#pragma unroll
+      for (int k = 0; k < VW; k++) st_act<COH>(out + vd + k, V[k] / (float)(pos + 1));
     }
   }
-  if (lane == 0) __hip_atomic_store(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace llrs

@@ -14,20 +14,27 @@ struct AttnArgs {
   const int *pos;
   float *k_cache, *v_cache;  // this layer's [max_seq][kv_width]
   float *out;                // [nh * hd]
-  float *scratch;            // attention_scratch_floats(nh, hd, max_seq) floats
-  unsigned *counters;        // [nh], zero between launches
+  // Chunk partials, attention_scratch_words(nh, hd, max_seq) words: each value
+  // with the tag of the (step, layer) that wrote it in the high half.
+  unsigned long long *scratch;
+  const unsigned *epoch;     // step counter, advanced by the embedding kernel
+  unsigned *err;             // set when a merge gave up waiting for a partial
+  int layer, nlayers;        // tag = *epoch * nlayers + layer
+  unsigned tag;              // filled in on the device
   int nh, nkv, hd, max_seq;
   int max_chunks;            // attention_chunks(max_seq)
-  long part_stride;          // attention_part_stride(hd): floats per (head, chunk) partial
+  long part_stride;          // attention_part_stride(hd): words per (head, chunk) partial
   float scale;               // 1/sqrt(hd)
 };
 
-// Also zeroes clear[0 .. nclear) (the persistent kernel's barrier counters).
+// Also advances *epoch (the attention partials' tag) and zeroes
+// clear[0 .. nclear) (the persistent kernel's barrier counters).
 int launch_embed(const llrs_tensor *emb, const uint32_t *tok_by_pos, const int *pos, int max_seq,
-                 float *out, hipStream_t s, unsigned *clear = nullptr, int nclear = 0);
+                 float *out, unsigned *epoch, hipStream_t s, unsigned *clear = nullptr,
+                 int nclear = 0);
 int launch_rmsnorm(const float *in, const float *w, float *out, int n, float eps, hipStream_t s);
 long attention_part_stride(int hd);
-size_t attention_scratch_floats(int nh, int hd, int max_seq);
+size_t attention_scratch_words(int nh, int hd, int max_seq);
 int attention_chunks(int max_seq);
 int launch_attention(const AttnArgs &args, hipStream_t s);
 int launch_silu_mul(const float *g, const float *u, float *out, int n, hipStream_t s);

@@ -47,8 +47,10 @@ __device__ float block_sum(float v, float *sh) {
 __global__ void embed_kernel(const uint8_t *__restrict__ emb, uint32_t ty, size_t row_bytes, int H,
                              uint32_t vocab, const uint32_t *__restrict__ tok_by_pos,
                              const int *__restrict__ pos, int max_seq, float *__restrict__ out,
-                             unsigned *__restrict__ clear, int nclear) {
+                             unsigned *__restrict__ epoch, unsigned *__restrict__ clear,
+                             int nclear) {
   int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c == 0) *epoch += 1u;       // a fresh tag for this step's attention partials
   if (c < nclear) clear[c] = 0u;  // the step's barrier counters start at zero
   if (c >= H) return;
   uint32_t tok = tok_by_pos[bounded_pos(pos, max_seq)];
@@ -72,7 +74,10 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *__restrict__
 template <int HD>
 __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
   __shared__ __align__(16) float qs[HD], kn[HD];
-  // Grid (head, chunk): the low chunks, the ones that run, are dispatched first.
+  a.tag = *a.epoch * (unsigned)a.nlayers + (unsigned)a.layer;
+  // Grid (head, chunk): the low chunks, the ones that run, are dispatched
+  // first, so the chunk that merges a head always starts after the chunks it
+  // waits for.
   attention_item<HD, false>(a, blockIdx.x, blockIdx.y, bounded_pos(a.pos, a.max_seq), qs, kn);
 }
 
@@ -143,12 +148,12 @@ __global__ __launch_bounds__(256) void copy_kernel(uint4 *__restrict__ dst,
 // ------------------------------------------------------------------ launchers
 
 int launch_embed(const llrs_tensor *emb, const uint32_t *tok_by_pos, const int *pos, int max_seq,
-                 float *out, hipStream_t s, unsigned *clear, int nclear) {
+                 float *out, unsigned *epoch, hipStream_t s, unsigned *clear, int nclear) {
   int H = (int)emb->cols;
   int n = H > nclear ? H : nclear;
   hipLaunchKernelGGL(embed_kernel, dim3((n + 255) / 256), dim3(256), 0, s, emb->dev, emb->type,
-                     emb->row_bytes, H, (uint32_t)emb->rows, tok_by_pos, pos, max_seq, out, clear,
-                     nclear);
+                     emb->row_bytes, H, (uint32_t)emb->rows, tok_by_pos, pos, max_seq, out, epoch,
+                     clear, nclear);
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;
 }
@@ -161,7 +166,7 @@ int launch_rmsnorm(const float *in, const float *w, float *out, int n, float eps
 
 long attention_part_stride(int hd) { return 2L * hd + 2; }
 
-size_t attention_scratch_floats(int nh, int hd, int max_seq) {
+size_t attention_scratch_words(int nh, int hd, int max_seq) {
   return (size_t)nh * (size_t)attention_chunks(max_seq) * (size_t)attention_part_stride(hd);
 }
 

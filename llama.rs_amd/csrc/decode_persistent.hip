@@ -83,6 +83,7 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
   const int G = p.attn.nh / p.attn.nkv;
   const int n_pairs = p.attn.nkv * (pos / kChunk + 1);
   const int n_items = (n_pairs + 7) / 8 * 8 * G;
+  const unsigned epoch = *p.attn.epoch;  // advanced by this step's embedding launch
   unsigned k = 0;
   for (int l = 0; l < p.nlayers; l++) {
     // Through the constant address space: the arguments are never written
@@ -106,6 +107,7 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
       a.out += l * p.act_stride;
       a.k_cache += l * p.cache_stride;
       a.v_cache += l * p.cache_stride;
+      a.tag = epoch * (unsigned)p.nlayers + (unsigned)l;
       bar_wait(p.bar, p.err, nwg, k);
       for (int it = wave * nwg + wg; it < n_items; it += nwg * nwv) {
         const int r = it >> 3, pair = (r / G) * 8 + (it & 7);

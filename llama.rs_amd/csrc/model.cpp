@@ -65,8 +65,10 @@ struct llrs_kv {
   float *k_cache = nullptr, *v_cache = nullptr;  // [layer][pos][kv_width]
   float *hidden = nullptr, *residual = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
         *attn = nullptr, *gate = nullptr, *up = nullptr, *act = nullptr, *logits = nullptr,
-        *scores = nullptr, *rope = nullptr;  // scores: attention partials scratch
-  unsigned *attn_counters = nullptr;         // [nh] chunk completion counters
+        *rope = nullptr;
+  unsigned long long *scores = nullptr;  // attention chunk partials, tagged words
+  unsigned *epoch = nullptr;             // the step's tag, advanced by the embedding
+  unsigned *attn_err = nullptr;          // an attention merge gave up waiting
   int *pos = nullptr;
   uint32_t *tok_by_pos = nullptr, *next_token = nullptr;
   unsigned long long *amax_key = nullptr;  // LM-head argmax accumulator (zero between steps)
@@ -513,7 +515,10 @@ static AttnArgs attention_args(llrs_model *m, llrs_kv *kv, size_t l) {
   at.v_cache = kv->v_cache + l * layer_stride;
   at.out = kv->attn;
   at.scratch = kv->scores;
-  at.counters = kv->attn_counters;
+  at.epoch = kv->epoch;
+  at.err = kv->attn_err;
+  at.layer = (int)l;
+  at.nlayers = (int)c.num_hidden_layers;
   at.nh = (int)c.num_attention_heads;
   at.nkv = (int)c.num_key_value_heads;
   at.hd = (int)c.head_dim;
@@ -555,7 +560,7 @@ static int enqueue_layers(llrs_model *m, llrs_kv *kv) {
 // kernel's barrier counter).
 static int enqueue_embed(llrs_model *m, llrs_kv *kv) {
   return launch_embed(m->embed, kv->tok_by_pos, kv->pos, (int)kv->max_seq_len, kv->residual,
-                      m->b->stream, kv->p_bar, kv->p_bar ? kPersistentBarWords : 0);
+                      kv->epoch, m->b->stream, kv->p_bar, kv->p_bar ? kPersistentBarWords : 0);
 }
 
 static int enqueue_step(llrs_model *m, llrs_kv *kv, int mode) {
@@ -702,12 +707,16 @@ static int setup_persistent(llrs_model *m, llrs_kv *kv) {
   return LLRS_OK;
 }
 
-// Reports a persistent-decode barrier wait that gave up (the stream is idle).
+// Reports a device-side wait that gave up: a persistent-decode barrier or an
+// attention merge (the stream is idle).
 static int check_persistent(llrs_kv *kv) {
-  if (!kv->p_err) return LLRS_OK;
   unsigned err = 0;
-  LLRS_HIP(hipMemcpy(&err, kv->p_err, 4, hipMemcpyDeviceToHost));
-  if (err) return set_error(LLRS_E_HIP, "persistent decode: a device-wide barrier timed out");
+  if (kv->p_err) {
+    LLRS_HIP(hipMemcpy(&err, kv->p_err, 4, hipMemcpyDeviceToHost));
+    if (err) return set_error(LLRS_E_HIP, "persistent decode: a device-wide barrier timed out");
+  }
+  LLRS_HIP(hipMemcpy(&err, kv->attn_err, 4, hipMemcpyDeviceToHost));
+  if (err) return set_error(LLRS_E_HIP, "decode attention: a merge timed out waiting for partials");
   return LLRS_OK;
 }
 
@@ -744,9 +753,9 @@ static int kv_create_impl(llrs_model *m, size_t max_seq, llrs_kv **out) {
       (rc = A((void **)&kv->v, KV * 4)) || (rc = A((void **)&kv->attn, H * 4)) ||
       (rc = A((void **)&kv->gate, F * 4)) || (rc = A((void **)&kv->up, F * 4)) ||
       (rc = A((void **)&kv->act, F * 4)) || (rc = A((void **)&kv->logits, c.vocab_size * 4)) ||
-      (rc = A((void **)&kv->scores, attention_scratch_floats((int)c.num_attention_heads,
-                                                             (int)c.head_dim, (int)max_seq) * 4)) ||
-      (rc = A((void **)&kv->attn_counters, 4 * c.num_attention_heads + 64)) ||
+      (rc = A((void **)&kv->scores, attention_scratch_words((int)c.num_attention_heads,
+                                                            (int)c.head_dim, (int)max_seq) * 8)) ||
+      (rc = A((void **)&kv->epoch, 64)) || (rc = A((void **)&kv->attn_err, 64)) ||
       (rc = A((void **)&kv->rope, max_seq * c.head_dim * 4)) || (rc = A((void **)&kv->pos, 64)) ||
       (rc = A((void **)&kv->tok_by_pos, (max_seq + 1) * 4)) || (rc = A((void **)&kv->next_token, 64)) ||
       (rc = A((void **)&kv->amax_key, 64)) || (rc = A((void **)&kv->done, 64)) ||
@@ -774,7 +783,12 @@ static int kv_create_impl(llrs_model *m, size_t max_seq, llrs_kv **out) {
   if (e == hipSuccess) e = hipMemsetAsync(kv->amax_key, 0, 64, s);
   if (e == hipSuccess) e = hipMemsetAsync(kv->done, 0, 64, s);
   if (e == hipSuccess) e = hipMemsetAsync(kv->act_dig, 0, fast_gemv_digits_size(F), s);
-  if (e == hipSuccess) e = hipMemsetAsync(kv->attn_counters, 0, 4 * c.num_attention_heads + 64, s);
+  // Tag 0 is never a step's (the embedding advances the epoch first).
+  if (e == hipSuccess)
+    e = hipMemsetAsync(kv->scores, 0,
+                       attention_scratch_words((int)c.num_attention_heads, (int)c.head_dim, (int)max_seq) * 8, s);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->epoch, 0, 64, s);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->attn_err, 0, 64, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) {
     free_kv(kv);
