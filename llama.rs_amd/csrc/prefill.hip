@@ -29,7 +29,10 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BN = 128, KC = 64, LS = KC + 8;  // weight rows per tile; LS: LDS row stride in halves
+constexpr int BN = 128, KC = 64, LS = KC + 8;
+// Weight-row tiles from which 128-token tiles are used (at 256+ tokens);
+// split K makes up the workgroups the larger tiles leave out.
+constexpr int kTile128Rows = 16;  // weight rows per tile; LS: LDS row stride in halves
 
 // The 32 values of `row` at columns [k0, k0 + 32) (k0 a multiple of 32), as
 // value_at computes them, in two stages: load() issues the loads of the raw
@@ -493,6 +496,14 @@ __global__ void swiglu_f16_kernel(const float *__restrict__ g, const float *__re
 
 __global__ void set_pos_kernel(int *pos, int value) { *pos = value; }
 
+// C[t][j] = bias[j] (or 0): the starting value of a split-K product that does
+// not accumulate into C.
+__global__ void fill_rows_kernel(float *__restrict__ c, int ldc, const float *__restrict__ bias,
+                                 int n, int t) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+  if (j < n && r < t) c[(size_t)r * ldc + j] = bias ? bias[j] : 0.f;
+}
+
 }  // namespace
 
 int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
@@ -501,15 +512,21 @@ int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
                      g.k, g.lda);
   PrefillGemmArgs a = g;
   // 128-token tiles when there are enough of them (the dequantized weight
-  // tile then serves twice the tokens), else 64.  Accumulating products
-  // (o_proj, ffn_down) with fewer tiles than two per CU split K over up to 4
-  // workgroups that add into C atomically.
+  // tile then serves twice the tokens), else 64.  Products with fewer tiles
+  // than two per CU split K over up to 8 workgroups (at least 6 K chunks
+  // each) that add into C atomically; C then starts from its residual
+  // (accumulate) or from the bias, written first.  The atomic adds make the
+  // order of the split sums, and so the last bits of C, vary between runs.
   const int ntiles = (g.n + BN - 1) / BN;
-  const int bm = (g.t >= 256 && ntiles >= 64) ? 128 : 64;
+  const int bm = (g.t >= 256 && ntiles >= kTile128Rows) ? 128 : 64;
   const int tiles = ntiles * ((g.t + bm - 1) / bm), chunks = (g.k + KC - 1) / KC;
   a.ksplit = 1;
-  if (g.accumulate)
-    while (a.ksplit < 4 && tiles * a.ksplit < 512 && chunks >= 16 * a.ksplit * 2) a.ksplit *= 2;
+  while (a.ksplit < 8 && tiles * a.ksplit * 2 <= 512 && chunks / (a.ksplit * 2) >= 6) a.ksplit *= 2;
+  if (a.ksplit > 1 && !g.accumulate) {
+    hipLaunchKernelGGL(fill_rows_kernel, dim3((unsigned)((g.n + 255) / 256), (unsigned)g.t), dim3(256),
+                       0, s, g.c, g.ldc, g.bias, g.n, g.t);
+    a.accumulate = 1;  // the splits add onto the bias
+  }
   const dim3 grid((unsigned)ntiles, (unsigned)((g.t + bm - 1) / bm), (unsigned)a.ksplit);
   const size_t lds = (size_t)2 * (bm + BN) * LS * sizeof(f16);
 #define GEMM(T)                                                                        \
