@@ -7,7 +7,8 @@ untied LM head, rope_theta 1e6), random-init N(0, 0.02) weights quantized
 with the reference's q4km recipe (Q4_K q/k/o/gate/up, Q8_0 v/embeddings/LM
 head, Q6_K ffn_down), generated in HBM.  A 512-token random prompt is
 prefilled (an untimed warm-up, then the median of 3 timed prefills), then
-`--warmup` untimed and `--steps` timed greedy decode steps run; one step = one token through the whole model (the decode loop of
+`--warmup` untimed and `--steps` timed greedy decode steps run; one step =
+one token through the whole model (the decode loop of
 InferenceEngine::benchmark_tokens, src/engine.rs:205-216), replayed from a
 captured hipGraph with the token and position kept on the device.
 

@@ -17,6 +17,8 @@
 // the GEMM is close to an f32 GEMM rather than an f16 one.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 
 #include "common.h"
 #include "prefill.h"
@@ -506,28 +508,35 @@ __global__ void fill_rows_kernel(float *__restrict__ c, int ldc, const float *__
 
 }  // namespace
 
-int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
-  if (g.k % 32 || g.lda % 8 || g.n <= 0 || g.k <= 0 || g.t <= 0)
-    return set_error(LLRS_E_UNSUPPORTED, "prefill GEMM shape %d x %d (lda %d) is not supported", g.n,
-                     g.k, g.lda);
-  PrefillGemmArgs a = g;
-  // 128-token tiles when there are enough of them (the dequantized weight
-  // tile then serves twice the tokens), else 64.  Products with fewer tiles
-  // than two per CU split K over up to 8 workgroups (at least 6 K chunks
-  // each) that add into C atomically; C then starts from its residual
-  // (accumulate) or from the bias, written first.  The atomic adds make the
-  // order of the split sums, and so the last bits of C, vary between runs.
-  const int ntiles = (g.n + BN - 1) / BN;
-  const int bm = (g.t >= 256 && ntiles >= kTile128Rows) ? 128 : 64;
-  const int tiles = ntiles * ((g.t + bm - 1) / bm), chunks = (g.k + KC - 1) / KC;
-  a.ksplit = 1;
-  while (a.ksplit < 8 && tiles * a.ksplit * 2 <= 512 && chunks / (a.ksplit * 2) >= 6) a.ksplit *= 2;
-  if (a.ksplit > 1 && !g.accumulate) {
-    hipLaunchKernelGGL(fill_rows_kernel, dim3((unsigned)((g.n + 255) / 256), (unsigned)g.t), dim3(256),
-                       0, s, g.c, g.ldc, g.bias, g.n, g.t);
+namespace {
+
+// Workgroup slots of the device for the GEMM: two workgroups per CU (their
+// LDS, 55-74 KB each, allows two).
+int gemm_slots() {
+  static int slots = 0;
+  if (!slots) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    slots = 2 * cus;
+  }
+  return slots;
+}
+
+// K split over `ksplit` workgroups that add into C atomically: C then starts
+// from its residual (accumulate) or from the bias, written first.
+void set_split(PrefillGemmArgs &a, int ksplit, hipStream_t s) {
+  a.ksplit = ksplit;
+  if (ksplit > 1 && !a.accumulate) {
+    hipLaunchKernelGGL(fill_rows_kernel, dim3((unsigned)((a.n + 255) / 256), (unsigned)a.t), dim3(256),
+                       0, s, a.c, a.ldc, a.bias, a.n, a.t);
     a.accumulate = 1;  // the splits add onto the bias
   }
-  const dim3 grid((unsigned)ntiles, (unsigned)((g.t + bm - 1) / bm), (unsigned)a.ksplit);
+}
+
+void launch_tiles(const PrefillGemmArgs &a, int bm, hipStream_t s) {
+  const dim3 grid((unsigned)((a.n + BN - 1) / BN), (unsigned)((a.t + bm - 1) / bm), (unsigned)a.ksplit);
   const size_t lds = (size_t)2 * (bm + BN) * LS * sizeof(f16);
 #define GEMM(T)                                                                        \
   if (bm == 128)                                                                       \
@@ -542,6 +551,47 @@ int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
     default: GEMM(0xffffffffu) break;
   }
 #undef GEMM
+}
+
+}  // namespace
+
+int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
+  if (g.k % 32 || g.lda % 8 || g.n <= 0 || g.k <= 0 || g.t <= 0)
+    return set_error(LLRS_E_UNSUPPORTED, "prefill GEMM shape %d x %d (lda %d) is not supported", g.n,
+                     g.k, g.lda);
+  // 128-token tiles when there are enough of them (the dequantized weight
+  // tile then serves twice the tokens), else 64.  Products with fewer tiles
+  // than half the slots split K over up to 8 workgroups (at least 6 K chunks
+  // each).  Otherwise whole rounds of tiles run as they are, and a last
+  // round that would fill at most half the slots runs as its own launch with
+  // K split over the slots.  The atomic adds of split K make the order of the
+  // split sums, and so the last bits of C, vary between runs.
+  const int slots = gemm_slots();
+  const int ntiles = (g.n + BN - 1) / BN;
+  const int bm = (g.t >= 256 && ntiles >= kTile128Rows) ? 128 : 64;
+  const int mt = (g.t + bm - 1) / bm, chunks = (g.k + KC - 1) / KC;
+  int ks = 1;
+  while (ks < 8 && ntiles * mt * ks * 2 <= slots && chunks / (ks * 2) >= 6) ks *= 2;
+  const int per_round = slots / mt;  // row tiles per round of slots
+  const int full = (ks == 1 && per_round > 0) ? ntiles / per_round * per_round : 0;
+  const int rem = ntiles - full;
+  if (full > 0 && rem > 0 && rem * mt * 2 <= slots) {
+    PrefillGemmArgs m = g;
+    m.n = full * BN;
+    m.ksplit = 1;
+    launch_tiles(m, bm, s);
+    PrefillGemmArgs r = g;
+    r.w = g.w + (size_t)full * BN * (size_t)g.row_bytes;
+    r.c = g.c + (size_t)full * BN;
+    r.bias = g.bias ? g.bias + (size_t)full * BN : nullptr;
+    r.n = g.n - full * BN;
+    set_split(r, std::max(1, std::min({8, slots / (rem * mt), chunks / 6})), s);
+    launch_tiles(r, bm, s);
+  } else {
+    PrefillGemmArgs a = g;
+    set_split(a, ks, s);
+    launch_tiles(a, bm, s);
+  }
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;
 }
