@@ -24,7 +24,7 @@ struct PrefillGemmArgs {
   const float *bias;  // [n] or null; ignored when accumulating
   int t;
   int accumulate;
-  int ksplit;  // set by launch_prefill_gemm: K ranges summed with atomic adds (accumulate only)
+  int ksplit;  // set by launch_prefill_gemm: K ranges summed into C with atomic adds
 };
 
 int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s);

@@ -2,14 +2,16 @@
 // T-row batch (CausalModel::prefill, src/architecture.rs:60-77, computed the
 // way Qwen2Model::forward_impl, src/model.rs:135-271, computes one token).
 //
-// The weight matrices run as MFMA dequant-GEMMs: a workgroup owns a 64-token x
-// 128-row output tile.  It dequantizes its 128 weight rows 64 columns at a
-// time from the native GGUF blocks (value_at, src/quant.rs:349-456) into LDS,
-// stages the matching activation tile, and accumulates
-// v_mfma_f32_16x16x32_f16 products in f32.  Each wave holds a 32 x 64 quarter
-// of the tile (2 x 4 MFMA blocks).  The raw weight blocks and activations of
-// the next 64 columns are loaded into registers before the current ones are
-// multiplied, so the loads' latency hides behind the MFMAs.
+// The weight matrices run as MFMA dequant-GEMMs: a workgroup owns a 64- or
+// 128-token x 128-row output tile (of one K range when K is split).  It
+// dequantizes its 128 weight rows 64 columns at a time from the native GGUF
+// blocks (value_at, src/quant.rs:349-456) into LDS, stages the matching
+// activation tile, and accumulates v_mfma_f32_16x16x32_f16 products in f32.
+// Each wave holds a quarter of the tile (BM/2 tokens x 64 rows).  The raw
+// weight blocks and activations of the next 64 columns are loaded into
+// registers before the current ones are multiplied, so the loads' latency
+// hides behind the MFMAs.  Causal attention runs on f32 MFMA
+// (attention_tile_kernel).
 //
 // Precision: f32 operands are carried as f16 pairs, v = hi + lo with hi =
 // f16(v) and lo = f16(v - hi) (22 significant bits), and each product is
@@ -18,7 +20,6 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-
 
 #include "common.h"
 #include "prefill.h"
