@@ -106,6 +106,19 @@ def test_prefill_128_token_tiles(llrs, backend, oracle, tmp_path):
     compare_run(llrs, backend, oracle, cfg, tmp_path / "w.gguf", prompt, 8, 320)
 
 
+def test_prefill_split_last_round(llrs, backend, oracle, tmp_path):
+    """A 512-token prompt through FFN matrices of 18944 rows (the 7B width): gate
+    and up have 148 x 4 = 592 tiles of 128 rows x 128 tokens, more than the 512
+    workgroup slots of a 256-CU part, so the last 80 run as their own launch
+    with K split over the slots (the bias-free products start from zeros
+    there); prefill, decode and KV still match the oracle (the oracle's
+    smallest top-2 logit gap over the 9 greedy steps is 6.9e-3)."""
+    cfg = tiny_cfg(llrs, intermediate_size=18944, num_hidden_layers=1, max_position_embeddings=1024,
+                   seed=37)
+    prompt = np.random.default_rng(37).integers(0, cfg.vocab_size, 512).astype(np.uint32)
+    compare_run(llrs, backend, oracle, cfg, tmp_path / "s.gguf", prompt, 8, 528)
+
+
 def test_forward_token_matches_prefill(llrs, backend, oracle, tmp_path, monkeypatch):
     """The batched (MFMA) prefill agrees with the token-by-token loop of
     CausalModel::prefill (src/architecture.rs:60-77) within the logits bar;
