@@ -119,6 +119,19 @@ def test_prefill_split_last_round(llrs, backend, oracle, tmp_path):
     compare_run(llrs, backend, oracle, cfg, tmp_path / "s.gguf", prompt, 8, 528)
 
 
+def test_prefill_two_chunks_head_dim_16(llrs, backend, oracle, tmp_path):
+    """A 600-token prompt goes through the batched prefill as a 512-row chunk
+    and an 88-row chunk starting at position 512, whose attention tiles reach
+    back into the first chunk's cache rows; head_dim 16 (16 heads over 4 KV
+    heads) takes the smallest attention tile kernel and the per-phase decode.
+    (Seed 47: the oracle's smallest top-2 logit gap over the 9 greedy steps
+    is 2.7e-2.)"""
+    cfg = tiny_cfg(llrs, num_attention_heads=16, num_key_value_heads=4, max_position_embeddings=1024,
+                   seed=47)
+    prompt = np.random.default_rng(47).integers(0, cfg.vocab_size, 600).astype(np.uint32)
+    compare_run(llrs, backend, oracle, cfg, tmp_path / "c.gguf", prompt, 8, 640)
+
+
 def test_forward_token_matches_prefill(llrs, backend, oracle, tmp_path, monkeypatch):
     """The batched (MFMA) prefill agrees with the token-by-token loop of
     CausalModel::prefill (src/architecture.rs:60-77) within the logits bar;
