@@ -142,6 +142,61 @@ def projection_only(llrs, be, model, which: str, iters: int) -> int:
     return 0
 
 
+TUNED_TYPES = ("Q4K", "Q6K", "Q8_0", "Q5_0")  # types the tuned GEMV takes; the rest run generic
+
+
+def gemv_sweep(llrs, be) -> int:
+    """Configs 1 and 2: single batch-1 GEMVs through KernelBackend::matvec
+    (llrs_matvec_dev on device buffers).  Config 1: Q4_K 8960 x 1536 (seed 1);
+    config 2: every type at 18944 x 3584 and 3584 x 18944 (seed 2).  Each
+    tensor is uploaded as many times as makes >= 1.2 GB, and the launches
+    rotate over the copies, so the 256 MB MALL cannot serve a repeat; the
+    timed loop is one synchronisation around n launches.  Algorithmic bytes
+    = weights + x + y."""
+    import ctypes as C
+    QT = llrs.QuantType
+    lib = llrs.lib()
+    cases = [("cfg1", QT.Q4K, 8960, 1536, 1)]
+    for name in ("Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q4K", "Q5K", "Q6K", "F16", "BF16"):
+        cases += [("cfg2", QT[name], 18944, 3584, 2), ("cfg2", QT[name], 3584, 18944, 2)]
+    out = []
+    for cfg, ty, rows, cols, seed in cases:
+        data = llrs.blocks.random_tensor_bytes(ty, rows, cols, seed=seed)
+        nbytes = len(data)
+        copies = max(2, int(1.2e9 // nbytes) + 1)
+        qt = llrs.QuantTensor(data, (rows, cols), ty)
+        ts = [be.upload(qt) for _ in range(copies)]
+        x, y = C.c_void_p(), C.c_void_p()
+        llrs._check(lib.llrs_device_alloc(be.handle, cols * 4, C.byref(x)))
+        llrs._check(lib.llrs_device_alloc(be.handle, rows * 4, C.byref(y)))
+        try:
+            xs = llrs.blocks.random_activation(cols, seed)
+            llrs._check(lib.llrs_copy_h2d(be.handle, x, xs.ctypes.data, cols * 4))
+            for t in ts:
+                llrs._check(lib.llrs_matvec_dev(be.handle, t.handle, x, y))
+            be.synchronize()
+            n = max(2 * copies, min(2000, int(0.2 / (nbytes / 5e12))))  # ~0.2 s, at most 2000
+            t0 = time.perf_counter()
+            for i in range(n):
+                lib.llrs_matvec_dev(be.handle, ts[i % copies].handle, x, y)
+            be.synchronize()
+            dt = (time.perf_counter() - t0) / n
+        finally:
+            lib.llrs_device_free(be.handle, x)
+            lib.llrs_device_free(be.handle, y)
+            del ts
+        alg = nbytes + 4 * (rows + cols)
+        rec = {"config": cfg, "type": ty.name, "rows": rows, "cols": cols, "weight_bytes": nbytes,
+               "kernel": "tuned" if ty.name in TUNED_TYPES else "generic", "launches": n,
+               "copies": copies, "us": round(dt * 1e6, 2), "gbs": round(alg / dt / 1e9, 1),
+               "frac": round(alg / dt / 1e9 / PEAK_HBM_GBS, 4)}
+        log(f"{cfg} {ty.name:5s} {rows:6d} x {cols:5d} {nbytes / 1e6:8.2f} MB {rec['kernel']:7s} "
+            f"{rec['us']:9.2f} us {rec['gbs']:7.1f} GB/s ({100 * rec['frac']:.1f}% of peak)")
+        out.append(rec)
+    print(json.dumps({"gemv": out}), flush=True)
+    return 0
+
+
 def profiled_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration copy), or None."""
@@ -168,6 +223,8 @@ def main() -> int:
     ap.add_argument("--projection-only", choices=["qkv", "o", "gate_up", "down", "lm_head", "layers"],
                     help="only time this projection's launches over all layers and run the "
                          "calibration copy (the workload of the rocprofv3 --pmc traffic runs)")
+    ap.add_argument("--gemv", action="store_true",
+                    help="configs 1 and 2 instead: single GEMVs per type over rotating weight copies")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -180,6 +237,8 @@ def main() -> int:
     llrs = package()
     be = llrs.HipBackend(0)
     log(f"backend {be.name()} with {be.threads()} CUs")
+    if args.gemv:
+        return gemv_sweep(llrs, be)
     cfg = llrs.SynthConfig(hidden_size=3584, intermediate_size=18944, num_attention_heads=28,
                            num_key_value_heads=4, num_hidden_layers=28, vocab_size=152064,
                            max_position_embeddings=32768, rope_theta=1e6, rms_norm_eps=1e-6,
