@@ -15,7 +15,8 @@ captured hipGraph with the token and position kept on the device.
 Prints ONE JSON line: decode tok/s as `value`, the whole-step HBM rate, the
 dominant kernel's roofline (HIP-event timing of its own launches) and the
 CPU baseline (the oracle's restated AVX2 path on this host's cores, on a
-bounded sample of the same model).
+bounded sample of the same model).  `--workload cfg3|cfg4` runs the 0.5B and
+1.5B end-to-end configs the same way; `--gemv` runs configs 1 and 2.
 """
 from __future__ import annotations
 
@@ -74,7 +75,7 @@ def kv_bytes_per_token(cfg, pos: int) -> int:
     return cfg.num_hidden_layers * 2 * ((pos + 1) * row + row)
 
 
-def cpu_baseline(llrs, model, seconds: float, log_prefix="cpu") -> dict:
+def cpu_baseline(llrs, model, seconds: float, label: str, log_prefix="cpu") -> dict:
     """The oracle's restated AVX2 path (src/simd.rs) on all host threads, on the same
     model bytes (exported from HBM), decoding from position 0 for ~`seconds`."""
     sys.path.insert(0, str(ROOT / "tests"))
@@ -88,7 +89,7 @@ def cpu_baseline(llrs, model, seconds: float, log_prefix="cpu") -> dict:
         model.export_gguf(path)
         log(f"{log_prefix}: exported model to {path} in {time.perf_counter() - t0:.1f}s")
         om = Oracle().load(path, kernel=AVX2, threads=threads)
-        om.new_state(64)
+        om.new_state(160)  # the timed sample is at most 128 steps after position 0
         t0 = time.perf_counter()
         om.forward_token(1, 0, True)
         first = time.perf_counter() - t0
@@ -105,7 +106,7 @@ def cpu_baseline(llrs, model, seconds: float, log_prefix="cpu") -> dict:
         if path.exists():
             path.unlink()
     return {"value": round(n / dt, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} greedy decode steps at positions 1-{n} of the same 7B q4km model "
+            "sample": f"{n} greedy decode steps at positions 1-{n} of the same {label} model "
                       f"(after 1 warm-up token at position 0), oracle's restated AVX2 path "
                       f"(src/simd.rs) with the reference's row-parallel policy on {threads} "
                       f"threads; the Rust reference itself cannot be built here"}
@@ -210,12 +211,40 @@ def profiled_traffic(kernel: str):
     return None
 
 
+# The end-to-end configs of BASELINE.json: synthetic models (random-init
+# N(0, 0.02) weights, quantized in HBM), prompt length and decode steps.
+# cfg5 is the headline (the default); cfg3 and cfg4 are run on request.
+WORKLOADS = {
+    "cfg5": dict(metric=METRIC, prompt=512, steps=128, recipe="Q4KM", seed=5,
+                 desc="cfg5: Qwen2.5-7B-shape q4km, 512-token prefill then batch-1 greedy decode",
+                 shape=dict(hidden_size=3584, intermediate_size=18944, num_attention_heads=28,
+                            num_key_value_heads=4, num_hidden_layers=28, vocab_size=152064,
+                            tie_word_embeddings=False)),
+    "cfg3": dict(metric="batch-1 decode tok/s + achieved HBM GB/s (% of peak), Qwen2.5-0.5B-shape q4km",
+                 prompt=128, steps=32, recipe="Q4KM", seed=3,
+                 desc="cfg3: Qwen2.5-0.5B-shape q4km (Q5_0 fallback for 896-wide rows, tied "
+                      "embeddings), 128-token prefill then 32 greedy decode steps",
+                 shape=dict(hidden_size=896, intermediate_size=4864, num_attention_heads=14,
+                            num_key_value_heads=2, num_hidden_layers=24, vocab_size=151936,
+                            tie_word_embeddings=True)),
+    "cfg4": dict(metric="batch-1 decode tok/s + achieved HBM GB/s (% of peak), Qwen2.5-1.5B-shape q4k "
+                        "at KV depth 4000",
+                 prompt=4000, steps=64, recipe="Q4K", seed=4,
+                 desc="cfg4: Qwen2.5-1.5B-shape uniform q4k (tied embeddings), KV cache prefilled to "
+                      "depth 4000 with random tokens, then 64 greedy decode steps",
+                 shape=dict(hidden_size=1536, intermediate_size=8960, num_attention_heads=12,
+                            num_key_value_heads=2, num_hidden_layers=28, vocab_size=151936,
+                            tie_word_embeddings=True)),
+}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg5")
+    ap.add_argument("--steps", type=int, default=None, help="timed decode steps (workload default)")
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (workload default)")
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -226,6 +255,11 @@ def main() -> int:
     ap.add_argument("--gemv", action="store_true",
                     help="configs 1 and 2 instead: single GEMVs per type over rotating weight copies")
     args = ap.parse_args()
+    wl = WORKLOADS[args.workload]
+    if args.steps is None:
+        args.steps = wl["steps"]
+    if args.prompt is None:
+        args.prompt = wl["prompt"]
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path; see DESIGN.md on sharding)", file=sys.stderr)
@@ -239,22 +273,22 @@ def main() -> int:
     log(f"backend {be.name()} with {be.threads()} CUs")
     if args.gemv:
         return gemv_sweep(llrs, be)
-    cfg = llrs.SynthConfig(hidden_size=3584, intermediate_size=18944, num_attention_heads=28,
-                           num_key_value_heads=4, num_hidden_layers=28, vocab_size=152064,
-                           max_position_embeddings=32768, rope_theta=1e6, rms_norm_eps=1e-6,
-                           tie_word_embeddings=False, recipe=llrs.LoadQuantization.Q4KM, seed=5)
+    cfg = llrs.SynthConfig(max_position_embeddings=32768, rope_theta=1e6, rms_norm_eps=1e-6,
+                           recipe=getattr(llrs.LoadQuantization, wl["recipe"]), seed=wl["seed"],
+                           **wl["shape"])
     t0 = time.perf_counter()
     model = llrs.HipQwen2Model.synthetic(be, cfg)
     gen_s = time.perf_counter() - t0
     mc = model.config()
     wbytes = model.weight_bytes()
-    log(f"generated 7B q4km model in HBM in {gen_s:.1f}s: {wbytes / 1e9:.3f} GB of weights/token")
+    log(f"generated the {args.workload} model in HBM in {gen_s:.1f}s: {wbytes / 1e9:.3f} GB of "
+        f"weights/token")
 
     if args.projection_only:
         return projection_only(llrs, be, model, args.projection_only, args.profile_iters)
 
     kv = llrs.KVCache(model, args.context)
-    prompt = np.random.default_rng(5).integers(0, mc.vocab_size, args.prompt).astype(np.uint32)
+    prompt = np.random.default_rng(wl["seed"]).integers(0, mc.vocab_size, args.prompt).astype(np.uint32)
     # As llama-bench (src/bin/llama-bench.rs:113-126): an untimed warm-up
     # (first launches, the prefill buffers' allocation), then the median of
     # 3 timed prefills from position 0; the last one leaves the cache for
@@ -312,7 +346,7 @@ def main() -> int:
         achieved = (wb + kvb) / us / 1e3
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                    "traffic": profiled_traffic("decode_persistent_kernel"),
+                    "traffic": profiled_traffic("decode_persistent_kernel") if args.workload == "cfg5" else None,
                     "kernel": f"decode_persistent_kernel: all {mc.num_hidden_layers} layers in one "
                               f"launch ({wb} weight bytes + {kvb} KV bytes at position {pos_now})"}
     else:
@@ -321,21 +355,21 @@ def main() -> int:
         achieved = d["bytes"] / d["avg_us"] / 1e3
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                    "traffic": profiled_traffic(dom),
+                    "traffic": profiled_traffic(dom) if args.workload == "cfg5" else None,
                     "kernel": f"{dom} projection GEMV ({d['bytes']} algorithmic weight bytes/launch)"}
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(llrs, model, args.cpu_seconds)
+        cpu = cpu_baseline(llrs, model, args.cpu_seconds, f"{args.workload} {wl['recipe'].lower()}")
         log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
 
     out = {
-        "metric": METRIC, "value": round(tps, 3), "unit": "tok/s", "n_gpus": 1,
+        "metric": wl["metric"], "value": round(tps, 3), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * dt / args.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (random-init N(0,0.02) weights, q4km-quantized in HBM; random prompt ids)",
-        "config": {"workload": "cfg5: Qwen2.5-7B-shape q4km, 512-token prefill then batch-1 greedy "
-                               "decode", "prompt_tokens": args.prompt, "decode_start_pos": pos0,
+        "data": f"synthetic (random-init N(0,0.02) weights, {wl['recipe'].lower()}-quantized in HBM; "
+                "random prompt ids)",
+        "config": {"workload": wl["desc"], "prompt_tokens": args.prompt, "decode_start_pos": pos0,
                    "context": args.context, "global_batch": 1, "parallelism": "none"},
         "hbm_gbps": round(hbm_gbs, 1), "hbm_pct_peak": round(100 * hbm_gbs / PEAK_HBM_GBS, 2),
         "bytes_per_token": int(bytes_tok), "prefill_tps": round(args.prompt / prefill_s, 2),
