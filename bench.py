@@ -324,6 +324,17 @@ def main() -> int:
         f"{hbm_gbs:.0f} GB/s ({100 * hbm_gbs / PEAK_HBM_GBS:.1f}% of peak); "
         f"first tokens {toks[:6].tolist()}")
 
+    # On-device sampling (sample_current_logits, src/engine.rs:253-325) of the
+    # last logits with the engine's default options: host-synchronous calls.
+    sampler = llrs.Sampler(llrs.SamplingOptions())
+    sampler.sample(kv, 0.5)
+    t0 = time.perf_counter()
+    for i in range(20):
+        sampler.remember(sampler.sample(kv, (i + 0.5) / 20))
+    sample_us = (time.perf_counter() - t0) / 20 * 1e6
+    log(f"sampling {sample_us:.1f} us per call (temperature 0.7, top-k 40, top-p 0.9, penalty 1.1, "
+        f"vocab {mc.vocab_size})")
+
     # Per-projection launch timing (HIP events, the backend's stream), rotating
     # over all layers so every launch streams weights from HBM.
     per = {}
@@ -372,6 +383,7 @@ def main() -> int:
         "config": {"workload": wl["desc"], "prompt_tokens": args.prompt, "decode_start_pos": pos0,
                    "context": args.context, "global_batch": 1, "parallelism": "none"},
         "hbm_gbps": round(hbm_gbs, 1), "hbm_pct_peak": round(100 * hbm_gbs / PEAK_HBM_GBS, 2),
+        "sample_us": round(sample_us, 1),
         "bytes_per_token": int(bytes_tok), "prefill_tps": round(args.prompt / prefill_s, 2),
         "prefill": {"tokens": args.prompt, "ms": round(prefill_s * 1e3, 2),
                     "tflops": round(pf_flops / prefill_s / 1e12, 2),

@@ -191,6 +191,23 @@ int llrs_decode_greedy(llrs_model *m, llrs_kv *kv, size_t start_pos, size_t n_st
                        uint32_t *out_tokens);
 /* argmax_current_logits (src/engine.rs:233-241) of the current device logits. */
 int llrs_argmax(llrs_kv *kv, uint32_t *out_token);
+
+/* EngineOptions' sampling fields (src/engine.rs:14-31). */
+typedef struct llrs_sampling {
+  float temperature;        /* 0: greedy (the first candidate of the sorted logits) */
+  float top_p;              /* in (0, 1] */
+  uint32_t top_k;           /* 0: every token */
+  float repetition_penalty; /* > 0; 1: off */
+} llrs_sampling;
+/* InferenceEngine::sample_current_logits (src/engine.rs:253-325) on the
+ * device over the current logits: the repetition penalty for the tokens in
+ * recent[0 .. n_recent) (the repeat window, at most 65536), the temperature,
+ * the descending sort, top-k, softmax, the top-p cutoff and the draw.  The
+ * uniform number in [0, 1) is the caller's (the reference draws
+ * rand::thread_rng().gen::<f32>()).  Options are validated as
+ * validate_sampling (src/engine.rs:327-338). */
+int llrs_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent, size_t n_recent,
+                float uniform, uint32_t *out_token);
 /* Readback for tests: InferenceBuffers::logits (src/cache.rs:76) and
  * KVCache::{k,v}_cache[layer][0 .. n) (src/cache.rs:5-7). */
 int llrs_read_logits(llrs_kv *kv, float *out, size_t n);

@@ -66,6 +66,11 @@ class _ModelConfig(C.Structure):
         ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("tie_word_embeddings", C.c_int)]
 
 
+class _Sampling(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_uint32),
+                ("repetition_penalty", C.c_float)]
+
+
 class _SynthConfig(C.Structure):
     _fields_ = [(n, C.c_size_t) for n in (
         "hidden_size", "intermediate_size", "num_attention_heads", "num_key_value_heads",
@@ -118,6 +123,7 @@ SIGNATURES = [
     ("llrs_prefill", C.c_int, [P, P, U32P, SZ, SZ]),
     ("llrs_decode_greedy", C.c_int, [P, P, SZ, SZ, U32P]),
     ("llrs_argmax", C.c_int, [P, U32P]),
+    ("llrs_sample", C.c_int, [P, P, P, SZ, C.c_float, U32P]),
     ("llrs_read_logits", C.c_int, [P, F32P, SZ]),
     ("llrs_read_kv", C.c_int, [P, SZ, C.c_int, F32P, SZ]),
     ("llrs_profile_projection", C.c_int, [P, P, C.c_int, C.c_int, C.POINTER(C.c_double),
@@ -352,7 +358,7 @@ __all__ = ["gguf_read_tensor", "LlrsError", "QuantType", "QuantTensor", "LoadQua
 
 from . import blocks  # noqa: E402
 from .model import (LlamaConfig, KVCache, HipQwen2Model, ModelLoader,  # noqa: E402
-                    SynthConfig, InferenceEngine)
+                    SynthConfig, InferenceEngine, Sampler, SamplingOptions)
 
 __all__ += ["LlamaConfig", "KVCache", "HipQwen2Model", "ModelLoader", "SynthConfig",
-            "InferenceEngine"]
+            "InferenceEngine", "Sampler", "SamplingOptions"]

@@ -27,6 +27,7 @@
 #include "prefill.h"
 #include "quantize.h"
 #include "quant_encode.h"
+#include "sampling.h"
 #include "synth.h"
 
 namespace llrs {
@@ -69,6 +70,7 @@ struct llrs_kv {
   unsigned long long *scores = nullptr;  // attention chunk partials, tagged words
   unsigned *epoch = nullptr;             // the step's tag, advanced by the embedding
   unsigned *attn_err = nullptr;          // an attention merge gave up waiting
+  llrs::SampleScratch sample;            // llrs_sample's buffers, allocated on first use
   int *pos = nullptr;
   uint32_t *tok_by_pos = nullptr, *next_token = nullptr;
   unsigned long long *amax_key = nullptr;  // LM-head argmax accumulator (zero between steps)
@@ -1142,6 +1144,50 @@ int llrs_argmax(llrs_kv *kv, uint32_t *out_token) {
   *out_token = kv->pinned[0];
   LLRS_TRY(stage_tokens(kv, nullptr, 0, saved));
   LLRS_HIP(hipStreamSynchronize(s));
+  return LLRS_OK;
+}
+
+int llrs_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent, size_t n_recent,
+                float uniform, uint32_t *out_token) {
+  clear_error();
+  if (!kv || !opts || !out_token || (n_recent && !recent))
+    return set_error(LLRS_E_INVALID, "kv/opts/recent/out is NULL");
+  // validate_sampling (src/engine.rs:327-338).
+  if (!std::isfinite(opts->temperature) || opts->temperature < 0.0f)
+    return set_error(LLRS_E_INVALID, "temperature must be finite and non-negative");
+  if (!std::isfinite(opts->top_p) || !(0.0f < opts->top_p && opts->top_p <= 1.0f))
+    return set_error(LLRS_E_INVALID, "top_p must be in (0, 1]");
+  if (!std::isfinite(opts->repetition_penalty) || opts->repetition_penalty <= 0.0f)
+    return set_error(LLRS_E_INVALID, "repetition_penalty must be finite and positive");
+  if (!std::isfinite(uniform) || uniform < 0.0f || uniform >= 1.0f)
+    return set_error(LLRS_E_INVALID, "the uniform draw must be in [0, 1)");
+  constexpr size_t kMaxRecent = 65536;
+  if (n_recent > kMaxRecent) return set_error(LLRS_E_INVALID, "repeat window %zu > %zu", n_recent, kMaxRecent);
+  llrs_model *m = kv->m;
+  LLRS_HIP(hipSetDevice(m->b->device));
+  hipStream_t s = m->b->stream;
+  const int V = (int)m->cfg.vocab_size;
+  SampleScratch &w = kv->sample;
+  if (!w.n) {
+    auto A = [&](void **p, size_t bytes) { return dev_alloc(kv->allocs, p, bytes); };
+    w.tmp_bytes = sample_sort_bytes(V);
+    LLRS_TRY(A((void **)&w.keys, (size_t)V * 4));
+    LLRS_TRY(A((void **)&w.keys_sorted, (size_t)V * 4));
+    LLRS_TRY(A((void **)&w.idx, (size_t)V * 4));
+    LLRS_TRY(A((void **)&w.idx_sorted, (size_t)V * 4));
+    LLRS_TRY(A((void **)&w.recent, kMaxRecent * 4));
+    LLRS_TRY(A((void **)&w.token, 64));
+    LLRS_TRY(A(&w.tmp, w.tmp_bytes ? w.tmp_bytes : 1));
+    w.max_recent = (int)kMaxRecent;
+    w.n = V;
+  }
+  if (n_recent) LLRS_HIP(hipMemcpyAsync(w.recent, recent, n_recent * 4, hipMemcpyHostToDevice, s));
+  const SampleParams p{opts->temperature, (int)std::min<uint32_t>(opts->top_k, (uint32_t)V), opts->top_p,
+                       opts->repetition_penalty};
+  LLRS_TRY(launch_sample(kv->logits, V, p, (int)n_recent, uniform, w, s));
+  LLRS_HIP(hipMemcpyAsync(kv->pinned, w.token, 4, hipMemcpyDeviceToHost, s));
+  LLRS_HIP(hipStreamSynchronize(s));
+  *out_token = kv->pinned[0];
   return LLRS_OK;
 }
 

@@ -14,7 +14,36 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import (HipBackend, LlrsError, LoadQuantization, LogitsMode, _check, _f32, _ModelConfig,
-               _SynthConfig, lib, P, SZ, U32P)
+               _Sampling, _SynthConfig, lib, P, SZ, U32P)
+
+
+@dataclass
+class SamplingOptions:
+    """EngineOptions' sampling fields and their defaults (src/engine.rs:14-31)."""
+    temperature: float = 0.7
+    top_p: float = 0.9
+    top_k: int = 40
+    repetition_penalty: float = 1.1
+
+
+class Sampler:
+    """The engine's sampling state (src/engine.rs:36-90, 243-251): the options
+    and the window of the last `repeat_last_n` tokens the penalty applies to."""
+
+    def __init__(self, opts: SamplingOptions | None = None, repeat_last_n: int = 64):
+        self.opts = opts or SamplingOptions()
+        self.max_repeat_window = repeat_last_n
+        self.recent_tokens: list[int] = []
+
+    def remember(self, token: int) -> None:
+        if self.max_repeat_window == 0:
+            return
+        self.recent_tokens.append(int(token))
+        if len(self.recent_tokens) > self.max_repeat_window:
+            self.recent_tokens.pop(0)
+
+    def sample(self, kv: "KVCache", uniform: float) -> int:
+        return kv.sample(self.opts, uniform, self.recent_tokens)
 
 
 @dataclass
@@ -168,6 +197,16 @@ class KVCache:
     def argmax(self) -> int:
         t = C.c_uint32()
         _check(lib().llrs_argmax(self.handle, C.byref(t)))
+        return int(t.value)
+
+    def sample(self, opts: "SamplingOptions", uniform: float, recent=()) -> int:
+        """sample_current_logits (src/engine.rs:253-325) on the device with the
+        caller's uniform draw in [0, 1); `recent` is the repeat window."""
+        r = np.ascontiguousarray(np.asarray(recent, dtype=np.uint32))
+        o = _Sampling(opts.temperature, opts.top_p, opts.top_k, opts.repetition_penalty)
+        t = C.c_uint32()
+        _check(lib().llrs_sample(self.handle, C.byref(o), r.ctypes.data_as(P) if r.size else None,
+                                 r.size, float(uniform), C.byref(t)))
         return int(t.value)
 
     def layer(self, layer: int, which: str, n_pos: int) -> np.ndarray:

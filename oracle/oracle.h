@@ -109,6 +109,14 @@ int oq_decode_greedy(const oq_model *m, oq_state *s, size_t start_pos, size_t n_
 int oq_gguf_read_f32(const char *path, const char *name, uint32_t *version, size_t *rows,
                      size_t *cols, float *out, size_t capacity);
 
+/* sample_current_logits (src/engine.rs:253-325) with the uniform draw given:
+ * repetition penalty for the tokens in recent[0 .. n_recent), temperature,
+ * the descending total_cmp sort (ties: lower index first), top-k, softmax and
+ * top-p in sequential f32 sums, then random = uniform * kept_sum decremented
+ * by each kept probability until <= 0. */
+uint32_t oq_sample(const float *logits, size_t n, float temperature, size_t top_k, float top_p,
+                   float repetition_penalty, const uint32_t *recent, size_t n_recent, float uniform);
+
 /* Read access to the state, for tests. */
 const float *oq_state_logits(const oq_state *s);
 const float *oq_state_residual(const oq_state *s);

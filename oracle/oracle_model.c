@@ -642,6 +642,77 @@ uint32_t oq_argmax(const float *logits, size_t n) {
   return (uint32_t)best;
 }
 
+/* ---- sampling: sample_current_logits (src/engine.rs:253-325) ---- */
+
+typedef struct { uint32_t token; float value; } oq_cand;
+
+/* Descending in total_cmp order (src/engine.rs:285); equal values keep the
+ * lower token first (the reference's unstable sort leaves them unordered). */
+static int cand_cmp(const void *a, const void *b) {
+  const oq_cand *x = (const oq_cand *)a, *y = (const oq_cand *)b;
+  int32_t kx = total_key(x->value), ky = total_key(y->value);
+  if (kx != ky) return kx > ky ? -1 : 1;
+  return x->token < y->token ? -1 : (x->token > y->token);
+}
+
+uint32_t oq_sample(const float *logits, size_t n, float temperature, size_t top_k, float top_p,
+                   float repetition_penalty, const uint32_t *recent, size_t n_recent, float uniform) {
+  if (n == 0) return 0;
+  unsigned char *seen = calloc(n, 1);
+  oq_cand *c = malloc(n * sizeof *c);
+  if (!seen || !c) {
+    free(seen);
+    free(c);
+    return 0;
+  }
+  for (size_t i = 0; i < n_recent; i++)
+    if (recent[i] < n) seen[recent[i]] = 1;
+  for (size_t t = 0; t < n; t++) { /* src/engine.rs:262-278 */
+    float v = logits[t];
+    if (repetition_penalty != 1.0f && seen[t]) v = v > 0.0f ? v / repetition_penalty : v * repetition_penalty;
+    if (temperature > 0.0f) v /= temperature;
+    if (!isfinite(v)) v = -INFINITY;
+    c[t].token = (uint32_t)t;
+    c[t].value = v;
+  }
+  qsort(c, n, sizeof *c, cand_cmp);
+  uint32_t out = c[0].token;
+  if (temperature > 0.0f) {
+    size_t m = (top_k > 0 && top_k < n) ? top_k : n;
+    float max = c[0].value, sum = 0.0f;
+    for (size_t i = 0; i < m; i++) {
+      c[i].value = expf(c[i].value - max);
+      sum += c[i].value;
+    }
+    if (isfinite(sum) && sum > 0.0f) {
+      for (size_t i = 0; i < m; i++) c[i].value /= sum;
+      float cumulative = 0.0f;
+      size_t cutoff = m;
+      for (size_t i = 0; i < m; i++) {
+        cumulative += c[i].value;
+        if (cumulative >= top_p) {
+          cutoff = i + 1;
+          break;
+        }
+      }
+      float kept_sum = 0.0f;
+      for (size_t i = 0; i < cutoff; i++) kept_sum += c[i].value;
+      float random = uniform * kept_sum;
+      out = c[cutoff - 1].token;
+      for (size_t i = 0; i < cutoff; i++) {
+        random -= c[i].value;
+        if (random <= 0.0f) {
+          out = c[i].token;
+          break;
+        }
+      }
+    }
+  }
+  free(seen);
+  free(c);
+  return out;
+}
+
 int oq_decode_greedy(const oq_model *m, oq_state *s, size_t start_pos, size_t n_steps, uint32_t *out) {
   for (size_t i = 0; i < n_steps; i++) {
     uint32_t tok = oq_argmax(s->logits, m->cfg.vocab_size);

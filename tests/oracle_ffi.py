@@ -60,6 +60,8 @@ class Oracle:
             "oq_forward_token": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_size_t, C.c_int]),
             "oq_prefill": (C.c_int, [C.c_void_p, C.c_void_p, U32P, C.c_size_t, C.c_size_t]),
             "oq_argmax": (C.c_uint32, [F32P, C.c_size_t]),
+            "oq_sample": (C.c_uint32, [F32P, C.c_size_t, C.c_float, C.c_size_t, C.c_float, C.c_float,
+                                       U32P, C.c_size_t, C.c_float]),
             "oq_decode_greedy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, U32P]),
             "oq_gguf_read_f32": (C.c_int, [C.c_char_p, C.c_char_p, U32P, C.POINTER(C.c_size_t),
                                            C.POINTER(C.c_size_t), F32P, C.c_size_t]),
@@ -100,6 +102,15 @@ class Oracle:
                                 y.ctypes.data_as(F32P), kernel, threads, threshold)
         assert rc == 0
         return y
+
+    def sample(self, logits: np.ndarray, temperature: float, top_k: int, top_p: float,
+               repetition_penalty: float, recent, uniform: float) -> int:
+        """sample_current_logits (src/engine.rs:253-325) with the given uniform draw."""
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        r = np.ascontiguousarray(np.asarray(recent, dtype=np.uint32))
+        return int(self.lib.oq_sample(lg.ctypes.data_as(F32P), lg.size, temperature, top_k, top_p,
+                                      repetition_penalty, r.ctypes.data_as(U32P) if r.size else None,
+                                      r.size, uniform))
 
     def gguf_read_f32(self, path, name: str):
         """(version, values[rows, cols]) via the oracle's GGUF reader; raises on error."""
