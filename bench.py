@@ -16,7 +16,8 @@ Prints ONE JSON line: decode tok/s as `value`, the whole-step HBM rate, the
 dominant kernel's roofline (HIP-event timing of its own launches) and the
 CPU baseline (the oracle's restated AVX2 path on this host's cores, on a
 bounded sample of the same model).  `--workload cfg3|cfg4` runs the 0.5B and
-1.5B end-to-end configs the same way; `--gemv` runs configs 1 and 2.
+1.5B end-to-end configs the same way; `--gemv` runs configs 1 and 2;
+`--load` times the SafeTensors loader's load-time quantization.
 """
 from __future__ import annotations
 
@@ -238,6 +239,115 @@ WORKLOADS = {
 }
 
 
+HF_LAYER_TENSORS = (  # (name, rows, cols) per layer; "H", "F", "KV" stand for the widths
+    ("input_layernorm.weight", None, "H"), ("post_attention_layernorm.weight", None, "H"),
+    ("self_attn.q_proj.weight", "H", "H"), ("self_attn.q_proj.bias", None, "H"),
+    ("self_attn.k_proj.weight", "KV", "H"), ("self_attn.k_proj.bias", None, "KV"),
+    ("self_attn.v_proj.weight", "KV", "H"), ("self_attn.v_proj.bias", None, "KV"),
+    ("self_attn.o_proj.weight", "H", "H"), ("mlp.gate_proj.weight", "F", "H"),
+    ("mlp.up_proj.weight", "F", "H"), ("mlp.down_proj.weight", "H", "F"))
+
+
+def write_hf_checkpoint(shape: dict, out: pathlib.Path, seed: int) -> int:
+    """A Hugging Face BF16 checkpoint (config.json + model.safetensors) of the
+    workload's shape, its values tiled from a 32 MiB block of N(0, 0.02)
+    bf16 draws (norm gains 1 + N(0, 0.02)); returns the file's size."""
+    H, F, L, V = (shape[k] for k in ("hidden_size", "intermediate_size", "num_hidden_layers",
+                                     "vocab_size"))
+    KV = shape["num_key_value_heads"] * (H // shape["num_attention_heads"])
+    dims = {"H": H, "F": F, "KV": KV}
+    tensors = [("model.embed_tokens.weight", (V, H)), ("model.norm.weight", (H,))]
+    for i in range(L):
+        tensors += [(f"model.layers.{i}.{n}", (dims[c],) if r is None else (dims[r], dims[c]))
+                    for n, r, c in HF_LAYER_TENSORS]
+    if not shape["tie_word_embeddings"]:
+        tensors.append(("lm_head.weight", (V, H)))
+    header, off = {"__metadata__": {"format": "pt"}}, 0
+    for name, shp in tensors:
+        n = int(np.prod(shp)) * 2
+        header[name] = {"dtype": "BF16", "shape": list(shp), "data_offsets": [off, off + n]}
+        off += n
+    hdr = json.dumps(header).encode()
+    hdr += b" " * (-len(hdr) % 8)
+    rng = np.random.default_rng(seed)
+    block = (rng.standard_normal(16 << 20).astype(np.float32) * 0.02).view(np.uint32)
+    block = ((block + 0x8000) >> 16).astype(np.uint16)  # round to nearest bf16
+    gain = ((((1 + rng.standard_normal(65536).astype(np.float32) * 0.02).view(np.uint32)
+              + 0x8000) >> 16).astype(np.uint16))
+    with open(out / "model.safetensors", "wb") as f:
+        f.write(len(hdr).to_bytes(8, "little") + hdr)
+        for name, shp in tensors:
+            n = int(np.prod(shp))
+            src = gain if name.endswith("norm.weight") else block
+            while n:
+                k = min(n, src.size)
+                f.write(src[:k].tobytes())
+                n -= k
+    config = {"model_type": "qwen2", "architectures": ["Qwen2ForCausalLM"],
+              "max_position_embeddings": 32768, "rms_norm_eps": 1e-6, "rope_theta": 1e6,
+              "torch_dtype": "bfloat16", **shape}
+    (out / "config.json").write_text(json.dumps(config))
+    return 8 + len(hdr) + off
+
+
+def load_bench(llrs, be, workload: str, cpu_seconds: float, keep: bool) -> int:
+    """SafetensorsLoader::load with load-time q4km quantization: a BF16
+    checkpoint of the workload's shape is written to a temporary directory,
+    loaded once untimed (page cache, code objects) and once timed.  `value`
+    is checkpoint bytes / load seconds; the CPU baseline is the host encoder
+    (the reference's sequential quantize_* loops, one thread) on a bounded
+    sample of the same matrices."""
+    import shutil
+    import tempfile
+    wl = WORKLOADS[workload]
+    d = pathlib.Path(tempfile.mkdtemp(prefix="llrs_ckpt_", dir=os.environ.get("TMPDIR", "/tmp")))
+    try:
+        t0 = time.perf_counter()
+        nbytes = write_hf_checkpoint(wl["shape"], d, wl["seed"])
+        log(f"wrote a {nbytes / 1e9:.2f} GB BF16 checkpoint in {time.perf_counter() - t0:.1f}s")
+        times = []
+        for i in range(2):
+            t0 = time.perf_counter()
+            model = llrs.ModelLoader.load(d, be, llrs.LoadQuantization.Q4KM)
+            be.synchronize()
+            times.append(time.perf_counter() - t0)
+            wbytes = model.weight_bytes()
+            log(f"load {i} ({'timed' if i else 'warm-up'}): {times[-1]:.2f}s")
+            if i == 0:
+                del model
+        kv = llrs.KVCache(model, 64)
+        model.prefill(np.arange(8, dtype=np.uint32), 0, kv)
+        toks = model.decode_greedy(8, 4, kv)
+        log(f"loaded model decodes: {toks.tolist()}")
+        # Host encoder on a sample of the same matrices (gate_proj rows).
+        H, F = wl["shape"]["hidden_size"], wl["shape"]["intermediate_size"]
+        rng = np.random.default_rng(wl["seed"])
+        vals = rng.standard_normal((256, H)).astype(np.float32) * 0.02
+        rows, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < min(cpu_seconds, 10.0):
+            llrs.QuantTensor.quantize(llrs.QuantType.Q4K, vals, 256, H)
+            rows += 256
+        cpu_s = time.perf_counter() - t0
+        cpu_gbs = rows * H * 2 / cpu_s / 1e9
+        rec = {"metric": "load-time q4km quantization of a BF16 safetensors checkpoint",
+               "value": round(nbytes / times[1] / 1e9, 3), "unit": "GB/s of checkpoint",
+               "load_s": round(times[1], 3), "checkpoint_bytes": nbytes,
+               "weight_bytes_per_token_after": wbytes, "higher_is_better": True,
+               "dtype": "bf16->q4km", "data": "synthetic",
+               "config": {"workload": f"{workload} shape, HF BF16 -> q4km (Q4_K/Q8_0/Q6_K)"},
+               "cpu_baseline": {"value": round(cpu_gbs, 4), "unit": "GB/s of checkpoint",
+                                "cores": 1, "kind": "port",
+                                "sample": f"{rows} rows x {H} of Q4_K (gate_proj-shaped), host encoder"},
+               "cpu_projected_load_s": round(nbytes / (cpu_gbs * 1e9), 1)}
+        print(json.dumps(rec), flush=True)
+    finally:
+        if keep:
+            log(f"kept {d}")
+        else:
+            shutil.rmtree(d, ignore_errors=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -254,6 +364,10 @@ def main() -> int:
                          "calibration copy (the workload of the rocprofv3 --pmc traffic runs)")
     ap.add_argument("--gemv", action="store_true",
                     help="configs 1 and 2 instead: single GEMVs per type over rotating weight copies")
+    ap.add_argument("--load", action="store_true",
+                    help="instead: load a BF16 safetensors checkpoint of the workload's shape with "
+                         "load-time q4km quantization")
+    ap.add_argument("--keep-checkpoint", action="store_true", help="--load: keep the written files")
     args = ap.parse_args()
     wl = WORKLOADS[args.workload]
     if args.steps is None:
@@ -273,6 +387,8 @@ def main() -> int:
     log(f"backend {be.name()} with {be.threads()} CUs")
     if args.gemv:
         return gemv_sweep(llrs, be)
+    if args.load:
+        return load_bench(llrs, be, args.workload, args.cpu_seconds, args.keep_checkpoint)
     cfg = llrs.SynthConfig(max_position_embeddings=32768, rope_theta=1e6, rms_norm_eps=1e-6,
                            recipe=getattr(llrs.LoadQuantization, wl["recipe"]), seed=wl["seed"],
                            **wl["shape"])

@@ -39,6 +39,8 @@ enum llrs_logits_mode { LLRS_LOGITS_SKIP = 0, LLRS_LOGITS_COMPUTE = 1 };
 
 /* LoadQuantization (src/loader.rs:16-25). */
 enum llrs_quantization { LLRS_QUANT_NONE = 0, LLRS_QUANT_Q4K = 1, LLRS_QUANT_Q4KM = 2 };
+/* Checkpoint formats ModelLoader::load recognises (src/loader.rs:44-77). */
+enum llrs_model_format { LLRS_FORMAT_GGUF = 1, LLRS_FORMAT_SAFETENSORS = 2 };
 
 typedef struct llrs_backend llrs_backend;
 typedef struct llrs_tensor llrs_tensor;
@@ -136,6 +138,34 @@ typedef struct {
  * the reference's q4k / q4km recipe when the file holds F32/F16/BF16
  * matrices (src/loader.rs:406-447). */
 int llrs_model_load_gguf(llrs_backend *b, const char *path, int quantization, llrs_model **out);
+/* SafetensorsLoader::load (src/loader.rs:80-228): a Hugging Face Qwen2
+ * checkpoint directory (config.json + model.safetensors, or the shards of
+ * model.safetensors.index.json).  F32/F16/BF16 matrices are uploaded as they
+ * are (quantization = LLRS_QUANT_NONE) or converted and quantized on the GPU
+ * with the q4k / q4km recipe (maybe_quantize, src/loader.rs:406-447); norms
+ * and biases become f32 (missing Q/K/V biases: zeros); the LM head is
+ * lm_head.weight when present, else the embedding matrix. */
+int llrs_model_load_safetensors(llrs_backend *b, const char *model_dir, int quantization,
+                                llrs_model **out);
+/* ModelLoader::load (src/loader.rs:44-77): a .gguf file, a .safetensors file
+ * (its directory is loaded), or a directory holding model.safetensors /
+ * model.safetensors.index.json or exactly one .gguf file. */
+int llrs_model_load(llrs_backend *b, const char *path, int quantization, llrs_model **out);
+/* The format llrs_model_load picks for path (LLRS_FORMAT_*) and what it opens
+ * (the GGUF file or the checkpoint directory), without a GPU.  resolved may
+ * be NULL. */
+int llrs_model_format(const char *path, int *format, char *resolved, size_t capacity);
+/* LlamaConfig::from_json + validate (src/config.rs:17-90) on a config.json
+ * whose model_type is "qwen2" (src/loader.rs:85-97), without a GPU. */
+int llrs_hf_config_read(const char *config_json_path, llrs_model_config *out);
+/* SafetensorStore::open + tensor (src/loader.rs:543-645) without a GPU: one
+ * F32/F16/BF16 tensor of a checkpoint directory, with every check of the
+ * safetensors header.  *ggml_type is LLRS_F32, LLRS_F16 or LLRS_BF16; shape
+ * receives *ndim (1 or 2) sizes, outermost first.  If out is NULL only the
+ * metadata is returned. */
+int llrs_safetensors_read_tensor(const char *model_dir, const char *name, uint32_t *ggml_type,
+                                 size_t *shape, size_t *ndim, void *out, size_t out_capacity,
+                                 size_t *nbytes);
 void llrs_model_free(llrs_model *m);
 int llrs_model_config_get(const llrs_model *m, llrs_model_config *out);
 /* Bytes of weights the decode step streams per token (all matrices incl.

@@ -109,6 +109,12 @@ SIGNATURES = [
     ("llrs_gguf_read_tensor", C.c_int, [C.c_char_p, C.c_char_p, U32P, U32P, C.POINTER(SZ),
                                         C.POINTER(SZ), P, SZ, C.POINTER(SZ)]),
     ("llrs_model_load_gguf", C.c_int, [P, C.c_char_p, C.c_int, C.POINTER(P)]),
+    ("llrs_model_load_safetensors", C.c_int, [P, C.c_char_p, C.c_int, C.POINTER(P)]),
+    ("llrs_model_load", C.c_int, [P, C.c_char_p, C.c_int, C.POINTER(P)]),
+    ("llrs_model_format", C.c_int, [C.c_char_p, C.POINTER(C.c_int), C.c_char_p, SZ]),
+    ("llrs_hf_config_read", C.c_int, [C.c_char_p, C.POINTER(_ModelConfig)]),
+    ("llrs_safetensors_read_tensor", C.c_int, [C.c_char_p, C.c_char_p, U32P, C.POINTER(SZ),
+                                               C.POINTER(SZ), P, SZ, C.POINTER(SZ)]),
     ("llrs_model_free", None, [P]),
     ("llrs_model_config_get", C.c_int, [P, C.POINTER(_ModelConfig)]),
     ("llrs_model_weight_bytes", SZ, [P]),
@@ -353,12 +359,38 @@ def gguf_read_tensor(path, name: str):
     return ver.value, QuantTensor(buf.tobytes(), shape, QuantType(ty.value))
 
 
-__all__ = ["gguf_read_tensor", "LlrsError", "QuantType", "QuantTensor", "LoadQuantization", "LogitsMode",
+def safetensors_read_tensor(model_dir, name: str):
+    """SafetensorStore::open(model_dir).tensor(name) (src/loader.rs:543-645):
+    (QuantType, shape, raw bytes)."""
+    ty, nd, nb = C.c_uint32(), SZ(), SZ()
+    shape = (SZ * 2)()
+    d, n = str(model_dir).encode(), name.encode()
+    _check(lib().llrs_safetensors_read_tensor(d, n, C.byref(ty), shape, C.byref(nd), None, 0,
+                                              C.byref(nb)))
+    buf = np.empty(nb.value, dtype=np.uint8)
+    _check(lib().llrs_safetensors_read_tensor(d, n, C.byref(ty), shape, C.byref(nd),
+                                              buf.ctypes.data if buf.size else None, buf.size,
+                                              C.byref(nb)))
+    return QuantType(ty.value), tuple(shape[i] for i in range(nd.value)), buf.tobytes()
+
+
+def model_format(path):
+    """ModelLoader::load's format choice (src/loader.rs:44-77): ("gguf", file)
+    or ("safetensors", directory)."""
+    fmt = C.c_int()
+    buf = C.create_string_buffer(4096)
+    _check(lib().llrs_model_format(str(path).encode(), C.byref(fmt), buf, len(buf)))
+    return ("gguf" if fmt.value == 1 else "safetensors"), buf.value.decode()
+
+
+__all__ = ["gguf_read_tensor", "safetensors_read_tensor", "model_format", "LlrsError", "QuantType", "QuantTensor", "LoadQuantization", "LogitsMode",
            "KernelBackend", "HipBackend", "DeviceTensor", "lib", "LIB_PATH", "HEADER"]
 
 from . import blocks  # noqa: E402
 from .model import (LlamaConfig, KVCache, HipQwen2Model, ModelLoader,  # noqa: E402
-                    SynthConfig, InferenceEngine, Sampler, SamplingOptions)
+                    GgufLoader, SafetensorsLoader, hf_config, SynthConfig, InferenceEngine,
+                    Sampler, SamplingOptions)
 
-__all__ += ["LlamaConfig", "KVCache", "HipQwen2Model", "ModelLoader", "SynthConfig",
-            "InferenceEngine", "Sampler", "SamplingOptions"]
+__all__ += ["LlamaConfig", "KVCache", "HipQwen2Model", "ModelLoader", "GgufLoader",
+            "SafetensorsLoader", "hf_config", "SynthConfig", "InferenceEngine", "Sampler",
+            "SamplingOptions"]

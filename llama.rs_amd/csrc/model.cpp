@@ -3,6 +3,9 @@
 //
 //   llrs_model_load_gguf   GgufLoader::load (src/loader.rs:233-399) incl.
 //                          maybe_quantize (406-447) and load_gguf_* (497-534)
+//   llrs_model_load_safetensors  SafetensorsLoader::load (src/loader.rs:80-228)
+//                          incl. load_st_* (458-495)
+//   llrs_model_load        ModelLoader::load's format detection (src/loader.rs:44-77)
 //   llrs_kv_create         KVCache::new + InferenceBuffers::new (src/cache.rs:13-101)
 //   llrs_forward_token     Qwen2Model::forward_impl (src/model.rs:135-271)
 //   llrs_prefill           CausalModel::prefill (src/architecture.rs:60-77)
@@ -26,6 +29,7 @@
 #include "gguf.h"
 #include "prefill.h"
 #include "quantize.h"
+#include "safetensors.h"
 #include "quant_encode.h"
 #include "sampling.h"
 #include "synth.h"
@@ -129,34 +133,41 @@ static int validate_config(llrs_model_config &c) {
   return LLRS_OK;
 }
 
-static void host_to_f32(uint32_t ty, const uint8_t *src, size_t n, float *dst) {
-  for (size_t i = 0; i < n; i++) {
-    if (ty == LLRS_F32) memcpy(&dst[i], src + 4 * i, 4);
-    else if (ty == LLRS_F16) dst[i] = f16_bits_to_f32_host((uint16_t)(src[2 * i] | (src[2 * i + 1] << 8)));
-    else {
-      uint32_t b = (uint32_t)(src[2 * i] | (src[2 * i + 1] << 8)) << 16;
-      if (((b >> 16) & 0x7fffu) > 0x7f80u) b |= 0x00400000u;
-      memcpy(&dst[i], &b, 4);
-    }
-  }
-}
-
-// maybe_quantize (src/loader.rs:406-447) on the GPU: f32 values are uploaded
-// and encoded by the same encoders the host quantizer uses (bit-identical).
-static int quantize_on_device(llrs_backend *b, uint32_t want, const float *vals, size_t rows,
-                              size_t cols, llrs_tensor **out) {
-  if (want == LLRS_F32) return llrs_tensor_upload(b, vals, rows * cols * 4, LLRS_F32, rows, cols, out);
-  float *dv = nullptr;
-  LLRS_HIP(hipMalloc(&dv, rows * cols * 4 + 4));
+// maybe_quantize (src/loader.rs:406-447) on the GPU: the F32/F16/BF16 source
+// bytes are uploaded as they are, widened to f32 on the device and encoded
+// by the same encoders the host quantizer uses (bit-identical).  want may be
+// LLRS_F32 (a recipe fallback), which keeps the widened values.
+static int quantize_on_device(llrs_backend *b, uint32_t want, uint32_t src_ty, const uint8_t *src,
+                              size_t rows, size_t cols, llrs_tensor **out) {
+  const size_t n = rows * cols;
+  if (want == LLRS_F32 && src_ty == LLRS_F32)
+    return llrs_tensor_upload(b, src, n * 4, LLRS_F32, rows, cols, out);
   llrs_tensor *t = nullptr;
+  void *raw = nullptr;
+  float *dv = nullptr;
   int rc = tensor_alloc(b, want, rows, cols, &t);
   hipError_t e = hipSuccess;
   if (rc == LLRS_OK) {
-    e = hipMemcpyAsync(dv, vals, rows * cols * 4, hipMemcpyHostToDevice, b->stream);
-    if (e == hipSuccess) rc = launch_encode(want, dv, rows, cols, t->dev, t->row_bytes, b->stream);
+    float *vals = want == LLRS_F32 ? (float *)t->dev : nullptr;
+    if (!vals) {
+      e = hipMalloc(&dv, n * 4 + 4);
+      vals = dv;
+    }
+    if (e == hipSuccess) {
+      if (src_ty == LLRS_F32) {
+        e = hipMemcpyAsync(vals, src, n * 4, hipMemcpyHostToDevice, b->stream);
+      } else {
+        e = hipMalloc(&raw, n * 2 + 4);
+        if (e == hipSuccess) e = hipMemcpyAsync(raw, src, n * 2, hipMemcpyHostToDevice, b->stream);
+        if (e == hipSuccess) rc = launch_widen(src_ty, raw, n, vals, b->stream);
+      }
+    }
+    if (e == hipSuccess && rc == LLRS_OK && want != LLRS_F32)
+      rc = launch_encode(want, vals, rows, cols, t->dev, t->row_bytes, b->stream);
     if (e == hipSuccess && rc == LLRS_OK) e = hipStreamSynchronize(b->stream);
   }
-  (void)hipFree(dv);
+  if (dv) (void)hipFree(dv);
+  if (raw) (void)hipFree(raw);
   if (rc == LLRS_OK && e != hipSuccess) rc = set_error(LLRS_E_HIP, "device quantization failed: %s", hipGetErrorString(e));
   if (rc != LLRS_OK) {
     if (t) llrs_tensor_free(t);
@@ -180,11 +191,8 @@ static int gguf_matrix(llrs_model *m, const GgufFile &g, const std::string &name
                      name.c_str(), (unsigned long long)(dims.size() == 2 ? dims[1] : dims[0]),
                      (unsigned long long)(dims.size() == 2 ? dims[0] : 0), rows, cols);
   uint32_t ty = t->type;
-  if (quantization != LLRS_QUANT_NONE && (ty == LLRS_F32 || ty == LLRS_F16 || ty == LLRS_BF16)) {
-    std::vector<float> vals(rows * cols);
-    host_to_f32(ty, g.data(*t), rows * cols, vals.data());
-    return quantize_on_device(m->b, recipe_type(quantization, name, cols), vals.data(), rows, cols, out);
-  }
+  if (quantization != LLRS_QUANT_NONE && (ty == LLRS_F32 || ty == LLRS_F16 || ty == LLRS_BF16))
+    return quantize_on_device(m->b, recipe_type(quantization, name, cols), ty, g.data(*t), rows, cols, out);
   return llrs_tensor_upload(m->b, g.data(*t), t->nbytes, ty, rows, cols, out);
 }
 
@@ -312,6 +320,115 @@ static int load_gguf_impl(llrs_backend *b, const char *path, int quantization, l
   };
   VecFn vec = [&](const std::string &name, size_t len, bool zeros, float *dst) {
     return gguf_vector(m, g, name, len, zeros, dst);
+  };
+  int rc = build_model(m, mat, vec);
+  if (rc != LLRS_OK) {
+    free_model(m);
+    return rc;
+  }
+  *out = m;
+  return LLRS_OK;
+}
+
+// The Hugging Face tensor name of a GGUF tensor name (the names
+// SafetensorsLoader::load reads, src/loader.rs:102-213).
+static std::string hf_name(const std::string &g) {
+  static const std::pair<const char *, const char *> kTop[] = {
+      {"token_embd.weight", "model.embed_tokens.weight"},
+      {"output_norm.weight", "model.norm.weight"},
+      {"output.weight", "lm_head.weight"}};
+  for (const auto &t : kTop)
+    if (g == t.first) return t.second;
+  static const std::pair<const char *, const char *> kLayer[] = {
+      {"attn_norm.weight", "input_layernorm.weight"},
+      {"ffn_norm.weight", "post_attention_layernorm.weight"},
+      {"attn_q.weight", "self_attn.q_proj.weight"},
+      {"attn_q.bias", "self_attn.q_proj.bias"},
+      {"attn_k.weight", "self_attn.k_proj.weight"},
+      {"attn_k.bias", "self_attn.k_proj.bias"},
+      {"attn_v.weight", "self_attn.v_proj.weight"},
+      {"attn_v.bias", "self_attn.v_proj.bias"},
+      {"attn_output.weight", "self_attn.o_proj.weight"},
+      {"ffn_gate.weight", "mlp.gate_proj.weight"},
+      {"ffn_up.weight", "mlp.up_proj.weight"},
+      {"ffn_down.weight", "mlp.down_proj.weight"}};
+  const size_t dot = g.find('.', 4);  // "blk.<i>.<rest>"
+  const std::string layer = g.substr(4, dot - 4), rest = g.substr(dot + 1);
+  for (const auto &t : kLayer)
+    if (rest == t.first) return "model.layers." + layer + "." + t.second;
+  return g;
+}
+
+static uint32_t st_type(const SafetensorInfo &t) {
+  return t.dtype == "F32" ? LLRS_F32 : t.dtype == "F16" ? LLRS_F16 : LLRS_BF16;
+}
+
+// load_st_matrix + check_matrix + maybe_quantize (src/loader.rs:406-467).
+static int st_matrix(llrs_model *m, SafetensorStore &st, const std::string &name, size_t rows,
+                     size_t cols, int quantization, llrs_tensor **out) {
+  const SafetensorsFile *f = nullptr;
+  const SafetensorInfo *t = nullptr;
+  LLRS_TRY(st.tensor(name, &f, &t));
+  if (t->shape.size() != 2 || t->shape[0] != rows || t->shape[1] != cols)
+    return set_error(LLRS_E_INVALID, "tensor %s has shape [%llu%s%llu], expected [%zu, %zu]", name.c_str(),
+                     (unsigned long long)t->shape[0], t->shape.size() == 2 ? ", " : "",
+                     (unsigned long long)(t->shape.size() == 2 ? t->shape[1] : 0), rows, cols);
+  const uint32_t ty = st_type(*t);
+  if (quantization != LLRS_QUANT_NONE)
+    return quantize_on_device(m->b, recipe_type(quantization, name, cols), ty, f->data(*t), rows, cols, out);
+  return llrs_tensor_upload(m->b, f->data(*t), t->nbytes, ty, rows, cols, out);
+}
+
+// load_st_vector (src/loader.rs:469-477) into an f32 device vector; a missing
+// Q/K/V bias is zeros (src/loader.rs:479-495).
+static int st_vector(llrs_model *m, SafetensorStore &st, const std::string &name, size_t len,
+                     bool zeros_if_missing, float *dst) {
+  if (zeros_if_missing && !st.contains(name)) {
+    LLRS_HIP(hipMemsetAsync(dst, 0, len * 4, m->b->stream));
+    LLRS_HIP(hipStreamSynchronize(m->b->stream));
+    return LLRS_OK;
+  }
+  const SafetensorsFile *f = nullptr;
+  const SafetensorInfo *t = nullptr;
+  LLRS_TRY(st.tensor(name, &f, &t));
+  if (t->shape.size() != 1 || t->shape[0] != len)
+    return set_error(LLRS_E_INVALID, "tensor %s has the wrong shape, expected [%zu]", name.c_str(), len);
+  const uint32_t ty = st_type(*t);
+  if (ty == LLRS_F32) {
+    LLRS_HIP(hipMemcpyAsync(dst, f->data(*t), len * 4, hipMemcpyHostToDevice, m->b->stream));
+    LLRS_HIP(hipStreamSynchronize(m->b->stream));
+    return LLRS_OK;
+  }
+  void *raw = nullptr;
+  LLRS_HIP(hipMalloc(&raw, len * 2 + 4));
+  hipError_t e = hipMemcpyAsync(raw, f->data(*t), len * 2, hipMemcpyHostToDevice, m->b->stream);
+  int rc = e == hipSuccess ? launch_widen(ty, raw, len, dst, m->b->stream) : LLRS_OK;
+  if (e == hipSuccess && rc == LLRS_OK) e = hipStreamSynchronize(m->b->stream);
+  (void)hipFree(raw);
+  LLRS_TRY(rc);
+  if (e != hipSuccess) return set_error(LLRS_E_HIP, "vector upload failed: %s", hipGetErrorString(e));
+  return LLRS_OK;
+}
+
+static int load_safetensors_impl(llrs_backend *b, const std::string &dir, int quantization,
+                                 llrs_model **out) {
+  llrs_model_config c{};
+  LLRS_TRY(hf_config_read(dir + "/config.json", c));
+  SafetensorStore st;
+  LLRS_TRY(st.open(dir));
+  // The LM head is lm_head.weight when the checkpoint has one, else the
+  // embedding matrix (src/loader.rs:203-214), whatever config.json says.
+  c.tie_word_embeddings = !st.contains("lm_head.weight");
+  LLRS_TRY(validate_config(c));
+  llrs_model *m = new (std::nothrow) llrs_model();
+  if (!m) return set_error(LLRS_E_OOM, "out of host memory");
+  m->b = b;
+  m->cfg = c;
+  MatFn mat = [&](const std::string &name, size_t rows, size_t cols, llrs_tensor **t) {
+    return st_matrix(m, st, hf_name(name), rows, cols, quantization, t);
+  };
+  VecFn vec = [&](const std::string &name, size_t len, bool zeros, float *dst) {
+    return st_vector(m, st, hf_name(name), len, zeros, dst);
   };
   int rc = build_model(m, mat, vec);
   if (rc != LLRS_OK) {
@@ -917,6 +1034,28 @@ int llrs_model_load_gguf(llrs_backend *b, const char *path, int quantization, ll
     return set_error(LLRS_E_INVALID, "unknown quantization %d", quantization);
   LLRS_HIP(hipSetDevice(b->device));
   return load_gguf_impl(b, path, quantization, out);
+}
+
+int llrs_model_load_safetensors(llrs_backend *b, const char *model_dir, int quantization,
+                                llrs_model **out) {
+  clear_error();
+  if (!b || !model_dir || !out) return set_error(LLRS_E_INVALID, "backend/model_dir/out is NULL");
+  *out = nullptr;
+  if (quantization < LLRS_QUANT_NONE || quantization > LLRS_QUANT_Q4KM)
+    return set_error(LLRS_E_INVALID, "unknown quantization %d", quantization);
+  LLRS_HIP(hipSetDevice(b->device));
+  return load_safetensors_impl(b, model_dir, quantization, out);
+}
+
+int llrs_model_load(llrs_backend *b, const char *path, int quantization, llrs_model **out) {
+  clear_error();
+  if (!b || !path || !out) return set_error(LLRS_E_INVALID, "backend/path/out is NULL");
+  *out = nullptr;
+  int format = 0;
+  std::string resolved;
+  LLRS_TRY(detect_model_format(path, format, resolved));
+  return format == LLRS_FORMAT_GGUF ? llrs_model_load_gguf(b, resolved.c_str(), quantization, out)
+                                    : llrs_model_load_safetensors(b, resolved.c_str(), quantization, out);
 }
 
 void llrs_model_free(llrs_model *m) { free_model(m); }

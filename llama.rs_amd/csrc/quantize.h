@@ -30,4 +30,7 @@ int launch_synth_encode(uint32_t ty, uint64_t key, size_t rows, size_t cols, flo
 int launch_encode(uint32_t ty, const float *vals, size_t rows, size_t cols, uint8_t *out,
                   size_t rbytes, hipStream_t s);
 
+// GPU: n F16 or BF16 values (device) widened to f32.
+int launch_widen(uint32_t ty, const void *src, size_t n, float *dst, hipStream_t s);
+
 }  // namespace llrs

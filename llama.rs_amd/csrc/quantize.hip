@@ -91,6 +91,23 @@ __global__ __launch_bounds__(64) void encode_kernel(const float *__restrict__ va
   }
 }
 
+// F16 / BF16 values widened to f32 with the host loader's conversions (a
+// bf16 NaN gets the quiet bit, as the host path sets it).
+__global__ void widen_kernel(uint32_t ty, const uint16_t *__restrict__ src, uint64_t n,
+                             float *__restrict__ dst) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint16_t h = src[i];
+    if (ty == LLRS_F16) {
+      dst[i] = enc::f16_to_f32(h);
+    } else {
+      uint32_t b = (uint32_t)h << 16;
+      if ((h & 0x7fffu) > 0x7f80u) b |= 0x00400000u;
+      dst[i] = enc::u2f(b);
+    }
+  }
+}
+
 static dim3 grid_for(uint64_t n) {
   uint64_t g = (n + 63) / 64;
   if (g > 65536) g = 65536;
@@ -126,6 +143,16 @@ int launch_encode(uint32_t ty, const float *vals, size_t rows, size_t cols, uint
     case LLRS_Q8_0: hipLaunchKernelGGL(encode_kernel<LLRS_Q8_0>, g, b, 0, s, vals, rows, cols, out, rbytes); break;
     default: return set_error(LLRS_E_UNSUPPORTED, "cannot encode %s", type_name(ty));
   }
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+int launch_widen(uint32_t ty, const void *src, size_t n, float *dst, hipStream_t s) {
+  if (ty != LLRS_F16 && ty != LLRS_BF16) return set_error(LLRS_E_UNSUPPORTED, "cannot widen %s", type_name(ty));
+  uint64_t g = (n + 255) / 256;
+  g = g > 8192 ? 8192 : g ? g : 1;
+  hipLaunchKernelGGL(widen_kernel, dim3((unsigned)g), dim3(256), 0, s, ty, (const uint16_t *)src,
+                     (uint64_t)n, dst);
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;
 }

@@ -1,6 +1,7 @@
 """Model-level mirror of the reference's CausalModel boundary over the C ABI.
 
-    ModelLoader.load_dynamic(path, LoadOptions)   src/loader.rs:37-42
+    ModelLoader.load_dynamic(path, LoadOptions)   src/loader.rs:37-77
+    GgufLoader / SafetensorsLoader .load          src/loader.rs:80-399
     HipQwen2Model.forward_token / prefill         src/architecture.rs:47-77
     KVCache (device-resident, + InferenceBuffers) src/cache.rs:4-101
     InferenceEngine.benchmark_tokens              src/engine.rs:189-223
@@ -63,6 +64,21 @@ class LlamaConfig:
     tie_word_embeddings: bool
 
 
+def _config_from_c(c: _ModelConfig) -> LlamaConfig:
+    return LlamaConfig(c.hidden_size, c.intermediate_size, c.num_attention_heads,
+                       c.num_key_value_heads, c.num_hidden_layers, c.vocab_size,
+                       c.max_position_embeddings, c.head_dim, c.kv_width, c.rms_norm_eps,
+                       c.rope_theta, bool(c.tie_word_embeddings))
+
+
+def hf_config(config_json_path) -> LlamaConfig:
+    """LlamaConfig::from_json + validate (src/config.rs:17-90) of a Qwen2
+    config.json (model_type checked as src/loader.rs:85-97 does)."""
+    c = _ModelConfig()
+    _check(lib().llrs_hf_config_read(str(config_json_path).encode(), C.byref(c)))
+    return _config_from_c(c)
+
+
 @dataclass
 class SynthConfig:
     """A synthetic Qwen2 model: shape, recipe and seed (llrs_synth_config)."""
@@ -101,10 +117,7 @@ class HipQwen2Model:
         self.handle = handle
         c = _ModelConfig()
         _check(lib().llrs_model_config_get(handle, C.byref(c)))
-        self._config = LlamaConfig(c.hidden_size, c.intermediate_size, c.num_attention_heads,
-                                   c.num_key_value_heads, c.num_hidden_layers, c.vocab_size,
-                                   c.max_position_embeddings, c.head_dim, c.kv_width,
-                                   c.rms_norm_eps, c.rope_theta, bool(c.tie_word_embeddings))
+        self._config = _config_from_c(c)
 
     @classmethod
     def synthetic(cls, backend: HipBackend, cfg: SynthConfig) -> "HipQwen2Model":
@@ -224,14 +237,43 @@ class KVCache:
 
 
 class ModelLoader:
-    """loader::ModelLoader (src/loader.rs:33-78), GGUF files only."""
+    """loader::ModelLoader (src/loader.rs:33-78): a .gguf file, a .safetensors
+    file (its directory), or a directory with a Hugging Face checkpoint or
+    exactly one .gguf file."""
 
     @staticmethod
-    def load_dynamic(path, backend: HipBackend,
-                     quantization: LoadQuantization = LoadQuantization.NONE) -> HipQwen2Model:
+    def load(path, backend: HipBackend,
+             quantization: LoadQuantization = LoadQuantization.NONE) -> HipQwen2Model:
+        h = P()
+        _check(lib().llrs_model_load(backend.handle, str(path).encode(), int(quantization),
+                                     C.byref(h)))
+        return HipQwen2Model(backend, h)
+
+    load_dynamic = load
+
+
+class GgufLoader:
+    """loader::GgufLoader (src/loader.rs:230-399)."""
+
+    @staticmethod
+    def load(path, backend: HipBackend,
+             quantization: LoadQuantization = LoadQuantization.NONE) -> HipQwen2Model:
         h = P()
         _check(lib().llrs_model_load_gguf(backend.handle, str(path).encode(), int(quantization),
                                           C.byref(h)))
+        return HipQwen2Model(backend, h)
+
+
+class SafetensorsLoader:
+    """loader::SafetensorsLoader (src/loader.rs:80-228): config.json plus
+    model.safetensors or the shards named by model.safetensors.index.json."""
+
+    @staticmethod
+    def load(model_dir, backend: HipBackend,
+             quantization: LoadQuantization = LoadQuantization.NONE) -> HipQwen2Model:
+        h = P()
+        _check(lib().llrs_model_load_safetensors(backend.handle, str(model_dir).encode(),
+                                                 int(quantization), C.byref(h)))
         return HipQwen2Model(backend, h)
 
 
