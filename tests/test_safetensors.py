@@ -382,3 +382,27 @@ def test_safetensors_load_errors(llrs, backend, tmp_path):
         llrs.ModelLoader.load(tmp_path / "b", backend)
     with pytest.raises(llrs.LlrsError, match="unknown quantization"):
         llrs.SafetensorsLoader.load(tmp_path / "b", backend, 7)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["BF16", "F16"])
+def test_gguf_half_matrices_quantize_like_safetensors(llrs, backend, tmp_path, dtype):
+    """GgufLoader's maybe_quantize on F16/BF16 matrices (src/loader.rs:406-447)
+    takes the same device path (raw upload, widen, encode): a GGUF file with
+    the checkpoint's half-precision matrices, loaded with q4km, holds the
+    same bytes as the checkpoint loaded with q4km."""
+    cfg = _tiny(llrs, num_hidden_layers=1, seed=31)
+    write_checkpoint(llrs, cfg, tmp_path / "ck", dtype)
+    half = llrs.SafetensorsLoader.load(tmp_path / "ck", backend)
+    half.export_gguf(tmp_path / "half.gguf")  # F16/BF16 matrices, f32 vectors
+    _, qt = llrs.gguf_read_tensor(tmp_path / "half.gguf", "blk.0.ffn_up.weight")
+    assert qt.quant_type == llrs.QuantType[dtype]
+    a = llrs.GgufLoader.load(tmp_path / "half.gguf", backend, llrs.LoadQuantization.Q4KM)
+    b = llrs.SafetensorsLoader.load(tmp_path / "ck", backend, llrs.LoadQuantization.Q4KM)
+    a.export_gguf(tmp_path / "a.gguf")
+    b.export_gguf(tmp_path / "b.gguf")
+    for g in ("token_embd.weight", "output.weight", "blk.0.attn_q.weight", "blk.0.attn_v.weight",
+              "blk.0.ffn_down.weight", "blk.0.ffn_gate.weight", "blk.0.attn_norm.weight"):
+        _, x = llrs.gguf_read_tensor(tmp_path / "a.gguf", g)
+        _, y = llrs.gguf_read_tensor(tmp_path / "b.gguf", g)
+        assert (x.quant_type, x.data) == (y.quant_type, y.data), g
