@@ -22,7 +22,8 @@ __device__ __forceinline__ int bounded_pos(const int *pos, int max_seq) {
 
 // ------------------------------------------------------------------ attention
 //
-// One wave per (query head, chunk of kChunk positions); chunks past the
+// One wave per (query head, item of attention_span(pos) consecutive chunks
+// of kChunk positions: one chunk up to 2,048 positions); items past the
 // current position exit at once, so one grid (sized for the whole context)
 // serves every position of a captured graph.  Per chunk: split-half RoPE
 // (src/model.rs:87-95) on the head's query, scores q.k * 1/sqrt(hd), softmax
@@ -44,6 +45,14 @@ __device__ __forceinline__ int bounded_pos(const int *pos, int max_seq) {
 // back to uniform, as softmax_inplace does.
 
 constexpr int kChunk = 32;  // positions per wave: lane = (half of the head, position)
+// Sub-chunks per attention item at position pos: one up to kMaxParts
+// chunks, then as many as keep a head's partials at most kMaxParts, so that
+// the merge reads at most kMaxParts partials however long the context.
+constexpr int kMaxParts = 64;
+__host__ __device__ __forceinline__ int attention_span(int pos) {
+  const int n = pos / kChunk + 1;
+  return (n + kMaxParts - 1) / kMaxParts;
+}
 
 // A partial's value with its tag in one single-copy-atomic 64-bit word.
 __device__ __forceinline__ void store_tagged(unsigned long long *p, float v, unsigned tag) {
@@ -70,7 +79,9 @@ __device__ __forceinline__ bool merge_wait_over(unsigned long long &t0, unsigned
 // One (query head, chunk) item, run by one wave.  COH: the output is read by
 // other workgroups of the same launch (the persistent decode kernel), so it is
 // stored at device scope.  qs and kn are the wave's own LDS (HD floats each).
-template <int HD, bool COH>
+// MULTI: the instantiation for attention_span(pos) > 1 (the other one
+// assumes single-chunk items and keeps their code straight-line).
+template <int HD, bool COH, bool MULTI>
 __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, float *qs, float *kn) {
   constexpr int KH = HD / 2;              // dimensions per score lane
   constexpr int NK4 = KH / 4;             // their float4s
@@ -83,19 +94,20 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
 
   const int G = a.nh / a.nkv, kvw = a.nkv * HD;
   const int kvh = h / G;
-  const int c0 = chunk * kChunk;
+  const int S = MULTI ? attention_span(pos) : 1, span = S * kChunk;
+  const int c0 = chunk * span;  // this item: positions [c0, c0 + span), S sub-chunks
   if (c0 > pos) return;
-  const int n_active = pos / kChunk + 1;
-  const int c1 = min(c0 + kChunk, pos + 1);  // exclusive
-  const bool owns_new = pos < c1;
+  const int n_active = pos / span + 1;  // items of the head
+  const bool owns_new = pos < c0 + span;
   const int lane = thread_x() & 63, half = lane >> 5, pl = lane & 31;
   const float *kc = a.k_cache + (size_t)kvh * HD, *vc = a.v_cache + (size_t)kvh * HD;
 
   // 1. Loads, all issued up front: this lane's query and new-key pair
   //    (i, i + KH) with its RoPE factors and its dimensions of the new value;
-  //    then the chunk's keys (lane = half x position, KH dims) and values
-  //    (lane = VW consecutive dims of row lane / VL, RV rows per load).  Rows
-  //    past the chunk's end are clamped onto its first row and masked later.
+  //    then the first sub-chunk's keys (lane = half x position, KH dims) and
+  //    values (lane = VW consecutive dims of row lane / VL, RV rows per
+  //    load).  Rows past the sub-chunk's end are clamped onto its first row
+  //    and masked later.
   const int ri = lane & (KH - 1);
   const float *cs = a.rope + (size_t)pos * HD, *sn = cs + KH;
   const float *qx = a.q + (size_t)h * HD, *kx = a.k + kvh * HD, *vx = a.v + kvh * HD;
@@ -107,17 +119,18 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
   const int vd = (lane % VL) * VW, vr0 = lane / VL;
   const VT vnew = *reinterpret_cast<const VT *>(vx + vd);
   float4 kr[NK4];
-  {
-    const float *kp = kc + (size_t)(c0 + pl < c1 ? c0 + pl : c0) * kvw + half * KH;
+  VT vv[NVI];
+  auto load_rows = [&](int s0, int s1) {
+    const float *kp = kc + (size_t)(s0 + pl < s1 ? s0 + pl : s0) * kvw + half * KH;
 #pragma unroll
     for (int j = 0; j < NK4; j++) kr[j] = *reinterpret_cast<const float4 *>(kp + 4 * j);
-  }
-  VT vv[NVI];
 #pragma unroll
-  for (int i = 0; i < NVI; i++) {
-    const int p = c0 + i * RV + vr0;
-    vv[i] = *reinterpret_cast<const VT *>(vc + (size_t)(p < c1 ? p : c0) * kvw + vd);
-  }
+    for (int i = 0; i < NVI; i++) {
+      const int p = s0 + i * RV + vr0;
+      vv[i] = *reinterpret_cast<const VT *>(vc + (size_t)(p < s1 ? p : s0) * kvw + vd);
+    }
+  };
+  load_rows(c0, min(c0 + kChunk, pos + 1));
 
   // 2. Rotated query and new key in LDS; the group's first head appends the
   //    new key and value to the cache.
@@ -138,60 +151,90 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
   // The wave's LDS writes complete before its reads below.
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   __builtin_amdgcn_wave_barrier();
-  if (owns_new) {
-    if (c0 + pl == pos) {
-#pragma unroll
-      for (int j = 0; j < NK4; j++) kr[j] = *reinterpret_cast<const float4 *>(kn + half * KH + 4 * j);
-    }
-#pragma unroll
-    for (int i = 0; i < NVI; i++)
-      if (c0 + i * RV + vr0 == pos) vv[i] = vnew;
-  }
 
-  // 3. Score of position pl (both halves end with the full dot), softmax partials.
-  float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < NK4; j++) {
-    const float4 q4 = *reinterpret_cast<const float4 *>(qs + half * KH + 4 * j);
-    s += q4.x * kr[j].x + q4.y * kr[j].y + q4.z * kr[j].z + q4.w * kr[j].w;
-  }
-  s += __shfl_xor(s, 32, 64);
-  const bool valid = c0 + pl < c1;
-  s = valid ? s * a.scale : -INFINITY;
-  float m = s;
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  const float x = valid ? expf(s - m) : 0.f;
-  float l = x;
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-
-  // 4. Exp-weighted and plain V sums of the lane's VW dimensions.
-  float O[VW], Vs[VW];
+  // 3-4. Per sub-chunk: scores of positions pl (both halves end with the
+  //    full dot), the softmax partials, exp-weighted and plain V sums of the
+  //    lane's VW dimensions; sub-chunks after the first fold in with the
+  //    running-max rescaling (their rows load after the previous one's sums).
+  float m = -INFINITY, l = 0.f, O[VW], Vs[VW];
 #pragma unroll
   for (int k = 0; k < VW; k++) O[k] = Vs[k] = 0.f;
+  for (int sub = 0; sub < S; sub++) {
+    const int s0 = c0 + sub * kChunk;
+    if (s0 > pos) break;
+    const int s1 = min(s0 + kChunk, pos + 1);  // exclusive
+    if (sub > 0) load_rows(s0, s1);
+    if (s0 <= pos && pos < s1) {  // the row this step appends, from registers / LDS
+      if (s0 + pl == pos) {
 #pragma unroll
-  for (int i = 0; i < NVI; i++) {
-    const int p = i * RV + vr0;  // position within the chunk
-    float wp;  // exp weight of position p, held by lane p
-    if constexpr (RV == 1)
-      wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i));
-    else
-      wp = __shfl(x, p, 64);
-    const bool in = c0 + p < c1;  // a clamped row adds nothing, whatever it holds
-    const float *e = reinterpret_cast<const float *>(&vv[i]);
+        for (int j = 0; j < NK4; j++) kr[j] = *reinterpret_cast<const float4 *>(kn + half * KH + 4 * j);
+      }
 #pragma unroll
-    for (int k = 0; k < VW; k++) {
-      O[k] += in ? wp * e[k] : 0.f;
-      Vs[k] += in ? e[k] : 0.f;
+      for (int i = 0; i < NVI; i++)
+        if (s0 + i * RV + vr0 == pos) vv[i] = vnew;
     }
-  }
+    float sc = 0.f;
 #pragma unroll
-  for (int o = VL; o < 64; o <<= 1) {
+    for (int j = 0; j < NK4; j++) {
+      const float4 q4 = *reinterpret_cast<const float4 *>(qs + half * KH + 4 * j);
+      sc += q4.x * kr[j].x + q4.y * kr[j].y + q4.z * kr[j].z + q4.w * kr[j].w;
+    }
+    sc += __shfl_xor(sc, 32, 64);
+    const bool valid = s0 + pl < s1;
+    sc = valid ? sc * a.scale : -INFINITY;
+    float ms = sc;
 #pragma unroll
-    for (int k = 0; k < VW; k++) {
-      O[k] += __shfl_xor(O[k], o, 64);
-      Vs[k] += __shfl_xor(Vs[k], o, 64);
+    for (int o = 16; o > 0; o >>= 1) ms = fmaxf(ms, __shfl_xor(ms, o, 64));
+    const float x = valid ? expf(sc - ms) : 0.f;
+    float ls = x;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) ls += __shfl_xor(ls, o, 64);
+    float Os[VW], Vss[VW];
+#pragma unroll
+    for (int k = 0; k < VW; k++) Os[k] = Vss[k] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NVI; i++) {
+      const int p = i * RV + vr0;  // position within the sub-chunk
+      float wp;  // exp weight of position p, held by lane p
+      if constexpr (RV == 1)
+        wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i));
+      else
+        wp = __shfl(x, p, 64);
+      const bool in = s0 + p < s1;  // a clamped row adds nothing, whatever it holds
+      const float *e = reinterpret_cast<const float *>(&vv[i]);
+#pragma unroll
+      for (int k = 0; k < VW; k++) {
+        Os[k] += in ? wp * e[k] : 0.f;
+        Vss[k] += in ? e[k] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int o = VL; o < 64; o <<= 1) {
+#pragma unroll
+      for (int k = 0; k < VW; k++) {
+        Os[k] += __shfl_xor(Os[k], o, 64);
+        Vss[k] += __shfl_xor(Vss[k], o, 64);
+      }
+    }
+    if (sub == 0) {  // one sub-chunk: exactly its own partial
+      m = ms;
+      l = ls;
+#pragma unroll
+      for (int k = 0; k < VW; k++) {
+        O[k] = Os[k];
+        Vs[k] = Vss[k];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < VW; k++) Vs[k] += Vss[k];
+      if (ms != -INFINITY) {
+        const float mn = fmaxf(m, ms);
+        const float sa = m == -INFINITY ? 0.f : expf(m - mn), sb = expf(ms - mn);
+        l = l * sa + ls * sb;
+#pragma unroll
+        for (int k = 0; k < VW; k++) O[k] = O[k] * sa + Os[k] * sb;
+        m = mn;
+      }
     }
   }
 

@@ -78,7 +78,11 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
   // Grid (head, chunk): the low chunks, the ones that run, are dispatched
   // first, so the chunk that merges a head always starts after the chunks it
   // waits for.
-  attention_item<HD, false>(a, blockIdx.x, blockIdx.y, bounded_pos(a.pos, a.max_seq), qs, kn);
+  const int pos = bounded_pos(a.pos, a.max_seq);
+  if (attention_span(pos) > 1)
+    attention_item<HD, false, true>(a, blockIdx.x, blockIdx.y, pos, qs, kn);
+  else
+    attention_item<HD, false, false>(a, blockIdx.x, blockIdx.y, pos, qs, kn);
 }
 
 // silu(gate) * up (src/model.rs:251-254).

@@ -81,7 +81,7 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
   // Item i: XCD x = i % 8, r = i / 8, head j = r % G of pair q * 8 + x with
   // q = r / G; pair = chunk * nkv + kv head.
   const int G = p.attn.nh / p.attn.nkv;
-  const int n_pairs = p.attn.nkv * (pos / kChunk + 1);
+  const int n_pairs = p.attn.nkv * (pos / (attention_span(pos) * kChunk) + 1);
   const int n_items = (n_pairs + 7) / 8 * 8 * G;
   const unsigned epoch = *p.attn.epoch;  // advanced by this step's embedding launch
   unsigned k = 0;
@@ -109,11 +109,15 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
       a.v_cache += l * p.cache_stride;
       a.tag = epoch * (unsigned)p.nlayers + (unsigned)l;
       bar_wait(p.bar, p.err, nwg, k);
+      const bool multi = attention_span(pos) > 1;
       for (int it = wave * nwg + wg; it < n_items; it += nwg * nwv) {
         const int r = it >> 3, pair = (r / G) * 8 + (it & 7);
-        if (pair < n_pairs)
-          attention_item<HD, true>(a, (pair % a.nkv) * G + r % G, pair / a.nkv, pos, aqs[wave],
-                                   akn[wave]);
+        if (pair >= n_pairs) continue;
+        const int hh = (pair % a.nkv) * G + r % G, item = pair / a.nkv;
+        if (multi)
+          attention_item<HD, true, true>(a, hh, item, pos, aqs[wave], akn[wave]);
+        else
+          attention_item<HD, true, false>(a, hh, item, pos, aqs[wave], akn[wave]);
       }
       bar_arrive(p.bar, wg);
       k++;
