@@ -44,15 +44,6 @@ __device__ __forceinline__ int bounded_pos(const int *pos, int max_seq) {
 // contributes exp(-inf) = 0; without a finite positive total the weights fall
 // back to uniform, as softmax_inplace does.
 
-constexpr int kChunk = 32;  // positions per wave: lane = (half of the head, position)
-// Sub-chunks per attention item at position pos: one up to kMaxParts
-// chunks, then as many as keep a head's partials at most kMaxParts, so that
-// the merge reads at most kMaxParts partials however long the context.
-constexpr int kMaxParts = 64;
-__host__ __device__ __forceinline__ int attention_span(int pos) {
-  const int n = pos / kChunk + 1;
-  return (n + kMaxParts - 1) / kMaxParts;
-}
 
 // A partial's value with its tag in one single-copy-atomic 64-bit word.
 __device__ __forceinline__ void store_tagged(unsigned long long *p, float v, unsigned tag) {

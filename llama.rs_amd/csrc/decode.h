@@ -7,6 +7,17 @@
 
 namespace llrs {
 
+// Decode attention items.
+constexpr int kChunk = 32;  // positions per wave: lane = (half of the head, position)
+// Sub-chunks per attention item at position pos: one up to kMaxParts
+// chunks, then as many as keep a head's partials at most kMaxParts, so that
+// the merge reads at most kMaxParts partials however long the context.
+constexpr int kMaxParts = 64;
+__host__ __device__ inline int attention_span(int pos) {
+  const int n = pos / kChunk + 1;
+  return (n + kMaxParts - 1) / kMaxParts;
+}
+
 // Fused RoPE + KV append + GQA attention of one layer.
 struct AttnArgs {
   const float *q, *k, *v;  // projections of the current token (q, k before RoPE)

@@ -50,6 +50,8 @@ bool decode_persistent_supports(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, uint
                                 uint32_t t_down, int head_dim);
 int launch_decode_persistent(const PersistentArgs &p, uint32_t t_qkv, uint32_t t_v, uint32_t t_o,
                              uint32_t t_gu, uint32_t t_down, int head_dim, int grid, size_t lds,
-                             hipStream_t s);
+                             hipStream_t s, bool long_items);
+// Whether a step at position pos should launch the long_items instantiation.
+inline bool persistent_long_items(size_t pos) { return attention_span((int)pos) > 1; }
 
 }  // namespace llrs

@@ -67,7 +67,10 @@ __device__ void bar_wait(unsigned *bar, unsigned *err, int nwg, unsigned k) {
 
 typedef const __attribute__((address_space(4))) PersistentLayer ConstLayer;
 
-template <uint32_t TQ, uint32_t TV, uint32_t TO, uint32_t TGU, uint32_t TD, int HD>
+// LONG: the instantiation whose attention also has the multi-chunk items of
+// positions past 2,048 (the other one keeps the single-chunk path's register
+// allocation; it stays correct at any position, with more partials to merge).
+template <uint32_t TQ, uint32_t TV, uint32_t TO, uint32_t TGU, uint32_t TD, int HD, bool LONG>
 __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(PersistentArgs p) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[16];
@@ -81,7 +84,8 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
   // Item i: XCD x = i % 8, r = i / 8, head j = r % G of pair q * 8 + x with
   // q = r / G; pair = chunk * nkv + kv head.
   const int G = p.attn.nh / p.attn.nkv;
-  const int n_pairs = p.attn.nkv * (pos / (attention_span(pos) * kChunk) + 1);
+  const int span = LONG ? attention_span(pos) : 1;
+  const int n_pairs = p.attn.nkv * (pos / (span * kChunk) + 1);
   const int n_items = (n_pairs + 7) / 8 * 8 * G;
   const unsigned epoch = *p.attn.epoch;  // advanced by this step's embedding launch
   unsigned k = 0;
@@ -109,15 +113,18 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
       a.v_cache += l * p.cache_stride;
       a.tag = epoch * (unsigned)p.nlayers + (unsigned)l;
       bar_wait(p.bar, p.err, nwg, k);
-      const bool multi = attention_span(pos) > 1;
+      const bool multi = span > 1;
       for (int it = wave * nwg + wg; it < n_items; it += nwg * nwv) {
         const int r = it >> 3, pair = (r / G) * 8 + (it & 7);
         if (pair >= n_pairs) continue;
         const int hh = (pair % a.nkv) * G + r % G, item = pair / a.nkv;
-        if (multi)
-          attention_item<HD, true, true>(a, hh, item, pos, aqs[wave], akn[wave]);
-        else
-          attention_item<HD, true, false>(a, hh, item, pos, aqs[wave], akn[wave]);
+        if constexpr (LONG) {
+          if (multi) {
+            attention_item<HD, true, true>(a, hh, item, pos, aqs[wave], akn[wave]);
+            continue;
+          }
+        }
+        attention_item<HD, true, false>(a, hh, item, pos, aqs[wave], akn[wave]);
       }
       bar_arrive(p.bar, wg);
       k++;
@@ -150,13 +157,15 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
 }
 
 template <uint32_t TQ, uint32_t TV, uint32_t TO, uint32_t TGU, uint32_t TD>
-int launch_types(const PersistentArgs &p, int head_dim, int grid, size_t lds, hipStream_t s) {
+int launch_types(const PersistentArgs &p, int head_dim, int grid, size_t lds, hipStream_t s, bool lng) {
   const dim3 g((unsigned)grid), b(kPersistentThreads);
+#define PK(HD, L) hipLaunchKernelGGL((decode_persistent_kernel<TQ, TV, TO, TGU, TD, HD, L>), g, b, lds, s, p)
   switch (head_dim) {
-    case 64: hipLaunchKernelGGL((decode_persistent_kernel<TQ, TV, TO, TGU, TD, 64>), g, b, lds, s, p); break;
-    case 128: hipLaunchKernelGGL((decode_persistent_kernel<TQ, TV, TO, TGU, TD, 128>), g, b, lds, s, p); break;
+    case 64: if (lng) PK(64, true); else PK(64, false); break;
+    case 128: if (lng) PK(128, true); else PK(128, false); break;
     default: return set_error(LLRS_E_UNSUPPORTED, "persistent decode: head_dim %d", head_dim);
   }
+#undef PK
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;
 }
@@ -180,16 +189,16 @@ bool decode_persistent_supports(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, uint
 
 int launch_decode_persistent(const PersistentArgs &p, uint32_t t_qkv, uint32_t t_v, uint32_t t_o,
                              uint32_t t_gu, uint32_t t_down, int head_dim, int grid, size_t lds,
-                             hipStream_t s) {
+                             hipStream_t s, bool long_items) {
   if (grid < 1) return set_error(LLRS_E_INVALID, "persistent decode: grid %d", grid);
   if (lds + persistent_static_lds(head_dim) > kCuLds)
     return set_error(LLRS_E_UNSUPPORTED, "persistent decode needs %zu bytes of LDS", lds);
   if (t_qkv == LLRS_Q4_K && t_v == LLRS_Q8_0 && t_down == LLRS_Q6_K)
-    return launch_types<LLRS_Q4_K, LLRS_Q8_0, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q6_K>(p, head_dim, grid, lds, s);
+    return launch_types<LLRS_Q4_K, LLRS_Q8_0, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q6_K>(p, head_dim, grid, lds, s, long_items);
   if (t_qkv == LLRS_Q5_0)
-    return launch_types<LLRS_Q5_0, LLRS_Q8_0, LLRS_Q5_0, LLRS_Q5_0, LLRS_Q6_K>(p, head_dim, grid, lds, s);
+    return launch_types<LLRS_Q5_0, LLRS_Q8_0, LLRS_Q5_0, LLRS_Q5_0, LLRS_Q6_K>(p, head_dim, grid, lds, s, long_items);
   if (t_qkv == LLRS_Q4_K && t_v == LLRS_Q4_K)
-    return launch_types<LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K>(p, head_dim, grid, lds, s);
+    return launch_types<LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K>(p, head_dim, grid, lds, s, long_items);
   return set_error(LLRS_E_UNSUPPORTED, "persistent decode: no instantiation for these weight types");
 }
 

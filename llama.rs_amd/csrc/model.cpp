@@ -90,8 +90,10 @@ struct llrs_kv {
   size_t p_lds = 0;
   uint32_t p_types[5] = {};
   uint32_t *pinned = nullptr;  // host staging, max_seq_len + 2 words
-  hipGraph_t graph[2] = {nullptr, nullptr};
-  hipGraphExec_t exec[2] = {nullptr, nullptr};
+  // Captured steps: [logits mode + 2 * long] (long: the persistent kernel's
+  // instantiation for positions past 2,048).
+  hipGraph_t graph[4] = {};
+  hipGraphExec_t exec[4] = {};
   std::vector<void *> allocs;
   // Multi-token prefill buffers (allocated on first use, pf_cap token rows).
   size_t pf_cap = 0;
@@ -649,7 +651,7 @@ static AttnArgs attention_args(llrs_model *m, llrs_kv *kv, size_t l) {
 }
 
 // The step's layers: one persistent launch, or five launches per layer.
-static int enqueue_layers(llrs_model *m, llrs_kv *kv) {
+static int enqueue_layers(llrs_model *m, llrs_kv *kv, bool long_items) {
   const llrs_model_config &c = m->cfg;
   hipStream_t s = m->b->stream;
   if (kv->p_layers) {
@@ -663,7 +665,7 @@ static int enqueue_layers(llrs_model *m, llrs_kv *kv) {
     p.err = kv->p_err;
     const uint32_t *t = kv->p_types;
     return launch_decode_persistent(p, t[0], t[1], t[2], t[3], t[4], (int)c.head_dim, kv->p_grid,
-                                    kv->p_lds, s);
+                                    kv->p_lds, s, long_items);
   }
   for (size_t l = 0; l < c.num_hidden_layers; l++) {
     LLRS_TRY(launch_projection(m, kv, l, P_QKV, s));
@@ -682,11 +684,11 @@ static int enqueue_embed(llrs_model *m, llrs_kv *kv) {
                       kv->epoch, m->b->stream, kv->p_bar, kv->p_bar ? kPersistentBarWords : 0);
 }
 
-static int enqueue_step(llrs_model *m, llrs_kv *kv, int mode) {
+static int enqueue_step(llrs_model *m, llrs_kv *kv, int mode, bool long_items) {
   hipStream_t s = m->b->stream;
   const int max_seq = (int)kv->max_seq_len;
   LLRS_TRY(enqueue_embed(m, kv));
-  LLRS_TRY(enqueue_layers(m, kv));
+  LLRS_TRY(enqueue_layers(m, kv, long_items));
   if (mode == LLRS_LOGITS_COMPUTE) {
     LLRS_TRY(launch_projection(m, kv, 0, P_LM_HEAD, s));
   } else {
@@ -700,13 +702,16 @@ static bool use_graphs() {
   return !(e && *e && *e != '0');
 }
 
-// One step, replayed from a captured hipGraph (captured on first use).
-static int run_step(llrs_model *m, llrs_kv *kv, int mode) {
-  if (!use_graphs()) return enqueue_step(m, kv, mode);
+// One step at position pos (known to the host; the graph reads it from the
+// device), replayed from a captured hipGraph (captured on first use).
+static int run_step(llrs_model *m, llrs_kv *kv, int mode, size_t pos) {
+  const bool lng = persistent_long_items(pos);
+  if (!use_graphs()) return enqueue_step(m, kv, mode, lng);
   hipStream_t s = m->b->stream;
-  if (!kv->exec[mode]) {
+  const int gi = mode + 2 * (lng ? 1 : 0);
+  if (!kv->exec[gi]) {
     LLRS_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(m, kv, mode);
+    int rc = enqueue_step(m, kv, mode, lng);
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(s, &g);
     if (rc != LLRS_OK) {
@@ -714,10 +719,10 @@ static int run_step(llrs_model *m, llrs_kv *kv, int mode) {
       return rc;
     }
     if (e != hipSuccess) return set_error(LLRS_E_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
-    kv->graph[mode] = g;
-    LLRS_HIP(hipGraphInstantiate(&kv->exec[mode], g, nullptr, nullptr, 0));
+    kv->graph[gi] = g;
+    LLRS_HIP(hipGraphInstantiate(&kv->exec[gi], g, nullptr, nullptr, 0));
   }
-  LLRS_HIP(hipGraphLaunch(kv->exec[mode], s));
+  LLRS_HIP(hipGraphLaunch(kv->exec[gi], s));
   return LLRS_OK;
 }
 
@@ -843,7 +848,7 @@ static void free_kv(llrs_kv *kv) {
   if (!kv) return;
   (void)hipSetDevice(kv->m->b->device);
   (void)hipStreamSynchronize(kv->m->b->stream);
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < 4; i++) {
     if (kv->exec[i]) (void)hipGraphExecDestroy(kv->exec[i]);
     if (kv->graph[i]) (void)hipGraphDestroy(kv->graph[i]);
   }
@@ -1214,7 +1219,7 @@ int llrs_forward_token(llrs_model *m, llrs_kv *kv, uint32_t token, size_t pos, i
     return set_error(LLRS_E_INVALID, "unknown logits mode %d", logits_mode);
   LLRS_HIP(hipSetDevice(m->b->device));
   LLRS_TRY(stage_tokens(kv, &token, 1, pos));
-  LLRS_TRY(run_step(m, kv, logits_mode));
+  LLRS_TRY(run_step(m, kv, logits_mode, pos));
   LLRS_HIP(hipStreamSynchronize(m->b->stream));
   return check_persistent(kv);
 }
@@ -1237,7 +1242,7 @@ int llrs_prefill(llrs_model *m, llrs_kv *kv, const uint32_t *tokens, size_t n, s
     LLRS_TRY(prefill_batched(m, kv, start_pos, n));
   } else {
     for (size_t i = 0; i < n; i++)
-      LLRS_TRY(run_step(m, kv, i + 1 == n ? LLRS_LOGITS_COMPUTE : LLRS_LOGITS_SKIP));
+      LLRS_TRY(run_step(m, kv, i + 1 == n ? LLRS_LOGITS_COMPUTE : LLRS_LOGITS_SKIP, start_pos + i));
   }
   LLRS_HIP(hipStreamSynchronize(m->b->stream));
   return check_persistent(kv);
@@ -1257,7 +1262,7 @@ int llrs_decode_greedy(llrs_model *m, llrs_kv *kv, size_t start_pos, size_t n_st
   // token = argmax(current logits) for position start_pos; nothing advances.
   LLRS_TRY(launch_argmax(kv->logits, (int)m->cfg.vocab_size, kv->pos, (int)kv->max_seq_len,
                          kv->tok_by_pos, kv->next_token, 0, s));
-  for (size_t i = 0; i < n_steps; i++) LLRS_TRY(run_step(m, kv, LLRS_LOGITS_COMPUTE));
+  for (size_t i = 0; i < n_steps; i++) LLRS_TRY(run_step(m, kv, LLRS_LOGITS_COMPUTE, start_pos + i));
   LLRS_HIP(hipMemcpyAsync(kv->pinned, kv->tok_by_pos + start_pos, n_steps * 4,
                           hipMemcpyDeviceToHost, s));
   LLRS_HIP(hipStreamSynchronize(s));
@@ -1387,7 +1392,7 @@ int llrs_profile_projection(llrs_model *m, llrs_kv *kv, int which, int iters, do
     for (int it = -1; it < iters && rc == LLRS_OK && e == hipSuccess; it++) {  // round -1 warms
       rc = enqueue_embed(m, kv);
       if (rc == LLRS_OK) e = hipEventRecord(ev[2 * (it + 1)], s);
-      if (rc == LLRS_OK && e == hipSuccess) rc = enqueue_layers(m, kv);
+      if (rc == LLRS_OK && e == hipSuccess) rc = enqueue_layers(m, kv, persistent_long_items((size_t)saved_pos));
       if (rc == LLRS_OK && e == hipSuccess) e = hipEventRecord(ev[2 * (it + 1) + 1], s);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(s);

@@ -92,13 +92,14 @@ def test_head_dim_128_long_context(llrs, backend, oracle, tmp_path):
 def test_attention_items_of_two_chunks(llrs, backend, oracle, tmp_path):
     """Past 64 chunks (2,048 positions) an attention item covers consecutive
     chunks, folded in the wave with the running-max rescaling, so a head
-    merges at most 64 partials: a 2,100-token context decodes with items of
-    two chunks.  (Seed 43: the oracle's top-2 logit gap stays above 1.5e-2 on
-    every step.)"""
+    merges at most 64 partials.  The decode runs from position 2,030 across
+    2,048: single-chunk items (and the persistent launch without the
+    multi-chunk path) first, items of two chunks after.  (Seed 43: the
+    oracle's top-2 logit gap stays above 4.5e-3 on every step.)"""
     cfg = tiny_cfg(llrs, hidden_size=1024, num_attention_heads=8, num_key_value_heads=2,
                    intermediate_size=1024, num_hidden_layers=1, vocab_size=600,
                    max_position_embeddings=4096, seed=43)
-    prompt = np.random.default_rng(43).integers(0, cfg.vocab_size, 2100).astype(np.uint32)
+    prompt = np.random.default_rng(43).integers(0, cfg.vocab_size, 2030).astype(np.uint32)
     compare_run(llrs, backend, oracle, cfg, tmp_path / "s.gguf", prompt, 32, 2200)
 
 
