@@ -18,6 +18,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <thread>
 #include <new>
 #include <string>
 #include <vector>
@@ -135,14 +136,62 @@ static int validate_config(llrs_model_config &c) {
   return LLRS_OK;
 }
 
+// Host staging of a model load: two pinned buffers that the mapped
+// checkpoint bytes are copied into by several threads (the page faults of the
+// mapping spread over them), and a copy stream (default priority) whose
+// transfers overlap the encoding of the previous chunk on the backend stream.
+struct LoadStaging {
+  static constexpr size_t kCap = 64u << 20;
+  llrs_backend *b = nullptr;
+  hipStream_t cs = nullptr;
+  uint8_t *pin[2] = {nullptr, nullptr};
+  hipEvent_t copied[2] = {nullptr, nullptr};
+  ~LoadStaging() {
+    if (cs) (void)hipStreamSynchronize(cs);
+    if (b) (void)hipStreamSynchronize(b->stream);
+    for (int i = 0; i < 2; i++) {
+      if (pin[i]) (void)hipHostFree(pin[i]);
+      if (copied[i]) (void)hipEventDestroy(copied[i]);
+    }
+    if (cs) (void)hipStreamDestroy(cs);
+  }
+  int init(llrs_backend *be) {
+    b = be;
+    LLRS_HIP(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking));
+    for (int i = 0; i < 2; i++) {
+      LLRS_HIP(hipHostMalloc((void **)&pin[i], kCap, hipHostMallocDefault));
+      LLRS_HIP(hipEventCreateWithFlags(&copied[i], hipEventDisableTiming));
+    }
+    return LLRS_OK;
+  }
+};
+
+static void parallel_copy(uint8_t *dst, const uint8_t *src, size_t n) {
+  const size_t kMinPart = 4u << 20;
+  const unsigned nt = (unsigned)std::min<size_t>(8, std::max<size_t>(1, n / kMinPart));
+  if (nt == 1) {
+    memcpy(dst, src, n);
+    return;
+  }
+  std::vector<std::thread> th;
+  const size_t part = (n + nt - 1) / nt;
+  for (unsigned i = 0; i < nt; i++) {
+    const size_t o = i * part, len = o < n ? std::min(part, n - o) : 0;
+    if (len) th.emplace_back([=] { memcpy(dst + o, src + o, len); });
+  }
+  for (auto &t : th) t.join();
+}
+
 // maybe_quantize (src/loader.rs:406-447) on the GPU: the F32/F16/BF16 source
 // bytes are uploaded as they are, widened to f32 on the device and encoded
 // by the same encoders the host quantizer uses (bit-identical).  want may be
-// LLRS_F32 (a recipe fallback), which keeps the widened values.
+// LLRS_F32 (a recipe fallback), which keeps the widened values.  With
+// staging, the rows go up in chunks of at most 64 MB through its pinned
+// buffers, each chunk widened and encoded while the next one is staged.
 static int quantize_on_device(llrs_backend *b, uint32_t want, uint32_t src_ty, const uint8_t *src,
-                              size_t rows, size_t cols, llrs_tensor **out) {
-  const size_t n = rows * cols;
-  if (want == LLRS_F32 && src_ty == LLRS_F32)
+                              size_t rows, size_t cols, llrs_tensor **out, LoadStaging *st = nullptr) {
+  const size_t n = rows * cols, es = src_ty == LLRS_F32 ? 4 : 2;
+  if (want == LLRS_F32 && src_ty == LLRS_F32 && !st)
     return llrs_tensor_upload(b, src, n * 4, LLRS_F32, rows, cols, out);
   llrs_tensor *t = nullptr;
   void *raw = nullptr;
@@ -155,18 +204,36 @@ static int quantize_on_device(llrs_backend *b, uint32_t want, uint32_t src_ty, c
       e = hipMalloc(&dv, n * 4 + 4);
       vals = dv;
     }
-    if (e == hipSuccess) {
-      if (src_ty == LLRS_F32) {
-        e = hipMemcpyAsync(vals, src, n * 4, hipMemcpyHostToDevice, b->stream);
+    if (e == hipSuccess && src_ty != LLRS_F32) e = hipMalloc(&raw, n * 2 + 4);
+    // Rows per chunk: whole rows within the staging buffer (all rows without staging).
+    const size_t row_src = cols * es;
+    const size_t per = st ? std::max<size_t>(1, LoadStaging::kCap / std::max<size_t>(row_src, 1)) : rows;
+    if (st && row_src > LoadStaging::kCap) rc = set_error(LLRS_E_UNSUPPORTED, "a %zu-byte row exceeds the load staging", row_src);
+    for (size_t r0 = 0, i = 0; r0 < rows && e == hipSuccess && rc == LLRS_OK; r0 += per, i++) {
+      const size_t r1 = std::min(rows, r0 + per), off = r0 * row_src, len = (r1 - r0) * row_src;
+      uint8_t *dst = src_ty == LLRS_F32 ? (uint8_t *)(vals + r0 * cols) : (uint8_t *)raw + off;
+      if (st) {
+        const int k = (int)(i & 1);
+        e = hipEventSynchronize(st->copied[k]);  // the DMA that last read this buffer is done
+        if (e != hipSuccess) break;
+        parallel_copy(st->pin[k], src + off, len);
+        e = hipMemcpyAsync(dst, st->pin[k], len, hipMemcpyHostToDevice, st->cs);
+        if (e == hipSuccess) e = hipEventRecord(st->copied[k], st->cs);
+        if (e == hipSuccess) e = hipStreamWaitEvent(b->stream, st->copied[k], 0);
       } else {
-        e = hipMalloc(&raw, n * 2 + 4);
-        if (e == hipSuccess) e = hipMemcpyAsync(raw, src, n * 2, hipMemcpyHostToDevice, b->stream);
-        if (e == hipSuccess) rc = launch_widen(src_ty, raw, n, vals, b->stream);
+        e = hipMemcpyAsync(dst, src + off, len, hipMemcpyHostToDevice, b->stream);
       }
+      if (e == hipSuccess && src_ty != LLRS_F32)
+        rc = launch_widen(src_ty, dst, (r1 - r0) * cols, vals + r0 * cols, b->stream);
+      if (e == hipSuccess && rc == LLRS_OK && want != LLRS_F32)
+        rc = launch_encode(want, vals + r0 * cols, r1 - r0, cols, t->dev + r0 * t->row_bytes, t->row_bytes,
+                           b->stream);
     }
-    if (e == hipSuccess && rc == LLRS_OK && want != LLRS_F32)
-      rc = launch_encode(want, vals, rows, cols, t->dev, t->row_bytes, b->stream);
     if (e == hipSuccess && rc == LLRS_OK) e = hipStreamSynchronize(b->stream);
+  }
+  if (rc != LLRS_OK || e != hipSuccess) {
+    if (st) (void)hipStreamSynchronize(st->cs);
+    (void)hipStreamSynchronize(b->stream);
   }
   if (dv) (void)hipFree(dv);
   if (raw) (void)hipFree(raw);
@@ -181,7 +248,7 @@ static int quantize_on_device(llrs_backend *b, uint32_t want, uint32_t src_ty, c
 
 // load_gguf_matrix + check_matrix + maybe_quantize (src/loader.rs:406-456, 497-507).
 static int gguf_matrix(llrs_model *m, const GgufFile &g, const std::string &name, size_t rows,
-                       size_t cols, int quantization, llrs_tensor **out) {
+                       size_t cols, int quantization, llrs_tensor **out, LoadStaging *st) {
   const GgufTensorInfo *t = g.tensor(name);
   if (!t) return set_error(LLRS_E_INVALID, "missing GGUF tensor %s", name.c_str());
   const std::vector<uint64_t> &dims = t->dims;
@@ -194,7 +261,7 @@ static int gguf_matrix(llrs_model *m, const GgufFile &g, const std::string &name
                      (unsigned long long)(dims.size() == 2 ? dims[0] : 0), rows, cols);
   uint32_t ty = t->type;
   if (quantization != LLRS_QUANT_NONE && (ty == LLRS_F32 || ty == LLRS_F16 || ty == LLRS_BF16))
-    return quantize_on_device(m->b, recipe_type(quantization, name, cols), ty, g.data(*t), rows, cols, out);
+    return quantize_on_device(m->b, recipe_type(quantization, name, cols), ty, g.data(*t), rows, cols, out, st);
   return llrs_tensor_upload(m->b, g.data(*t), t->nbytes, ty, rows, cols, out);
 }
 
@@ -317,8 +384,16 @@ static int load_gguf_impl(llrs_backend *b, const char *path, int quantization, l
   if (!m) return set_error(LLRS_E_OOM, "out of host memory");
   m->b = b;
   m->cfg = c;
+  LoadStaging stg;
+  if (quantization != LLRS_QUANT_NONE) {
+    int rc = stg.init(b);
+    if (rc != LLRS_OK) {
+      delete m;
+      return rc;
+    }
+  }
   MatFn mat = [&](const std::string &name, size_t rows, size_t cols, llrs_tensor **t) {
-    return gguf_matrix(m, g, name, rows, cols, quantization, t);
+    return gguf_matrix(m, g, name, rows, cols, quantization, t, quantization != LLRS_QUANT_NONE ? &stg : nullptr);
   };
   VecFn vec = [&](const std::string &name, size_t len, bool zeros, float *dst) {
     return gguf_vector(m, g, name, len, zeros, dst);
@@ -367,7 +442,7 @@ static uint32_t st_type(const SafetensorInfo &t) {
 
 // load_st_matrix + check_matrix + maybe_quantize (src/loader.rs:406-467).
 static int st_matrix(llrs_model *m, SafetensorStore &st, const std::string &name, size_t rows,
-                     size_t cols, int quantization, llrs_tensor **out) {
+                     size_t cols, int quantization, llrs_tensor **out, LoadStaging *stg) {
   const SafetensorsFile *f = nullptr;
   const SafetensorInfo *t = nullptr;
   LLRS_TRY(st.tensor(name, &f, &t));
@@ -377,7 +452,7 @@ static int st_matrix(llrs_model *m, SafetensorStore &st, const std::string &name
                      (unsigned long long)(t->shape.size() == 2 ? t->shape[1] : 0), rows, cols);
   const uint32_t ty = st_type(*t);
   if (quantization != LLRS_QUANT_NONE)
-    return quantize_on_device(m->b, recipe_type(quantization, name, cols), ty, f->data(*t), rows, cols, out);
+    return quantize_on_device(m->b, recipe_type(quantization, name, cols), ty, f->data(*t), rows, cols, out, stg);
   return llrs_tensor_upload(m->b, f->data(*t), t->nbytes, ty, rows, cols, out);
 }
 
@@ -426,8 +501,16 @@ static int load_safetensors_impl(llrs_backend *b, const std::string &dir, int qu
   if (!m) return set_error(LLRS_E_OOM, "out of host memory");
   m->b = b;
   m->cfg = c;
+  LoadStaging stg;
+  if (quantization != LLRS_QUANT_NONE) {
+    int rc = stg.init(b);
+    if (rc != LLRS_OK) {
+      delete m;
+      return rc;
+    }
+  }
   MatFn mat = [&](const std::string &name, size_t rows, size_t cols, llrs_tensor **t) {
-    return st_matrix(m, st, hf_name(name), rows, cols, quantization, t);
+    return st_matrix(m, st, hf_name(name), rows, cols, quantization, t, quantization != LLRS_QUANT_NONE ? &stg : nullptr);
   };
   VecFn vec = [&](const std::string &name, size_t len, bool zeros, float *dst) {
     return st_vector(m, st, hf_name(name), len, zeros, dst);
