@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Batch-1 greedy decode of the Qwen2.5-7B-shaped Q4_K_M model on one MI355X.
 
-Workload: a synthetic Qwen2.5-7B-shaped model (hidden
+Workload (benchmark config 5): a synthetic Qwen2.5-7B-shaped model (hidden
 3584, 28 layers, 28 Q / 4 KV heads, head_dim 128, FFN 18944, vocab 152064,
 untied LM head, rope_theta 1e6), random-init N(0, 0.02) weights quantized
 with the reference's q4km recipe (Q4_K q/k/o/gate/up, Q8_0 v/embeddings/LM
@@ -212,7 +212,7 @@ def profiled_traffic(kernel: str):
     return None
 
 
-# The end-to-end configs of BASELINE.json: synthetic models (random-init
+# The end-to-end benchmark configs: synthetic models (random-init
 # N(0, 0.02) weights, quantized in HBM), prompt length and decode steps.
 # cfg5 is the headline (the default); cfg3 and cfg4 are run on request.
 WORKLOADS = {
@@ -376,7 +376,7 @@ def main() -> int:
         args.prompt = wl["prompt"]
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(this build has no multi-GPU path; see DESIGN.md on sharding)", file=sys.stderr)
+              "(this build has no multi-GPU path)", file=sys.stderr)
         return 2
     if args.prompt + args.warmup + args.steps > args.context:
         print("prompt + warmup + steps exceed the context", file=sys.stderr)

@@ -66,7 +66,7 @@ def test_gemv_small_shapes(llrs, backend, oracle, ty):
 
 
 def test_config1_q4k_8960x1536(llrs, backend, oracle):
-    """Qwen2.5-1.5B ffn_gate shape, seed 1."""
+    """Benchmark config 1: the Qwen2.5-1.5B ffn_gate shape, seed 1."""
     run_case(llrs, backend, oracle, 12, 8960, 1536, seed=1)
 
 
@@ -74,7 +74,7 @@ def test_config1_q4k_8960x1536(llrs, backend, oracle):
                          ids=[NAMES[t] for t in [2, 3, 6, 7, 8, 13, 14, 1, 30]])
 @pytest.mark.parametrize("shape", [(18944, 3584), (3584, 18944)], ids=["up", "down"])
 def test_config2_type_sweep(llrs, backend, oracle, ty, shape):
-    """every KernelBackend dot path at the 7B FFN shapes."""
+    """Benchmark config 2: every KernelBackend dot path at the 7B FFN shapes."""
     run_case(llrs, backend, oracle, ty, shape[0], shape[1], seed=2)
 
 

@@ -231,7 +231,7 @@ def test_model_error_paths(llrs, backend, tmp_path):
 
 
 def test_config3_qwen05b_shape_greedy_parity(llrs, backend, oracle, tmp_path):
-    """Qwen2.5-0.5B shape, q4km, 128-token random prompt, 32 greedy steps."""
+    """Benchmark config 3: Qwen2.5-0.5B shape, q4km, 128-token random prompt, 32 greedy steps."""
     cfg = llrs.SynthConfig(hidden_size=896, intermediate_size=4864, num_attention_heads=14,
                            num_key_value_heads=2, num_hidden_layers=24, vocab_size=151936,
                            max_position_embeddings=32768, rope_theta=1e6, rms_norm_eps=1e-6,
