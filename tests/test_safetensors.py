@@ -406,3 +406,22 @@ def test_gguf_half_matrices_quantize_like_safetensors(llrs, backend, tmp_path, d
         _, x = llrs.gguf_read_tensor(tmp_path / "a.gguf", g)
         _, y = llrs.gguf_read_tensor(tmp_path / "b.gguf", g)
         assert (x.quant_type, x.data) == (y.quant_type, y.data), g
+
+
+def test_header_json_escapes_and_nesting(llrs, tmp_path):
+    """The header's JSON strings decode escapes (\\u, surrogate pairs) to the
+    UTF-8 names they stand for, as the package reads them; nesting beyond
+    the parser's limit is rejected by both."""
+    f4 = struct.pack("<4f", 1, 2, 3, 4)
+    hdr = b'{"t\\u00e9\\ud83d\\ude00\\n": {"dtype": "F32", "shape": [4], "data_offsets": [0, 16]}}'
+    path = tmp_path / "model.safetensors"
+    path.write_bytes(raw_file(hdr, f4))
+    import safetensors.numpy
+    assert list(safetensors.numpy.load_file(str(path))) == ["té\U0001F600\n"]
+    assert llrs.safetensors_read_tensor(tmp_path, "té\U0001F600\n")[2] == f4
+    deep = b'{"__metadata__": {"a": "b"}, "x": ' + b"[" * 200 + b"]" * 200 + b"}"
+    path.write_bytes(raw_file(deep))
+    assert _pkg_rejects(path)
+    with pytest.raises(llrs.LlrsError) as e:
+        llrs.safetensors_read_tensor(tmp_path, "x")
+    assert e.value.code == E_FORMAT
