@@ -190,3 +190,50 @@ def test_device_sampler_validates_options(llrs, backend, tmp_path):
         kv.sample(llrs.SamplingOptions(), 0.5, np.zeros(65537, np.uint32))
     tok = kv.sample(llrs.SamplingOptions(temperature=0.0), 0.5)
     assert tok == int(np.argmax(kv.logits()))  # distinct logits: the greedy pick
+
+
+@pytest.mark.gpu
+def test_sampling_loop_matches_oracle(llrs, backend, oracle, tmp_path):
+    """The interactive loop (src/engine.rs:115-186, 243-325): sample with the
+    repeat window, remember the token, feed it back.  Each step the device
+    logits stay within 2e-2 of the oracle model's, and the device draw equals
+    the oracle sampler's on the same logits and uniform number; that token is
+    fed to both models, so a draw within rounding of a boundary (skipped)
+    cannot derail the rest."""
+    cfg = llrs.SynthConfig(hidden_size=256, intermediate_size=512, num_attention_heads=4,
+                           num_key_value_heads=2, num_hidden_layers=2, vocab_size=800,
+                           max_position_embeddings=128, recipe=llrs.LoadQuantization.Q4KM, seed=53,
+                           tie_word_embeddings=False)
+    cfg.write_gguf(tmp_path / "loop.gguf")
+    model = llrs.ModelLoader.load(tmp_path / "loop.gguf", backend)
+    kv = llrs.KVCache(model, 64)
+    om = oracle.load(tmp_path / "loop.gguf")
+    om.new_state(64)
+    prompt = np.array([11, 403, 77, 5, 260], np.uint32)
+    model.prefill(prompt, 0, kv)
+    om.prefill(prompt, 0)
+    opts = llrs.SamplingOptions(temperature=0.9, top_p=0.95, top_k=50, repetition_penalty=1.15)
+    sampler = llrs.Sampler(opts, repeat_last_n=16)
+    for t in prompt:
+        sampler.remember(int(t))
+    rng = np.random.default_rng(53)
+    compared = 0
+    for step in range(24):
+        u = float(rng.random())
+        recent = list(sampler.recent_tokens)
+        lg = kv.logits()
+        assert float(np.abs(lg - om.logits()).max()) <= 2e-2
+        want = oracle.sample(lg, opts.temperature, opts.top_k, opts.top_p,
+                             opts.repetition_penalty, recent, u)
+        _, margin = f64_sample(lg, opts.temperature, opts.top_k, opts.top_p,
+                               opts.repetition_penalty, recent, u)
+        got = sampler.sample(kv, u)
+        if margin >= 1e-4:
+            assert got == want, (step, got, want)
+            compared += 1
+        sampler.remember(want)
+        pos = len(prompt) + step
+        model.forward_token(want, pos, kv, llrs.LogitsMode.COMPUTE)
+        om.forward_token(want, pos)
+    print(f"[sample] loop: {compared} of 24 draws compared", flush=True)
+    assert compared >= 20
