@@ -199,8 +199,20 @@ int llrs_model_export_gguf(const llrs_model *m, const char *path);
  * exceeds max_position_embeddings (src/cache.rs:14-19). */
 int llrs_kv_create(llrs_model *m, size_t max_seq_len, llrs_kv **out);
 void llrs_kv_free(llrs_kv *kv);
-/* KVCache::reset (src/cache.rs:55-57): a no-op, positions are overwritten before read. */
+/* KVCache::reset (src/cache.rs:55-57): the rows are kept (positions are
+ * overwritten before they are read); the device's wait flags (below) are
+ * cleared. */
 int llrs_kv_reset(llrs_kv *kv);
+/* Every device-side wait of a decode step is bounded (~20 ms): a barrier of
+ * the persistent kernel, or an attention merge waiting for partials.  On
+ * expiry the kernel sets a flag and finishes; the next call that checks
+ * (forward_token, prefill, decode_greedy: every 64 steps and at the end)
+ * returns LLRS_E_HIP and clears the flag, so later calls run normally (the
+ * steps since the last check are untrustworthy: prefill the cache again).
+ * This hook sets a flag from the host (which: 0 = barrier, 1 = attention
+ * merge) so that tests can exercise the reporting path; no counterpart in
+ * the reference. */
+int llrs_kv_debug_set_wait_flag(llrs_kv *kv, int which);
 /* Which implementation runs this state's decode steps: 1 = one persistent
  * launch for all layers (chosen at llrs_kv_create when the model's weight
  * types and head_dim have an instantiation and LLRS_NO_PERSISTENT is unset),
@@ -242,6 +254,13 @@ int llrs_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent, 
  * KVCache::{k,v}_cache[layer][0 .. n) (src/cache.rs:5-7). */
 int llrs_read_logits(llrs_kv *kv, float *out, size_t n);
 int llrs_read_kv(llrs_kv *kv, size_t layer, int which /*0 = K, 1 = V*/, float *out, size_t n);
+/* Readback for tests: the token ids the device holds for positions
+ * [start, start + n).  Position p holds the token fed at p; after a step (or
+ * a prefill) that computed logits at p, position p + 1 holds their greedy
+ * token, written by the LM-head launch (the argmax_current_logits of
+ * src/engine.rs:233-241 that the next step consumes).  start + n may reach
+ * max_seq_len + 1 (the slot after the context). */
+int llrs_read_tokens(llrs_kv *kv, size_t start, size_t n, uint32_t *out);
 
 /* Measurement hook (no reference counterpart; llama-bench times whole steps,
  * src/bin/llama-bench.rs:117-126): times the decode step's launch(es) for one

@@ -125,6 +125,7 @@ SIGNATURES = [
     ("llrs_kv_free", None, [P]),
     ("llrs_kv_reset", C.c_int, [P]),
     ("llrs_kv_decode_path", C.c_int, [P]),
+    ("llrs_kv_debug_set_wait_flag", C.c_int, [P, C.c_int]),
     ("llrs_forward_token", C.c_int, [P, P, C.c_uint32, SZ, C.c_int]),
     ("llrs_prefill", C.c_int, [P, P, U32P, SZ, SZ]),
     ("llrs_decode_greedy", C.c_int, [P, P, SZ, SZ, U32P]),
@@ -132,6 +133,7 @@ SIGNATURES = [
     ("llrs_sample", C.c_int, [P, P, P, SZ, C.c_float, U32P]),
     ("llrs_read_logits", C.c_int, [P, F32P, SZ]),
     ("llrs_read_kv", C.c_int, [P, SZ, C.c_int, F32P, SZ]),
+    ("llrs_read_tokens", C.c_int, [P, SZ, SZ, U32P]),
     ("llrs_profile_projection", C.c_int, [P, P, C.c_int, C.c_int, C.POINTER(C.c_double),
                                           C.POINTER(SZ)]),
 ]

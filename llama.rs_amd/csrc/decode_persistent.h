@@ -51,6 +51,12 @@ bool decode_persistent_supports(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, uint
 int launch_decode_persistent(const PersistentArgs &p, uint32_t t_qkv, uint32_t t_v, uint32_t t_o,
                              uint32_t t_gu, uint32_t t_down, int head_dim, int grid, size_t lds,
                              hipStream_t s, bool long_items);
+// Workgroups of the instantiation that fit one CU with `lds` bytes of dynamic
+// LDS (hipOccupancyMaxActiveBlocksPerMultiprocessor).  The kernel's barriers
+// need every workgroup resident at once: one per CU at least.
+int decode_persistent_blocks_per_cu(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, uint32_t t_gu,
+                                    uint32_t t_down, int head_dim, size_t lds, bool long_items,
+                                    int *blocks);
 // Whether a step at position pos should launch the long_items instantiation.
 inline bool persistent_long_items(size_t pos) { return attention_span((int)pos) > 1; }
 

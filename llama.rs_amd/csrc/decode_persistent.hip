@@ -29,16 +29,36 @@
 
 namespace llrs {
 
+#ifdef LLRS_STAMPS
+// Timing build only (build.py --stamps): per barrier interval k (5 per layer)
+// and workgroup, wall-clock stamps (the 100 MHz clock) [0] released from
+// barrier k, [1] activation staged, [2] weight streaming done, [3] stores
+// done and arriving at barrier k + 1.  Interval 0 starts at kernel entry.
+constexpr int kStampIntervals = 5 * 64, kStampWgs = 512;
+__device__ unsigned long long g_stamps[kStampIntervals * kStampWgs * 4];
+#define STAMP(k, i)                                                                        \
+  do {                                                                                     \
+    if (threadIdx.x == 0 && (k) < kStampIntervals && wg < kStampWgs)                      \
+      g_stamps[((size_t)(k) * kStampWgs + wg) * 4 + (i)] = wall_clock64();                 \
+  } while (0)
+#define STAMP_PHASE(ph, k) ph.stamp = ((k) < kStampIntervals && wg < kStampWgs) ? g_stamps + ((size_t)(k) * kStampWgs + wg) * 4 : nullptr
+#else
+#define STAMP(k, i) do {} while (0)
+#define STAMP_PHASE(ph, k) do {} while (0)
+#endif
+
 namespace {
 
 __device__ __forceinline__ unsigned ld_u32_dev(unsigned *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The workgroup's stores are complete, then its arrival at the next barrier.
-__device__ void bar_arrive(unsigned *bar, int wg) {
+// The workgroup's stores are complete, then its arrival at the next barrier
+// (interval k ends).
+__device__ void bar_arrive(unsigned *bar, int wg, unsigned k) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  STAMP(k, 3);
   if (threadIdx.x == 0)
     __hip_atomic_fetch_add(bar + (wg % kBarCounters) * kBarStride, 1u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -99,8 +119,10 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
       GemvPhase<TQ, TV, false, true> ph{};
       ph.prefetch(L.qkv, wg, nwg);
       if (k) bar_wait(p.bar, p.err, nwg, k);
+      STAMP(k, 0);
+      STAMP_PHASE(ph, k);
       ph.finish(L.qkv, smem, red);
-      bar_arrive(p.bar, wg);
+      bar_arrive(p.bar, wg, k);
       k++;
     }
     {  // RoPE, KV append, attention: one (head, chunk) item per wave
@@ -113,6 +135,7 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
       a.v_cache += l * p.cache_stride;
       a.tag = epoch * (unsigned)p.nlayers + (unsigned)l;
       bar_wait(p.bar, p.err, nwg, k);
+      STAMP(k, 0);
       const bool multi = span > 1;
       for (int it = wave * nwg + wg; it < n_items; it += nwg * nwv) {
         const int r = it >> 3, pair = (r / G) * 8 + (it & 7);
@@ -126,31 +149,37 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
         }
         attention_item<HD, true, false>(a, hh, item, pos, aqs[wave], akn[wave]);
       }
-      bar_arrive(p.bar, wg);
+      bar_arrive(p.bar, wg, k);
       k++;
     }
     {  // o_proj (+ residual)
       GemvPhase<TO, TO, false, true> ph{};
       ph.prefetch(L.o, wg, nwg);
       bar_wait(p.bar, p.err, nwg, k);
+      STAMP(k, 0);
+      STAMP_PHASE(ph, k);
       ph.finish(L.o, smem, red);
-      bar_arrive(p.bar, wg);
+      bar_arrive(p.bar, wg, k);
       k++;
     }
     {  // RMSNorm + gate/up + SiLU*up
       GemvPhase<TGU, TGU, true, true> ph{};
       ph.prefetch(L.gate_up, wg, nwg);
       bar_wait(p.bar, p.err, nwg, k);
+      STAMP(k, 0);
+      STAMP_PHASE(ph, k);
       ph.finish(L.gate_up, smem, red);
-      bar_arrive(p.bar, wg);
+      bar_arrive(p.bar, wg, k);
       k++;
     }
     {  // ffn_down (+ residual)
       GemvPhase<TD, TD, false, true> ph{};
       ph.prefetch(L.down, wg, nwg);
       bar_wait(p.bar, p.err, nwg, k);
+      STAMP(k, 0);
+      STAMP_PHASE(ph, k);
       ph.finish(L.down, smem, red);
-      bar_arrive(p.bar, wg);
+      bar_arrive(p.bar, wg, k);
       k++;
     }
   }
@@ -167,6 +196,21 @@ int launch_types(const PersistentArgs &p, int head_dim, int grid, size_t lds, hi
   }
 #undef PK
   LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
+template <uint32_t TQ, uint32_t TV, uint32_t TO, uint32_t TGU, uint32_t TD>
+int occupancy_types(int head_dim, size_t lds, bool lng, int *blocks) {
+#define OCC(HD, L)                                                                                      \
+  LLRS_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(                                              \
+      blocks, reinterpret_cast<const void *>(decode_persistent_kernel<TQ, TV, TO, TGU, TD, HD, L>), \
+      kPersistentThreads, lds))
+  switch (head_dim) {
+    case 64: if (lng) OCC(64, true); else OCC(64, false); break;
+    case 128: if (lng) OCC(128, true); else OCC(128, false); break;
+    default: return set_error(LLRS_E_UNSUPPORTED, "persistent decode: head_dim %d", head_dim);
+  }
+#undef OCC
   return LLRS_OK;
 }
 
@@ -187,6 +231,19 @@ bool decode_persistent_supports(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, uint
   return q4km || q4km_q5 || q4k;
 }
 
+int decode_persistent_blocks_per_cu(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, uint32_t t_gu,
+                                    uint32_t t_down, int head_dim, size_t lds, bool long_items,
+                                    int *blocks) {
+  *blocks = 0;
+  if (t_qkv == LLRS_Q4_K && t_v == LLRS_Q8_0 && t_down == LLRS_Q6_K)
+    return occupancy_types<LLRS_Q4_K, LLRS_Q8_0, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q6_K>(head_dim, lds, long_items, blocks);
+  if (t_qkv == LLRS_Q5_0)
+    return occupancy_types<LLRS_Q5_0, LLRS_Q8_0, LLRS_Q5_0, LLRS_Q5_0, LLRS_Q6_K>(head_dim, lds, long_items, blocks);
+  if (t_qkv == LLRS_Q4_K && t_v == LLRS_Q4_K)
+    return occupancy_types<LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K>(head_dim, lds, long_items, blocks);
+  return set_error(LLRS_E_UNSUPPORTED, "persistent decode: no instantiation for these weight types");
+}
+
 int launch_decode_persistent(const PersistentArgs &p, uint32_t t_qkv, uint32_t t_v, uint32_t t_o,
                              uint32_t t_gu, uint32_t t_down, int head_dim, int grid, size_t lds,
                              hipStream_t s, bool long_items) {
@@ -203,3 +260,12 @@ int launch_decode_persistent(const PersistentArgs &p, uint32_t t_qkv, uint32_t t
 }
 
 }  // namespace llrs
+
+#ifdef LLRS_STAMPS
+// Timing build only: copies the stamps of the last persistent launch
+// ([interval][512 workgroup slots][4], 64-bit ticks of the 100 MHz clock).
+extern "C" int llrs_debug_stamps(void *dst, size_t bytes) {
+  if (bytes > sizeof(llrs::g_stamps)) bytes = sizeof(llrs::g_stamps);
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(llrs::g_stamps), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif

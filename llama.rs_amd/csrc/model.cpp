@@ -101,6 +101,8 @@ struct llrs_kv {
   float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_g = nullptr,
         *pf_u = nullptr;
   llrs::f16 *pf_h = nullptr, *pf_hl = nullptr;  // GEMM inputs as f16 hi + lo pairs
+  float *pf_part = nullptr;                     // split-K partial tiles of the prefill GEMMs
+  size_t pf_part_cap = 0;                       // floats
 };
 
 namespace llrs {
@@ -898,6 +900,14 @@ static int setup_persistent(llrs_model *m, llrs_kv *kv) {
   // More than half a CU's LDS per workgroup: exactly one workgroup per CU.
   lds = std::max(lds, kPersistentMinLds);
   if (lds + persistent_static_lds((int)c.head_dim) > kCuLds) return LLRS_OK;
+  // The barriers need all `grid` workgroups resident at once: both
+  // instantiations must fit one workgroup per CU with this LDS, else the
+  // step runs as per-phase launches.
+  for (bool lng : {false, true}) {
+    int blocks = 0;
+    LLRS_TRY(decode_persistent_blocks_per_cu(t[0], t[1], t[2], t[3], t[4], (int)c.head_dim, lds, lng, &blocks));
+    if (blocks < 1) return LLRS_OK;
+  }
   auto A = [&](void **p, size_t bytes) { return dev_alloc(kv->allocs, p, bytes); };
   LLRS_TRY(A((void **)&kv->p_layers, nl * sizeof(PersistentLayer)));
   LLRS_TRY(A((void **)&kv->p_bar, kPersistentBarWords * 4));
@@ -914,17 +924,27 @@ static int setup_persistent(llrs_model *m, llrs_kv *kv) {
   return LLRS_OK;
 }
 
-// Reports a device-side wait that gave up: a persistent-decode barrier or an
-// attention merge (the stream is idle).
-static int check_persistent(llrs_kv *kv) {
-  unsigned err = 0;
-  if (kv->p_err) {
-    LLRS_HIP(hipMemcpy(&err, kv->p_err, 4, hipMemcpyDeviceToHost));
-    if (err) return set_error(LLRS_E_HIP, "persistent decode: a device-wide barrier timed out");
-  }
-  LLRS_HIP(hipMemcpy(&err, kv->attn_err, 4, hipMemcpyDeviceToHost));
-  if (err) return set_error(LLRS_E_HIP, "decode attention: a merge timed out waiting for partials");
+// Clears the device-side wait flags (outside any graph capture).
+static int clear_wait_flags(llrs_kv *kv) {
+  hipStream_t s = kv->m->b->stream;
+  if (kv->p_err) LLRS_HIP(hipMemsetAsync(kv->p_err, 0, 4, s));
+  LLRS_HIP(hipMemsetAsync(kv->attn_err, 0, 4, s));
+  LLRS_HIP(hipStreamSynchronize(s));
   return LLRS_OK;
+}
+
+// Reports a device-side wait that gave up: a persistent-decode barrier or an
+// attention merge (the stream is idle).  The flags are cleared once
+// reported: the steps since the last check are untrustworthy (their K/V rows
+// too, so the cache should be prefilled again), but later calls run normally.
+static int check_persistent(llrs_kv *kv) {
+  unsigned err = 0, aerr = 0;
+  if (kv->p_err) LLRS_HIP(hipMemcpy(&err, kv->p_err, 4, hipMemcpyDeviceToHost));
+  LLRS_HIP(hipMemcpy(&aerr, kv->attn_err, 4, hipMemcpyDeviceToHost));
+  if (!err && !aerr) return LLRS_OK;
+  LLRS_TRY(clear_wait_flags(kv));
+  if (err) return set_error(LLRS_E_HIP, "persistent decode: a device-wide barrier timed out");
+  return set_error(LLRS_E_HIP, "decode attention: a merge timed out waiting for partials");
 }
 
 static void free_kv(llrs_kv *kv) {
@@ -1042,13 +1062,17 @@ static int prefill_buffers(llrs_kv *kv) {
   LLRS_TRY(A((void **)&kv->pf_u, T * F * 4));
   LLRS_TRY(A((void **)&kv->pf_h, T * (H > F ? H : F) * 2));
   LLRS_TRY(A((void **)&kv->pf_hl, T * (H > F ? H : F) * 2));
+  kv->pf_part_cap = prefill_split_scratch_floats();
+  LLRS_TRY(A((void **)&kv->pf_part, kv->pf_part_cap * 4));
   kv->pf_cap = T;
   return LLRS_OK;
 }
 
-static int prefill_gemm(const llrs_tensor *w, const f16 *a, const f16 *a_lo, int lda, float *c,
-                        int ldc, const float *bias, int T, bool accumulate, hipStream_t s) {
+static int prefill_gemm(llrs_kv *kv, const llrs_tensor *w, const f16 *a, const f16 *a_lo, int lda,
+                        float *c, int ldc, const float *bias, int T, bool accumulate, hipStream_t s) {
   PrefillGemmArgs g{};
+  g.part = kv->pf_part;
+  g.part_cap = kv->pf_part_cap;
   g.a = a;
   g.a_lo = a_lo;
   g.lda = lda;
@@ -1088,17 +1112,17 @@ static int prefill_batched(llrs_model *m, llrs_kv *kv, size_t start, size_t n) {
       const DevLayer &L = m->layers[l];
       float *kc = kv->k_cache + l * layer_stride, *vc = kv->v_cache + l * layer_stride;
       LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.attn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s));
-      LLRS_TRY(prefill_gemm(L.q, kv->pf_h, kv->pf_hl, H, kv->pf_q, H, L.bq, T, false, s));
-      LLRS_TRY(prefill_gemm(L.k, kv->pf_h, kv->pf_hl, H, kv->pf_k, KV, L.bk, T, false, s));
-      LLRS_TRY(prefill_gemm(L.v, kv->pf_h, kv->pf_hl, H, kv->pf_v, KV, L.bv, T, false, s));
+      LLRS_TRY(prefill_gemm(kv, L.q, kv->pf_h, kv->pf_hl, H, kv->pf_q, H, L.bq, T, false, s));
+      LLRS_TRY(prefill_gemm(kv, L.k, kv->pf_h, kv->pf_hl, H, kv->pf_k, KV, L.bk, T, false, s));
+      LLRS_TRY(prefill_gemm(kv, L.v, kv->pf_h, kv->pf_hl, H, kv->pf_v, KV, L.bv, T, false, s));
       LLRS_TRY(launch_rope_append(kv->pf_q, kv->pf_k, kv->pf_v, kv->rope, T, st, nh, nkv, hd, kc, vc, s));
       LLRS_TRY(launch_attention_rows(kv->pf_q, kc, vc, T, st, nh, nkv, hd, scale, kv->pf_h, kv->pf_hl, s));
-      LLRS_TRY(prefill_gemm(L.o, kv->pf_h, kv->pf_hl, H, kv->pf_x, H, nullptr, T, true, s));
+      LLRS_TRY(prefill_gemm(kv, L.o, kv->pf_h, kv->pf_hl, H, kv->pf_x, H, nullptr, T, true, s));
       LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.ffn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s));
-      LLRS_TRY(prefill_gemm(L.gate, kv->pf_h, kv->pf_hl, H, kv->pf_g, F, nullptr, T, false, s));
-      LLRS_TRY(prefill_gemm(L.up, kv->pf_h, kv->pf_hl, H, kv->pf_u, F, nullptr, T, false, s));
+      LLRS_TRY(prefill_gemm(kv, L.gate, kv->pf_h, kv->pf_hl, H, kv->pf_g, F, nullptr, T, false, s));
+      LLRS_TRY(prefill_gemm(kv, L.up, kv->pf_h, kv->pf_hl, H, kv->pf_u, F, nullptr, T, false, s));
       LLRS_TRY(launch_swiglu_f16(kv->pf_g, kv->pf_u, kv->pf_h, kv->pf_hl, (size_t)T * F, s));
-      LLRS_TRY(prefill_gemm(L.down, kv->pf_h, kv->pf_hl, F, kv->pf_x, H, nullptr, T, true, s));
+      LLRS_TRY(prefill_gemm(kv, L.down, kv->pf_h, kv->pf_hl, F, kv->pf_x, H, nullptr, T, true, s));
     }
     last_rows = (size_t)T;
   }
@@ -1106,6 +1130,43 @@ static int prefill_batched(llrs_model *m, llrs_kv *kv, size_t start, size_t n) {
                           hipMemcpyDeviceToDevice, s));
   LLRS_TRY(launch_set_pos(kv->pos, (int)(start + n - 1), s));
   return launch_projection(m, kv, 0, P_LM_HEAD, s);
+}
+
+// The repeat window's length limit of llrs_sample.
+constexpr size_t kMaxRecent = 65536;
+
+// Arguments of llrs_sample: validate_sampling (src/engine.rs:327-338) and the
+// draw.
+static int validate_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent,
+                           size_t n_recent, float uniform, uint32_t *out_token) {
+  if (!kv || !opts || !out_token || (n_recent && !recent))
+    return set_error(LLRS_E_INVALID, "kv/opts/recent/out is NULL");
+  if (!std::isfinite(opts->temperature) || opts->temperature < 0.0f)
+    return set_error(LLRS_E_INVALID, "temperature must be finite and non-negative");
+  if (!std::isfinite(opts->top_p) || !(0.0f < opts->top_p && opts->top_p <= 1.0f))
+    return set_error(LLRS_E_INVALID, "top_p must be in (0, 1]");
+  if (!std::isfinite(opts->repetition_penalty) || opts->repetition_penalty <= 0.0f)
+    return set_error(LLRS_E_INVALID, "repetition_penalty must be finite and positive");
+  if (!std::isfinite(uniform) || uniform < 0.0f || uniform >= 1.0f)
+    return set_error(LLRS_E_INVALID, "the uniform draw must be in [0, 1)");
+  if (n_recent > kMaxRecent) return set_error(LLRS_E_INVALID, "repeat window %zu > %zu", n_recent, kMaxRecent);
+  return LLRS_OK;
+}
+
+// sample_current_logits over the cache's logits with scratch w (the device is current).
+static int sample_with(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent, size_t n_recent,
+                       float uniform, SampleScratch &w, uint32_t *out_token) {
+  llrs_model *m = kv->m;
+  hipStream_t s = m->b->stream;
+  const int V = (int)m->cfg.vocab_size;
+  if (n_recent) LLRS_HIP(hipMemcpyAsync(w.recent, recent, n_recent * 4, hipMemcpyHostToDevice, s));
+  const SampleParams p{opts->temperature, (int)std::min<uint32_t>(opts->top_k, (uint32_t)V), opts->top_p,
+                       opts->repetition_penalty};
+  LLRS_TRY(launch_sample(kv->logits, V, p, (int)n_recent, uniform, w, s));
+  LLRS_HIP(hipMemcpyAsync(kv->pinned, w.token, 4, hipMemcpyDeviceToHost, s));
+  LLRS_HIP(hipStreamSynchronize(s));
+  *out_token = kv->pinned[0];
+  return LLRS_OK;
 }
 
 }  // namespace llrs
@@ -1285,7 +1346,22 @@ void llrs_kv_free(llrs_kv *kv) { free_kv(kv); }
 
 int llrs_kv_reset(llrs_kv *kv) {
   clear_error();
-  return kv ? LLRS_OK : set_error(LLRS_E_INVALID, "kv is NULL");
+  if (!kv) return set_error(LLRS_E_INVALID, "kv is NULL");
+  // KVCache::reset (src/cache.rs:55-57) keeps the rows (positions are written
+  // before they are read); only the device's wait flags start over.
+  LLRS_HIP(hipSetDevice(kv->m->b->device));
+  return clear_wait_flags(kv);
+}
+
+int llrs_kv_debug_set_wait_flag(llrs_kv *kv, int which) {
+  clear_error();
+  if (!kv) return set_error(LLRS_E_INVALID, "kv is NULL");
+  if (which != 0 && which != 1) return set_error(LLRS_E_INVALID, "unknown wait flag %d", which);
+  if (which == 0 && !kv->p_err) return set_error(LLRS_E_INVALID, "the cache has no persistent decode");
+  LLRS_HIP(hipSetDevice(kv->m->b->device));
+  const unsigned one = 1;
+  LLRS_HIP(hipMemcpy(which == 0 ? kv->p_err : kv->attn_err, &one, 4, hipMemcpyHostToDevice));
+  return LLRS_OK;
 }
 
 int llrs_kv_decode_path(const llrs_kv *kv) { return kv && kv->p_layers ? 1 : 0; }
@@ -1345,7 +1421,16 @@ int llrs_decode_greedy(llrs_model *m, llrs_kv *kv, size_t start_pos, size_t n_st
   // token = argmax(current logits) for position start_pos; nothing advances.
   LLRS_TRY(launch_argmax(kv->logits, (int)m->cfg.vocab_size, kv->pos, (int)kv->max_seq_len,
                          kv->tok_by_pos, kv->next_token, 0, s));
-  for (size_t i = 0; i < n_steps; i++) LLRS_TRY(run_step(m, kv, LLRS_LOGITS_COMPUTE, start_pos + i));
+  // The device's wait flags are checked every kCheckEvery steps, so a
+  // failed step stops the loop within that many steps.
+  constexpr size_t kCheckEvery = 64;
+  for (size_t i = 0; i < n_steps; i++) {
+    LLRS_TRY(run_step(m, kv, LLRS_LOGITS_COMPUTE, start_pos + i));
+    if ((i + 1) % kCheckEvery == 0 && i + 1 < n_steps) {
+      LLRS_HIP(hipStreamSynchronize(s));
+      LLRS_TRY(check_persistent(kv));
+    }
+  }
   LLRS_HIP(hipMemcpyAsync(kv->pinned, kv->tok_by_pos + start_pos, n_steps * 4,
                           hipMemcpyDeviceToHost, s));
   LLRS_HIP(hipStreamSynchronize(s));
@@ -1377,22 +1462,9 @@ int llrs_argmax(llrs_kv *kv, uint32_t *out_token) {
 int llrs_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent, size_t n_recent,
                 float uniform, uint32_t *out_token) {
   clear_error();
-  if (!kv || !opts || !out_token || (n_recent && !recent))
-    return set_error(LLRS_E_INVALID, "kv/opts/recent/out is NULL");
-  // validate_sampling (src/engine.rs:327-338).
-  if (!std::isfinite(opts->temperature) || opts->temperature < 0.0f)
-    return set_error(LLRS_E_INVALID, "temperature must be finite and non-negative");
-  if (!std::isfinite(opts->top_p) || !(0.0f < opts->top_p && opts->top_p <= 1.0f))
-    return set_error(LLRS_E_INVALID, "top_p must be in (0, 1]");
-  if (!std::isfinite(opts->repetition_penalty) || opts->repetition_penalty <= 0.0f)
-    return set_error(LLRS_E_INVALID, "repetition_penalty must be finite and positive");
-  if (!std::isfinite(uniform) || uniform < 0.0f || uniform >= 1.0f)
-    return set_error(LLRS_E_INVALID, "the uniform draw must be in [0, 1)");
-  constexpr size_t kMaxRecent = 65536;
-  if (n_recent > kMaxRecent) return set_error(LLRS_E_INVALID, "repeat window %zu > %zu", n_recent, kMaxRecent);
+  LLRS_TRY(validate_sample(kv, opts, recent, n_recent, uniform, out_token));
   llrs_model *m = kv->m;
   LLRS_HIP(hipSetDevice(m->b->device));
-  hipStream_t s = m->b->stream;
   const int V = (int)m->cfg.vocab_size;
   SampleScratch &w = kv->sample;
   if (!w.n) {
@@ -1408,14 +1480,7 @@ int llrs_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent, 
     w.max_recent = (int)kMaxRecent;
     w.n = V;
   }
-  if (n_recent) LLRS_HIP(hipMemcpyAsync(w.recent, recent, n_recent * 4, hipMemcpyHostToDevice, s));
-  const SampleParams p{opts->temperature, (int)std::min<uint32_t>(opts->top_k, (uint32_t)V), opts->top_p,
-                       opts->repetition_penalty};
-  LLRS_TRY(launch_sample(kv->logits, V, p, (int)n_recent, uniform, w, s));
-  LLRS_HIP(hipMemcpyAsync(kv->pinned, w.token, 4, hipMemcpyDeviceToHost, s));
-  LLRS_HIP(hipStreamSynchronize(s));
-  *out_token = kv->pinned[0];
-  return LLRS_OK;
+  return sample_with(kv, opts, recent, n_recent, uniform, w, out_token);
 }
 
 int llrs_read_logits(llrs_kv *kv, float *out, size_t n) {
@@ -1439,6 +1504,18 @@ int llrs_read_kv(llrs_kv *kv, size_t layer, int which, float *out, size_t n) {
   const float *src = (which ? kv->v_cache : kv->k_cache) + layer * per;
   LLRS_HIP(hipSetDevice(kv->m->b->device));
   LLRS_HIP(hipMemcpyAsync(out, src, n * 4, hipMemcpyDeviceToHost, kv->m->b->stream));
+  LLRS_HIP(hipStreamSynchronize(kv->m->b->stream));
+  return LLRS_OK;
+}
+
+int llrs_read_tokens(llrs_kv *kv, size_t start, size_t n, uint32_t *out) {
+  clear_error();
+  if (!kv || (n && !out)) return set_error(LLRS_E_INVALID, "kv/out is NULL");
+  if (start > kv->max_seq_len + 1 || n > kv->max_seq_len + 1 - start)
+    return set_error(LLRS_E_INVALID, "token range [%zu, %zu) exceeds the context", start, start + n);
+  if (!n) return LLRS_OK;
+  LLRS_HIP(hipSetDevice(kv->m->b->device));
+  LLRS_HIP(hipMemcpyAsync(out, kv->tok_by_pos + start, n * 4, hipMemcpyDeviceToHost, kv->m->b->stream));
   LLRS_HIP(hipStreamSynchronize(kv->m->b->stream));
   return LLRS_OK;
 }

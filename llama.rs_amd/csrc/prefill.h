@@ -24,9 +24,17 @@ struct PrefillGemmArgs {
   const float *bias;  // [n] or null; ignored when accumulating
   int t;
   int accumulate;
-  int ksplit;  // set by launch_prefill_gemm: K ranges summed into C with atomic adds
+  int ksplit;  // set by launch_prefill_gemm: K ranges whose partial tiles go to `part`
+  // Split-K scratch: each K range writes its partial products here ([ksplit][t][n]),
+  // and a reduction adds them to C in split order, so results do not depend
+  // on the order the workgroups finish in.
+  float *part;
+  size_t part_cap;  // floats
 };
 
+// Floats of split-K scratch a prefill GEMM may need on this device: one
+// 128 x 128 tile per workgroup slot.
+size_t prefill_split_scratch_floats();
 int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s);
 
 // x[t][:] = embedding row of tok[t] (bit-exact dequant), t < T.

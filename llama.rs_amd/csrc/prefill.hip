@@ -205,8 +205,9 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
     }
     Deq<TY>::load(wrow, g.type, min(k0 + wc, ke - 32), raw);
   };
-  if (kb >= ke) return;
-  load_chunk(kb);
+  // A split whose range is empty (rounding of the per-split chunk count)
+  // loads nothing and writes zero partials.
+  if (kb < ke) load_chunk(kb);
   for (int k0 = kb; k0 < ke; k0 += KC) {
     const int kc = min(KC, ke - k0);  // 32 or 64
     __syncthreads();  // the previous chunk's MFMAs have read LDS
@@ -275,11 +276,12 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
       for (int e = 0; e < 4; e++) {
         const int t = t0 + wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + e;
         if (t >= g.t) continue;
-        float *c = g.c + (size_t)t * g.ldc + n;
-        if (g.ksplit > 1)
-          atomicAdd(c, acc[i][j][e]);
-        else
+        if (g.ksplit > 1) {
+          g.part[((size_t)blockIdx.z * g.t + t) * g.n + n] = acc[i][j][e];
+        } else {
+          float *c = g.c + (size_t)t * g.ldc + n;
           *c = g.accumulate ? *c + acc[i][j][e] : acc[i][j][e] + bias;
+        }
       }
     }
 }
@@ -499,12 +501,17 @@ __global__ void swiglu_f16_kernel(const float *__restrict__ g, const float *__re
 
 __global__ void set_pos_kernel(int *pos, int value) { *pos = value; }
 
-// C[t][j] = bias[j] (or 0): the starting value of a split-K product that does
-// not accumulate into C.
-__global__ void fill_rows_kernel(float *__restrict__ c, int ldc, const float *__restrict__ bias,
-                                 int n, int t) {
+// C[t][j] = (C[t][j] when accumulating, else bias[j] or 0) + the split-K
+// partials of splits 0, 1, ..., ksplit - 1, added in that order.
+__global__ void split_reduce_kernel(float *__restrict__ c, int ldc, const float *__restrict__ bias,
+                                    const float *__restrict__ part, int n, int t, int ksplit,
+                                    int accumulate) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
-  if (j < n && r < t) c[(size_t)r * ldc + j] = bias ? bias[j] : 0.f;
+  if (j >= n || r >= t) return;
+  float *cp = c + (size_t)r * ldc + j;
+  float v = accumulate ? *cp : (bias ? bias[j] : 0.f);
+  for (int z = 0; z < ksplit; z++) v += part[((size_t)z * t + r) * n + j];
+  *cp = v;
 }
 
 }  // namespace
@@ -525,17 +532,6 @@ int gemm_slots() {
   return slots;
 }
 
-// K split over `ksplit` workgroups that add into C atomically: C then starts
-// from its residual (accumulate) or from the bias, written first.
-void set_split(PrefillGemmArgs &a, int ksplit, hipStream_t s) {
-  a.ksplit = ksplit;
-  if (ksplit > 1 && !a.accumulate) {
-    hipLaunchKernelGGL(fill_rows_kernel, dim3((unsigned)((a.n + 255) / 256), (unsigned)a.t), dim3(256),
-                       0, s, a.c, a.ldc, a.bias, a.n, a.t);
-    a.accumulate = 1;  // the splits add onto the bias
-  }
-}
-
 void launch_tiles(const PrefillGemmArgs &a, int bm, hipStream_t s) {
   const dim3 grid((unsigned)((a.n + BN - 1) / BN), (unsigned)((a.t + bm - 1) / bm), (unsigned)a.ksplit);
   const size_t lds = (size_t)2 * (bm + BN) * LS * sizeof(f16);
@@ -554,7 +550,25 @@ void launch_tiles(const PrefillGemmArgs &a, int bm, hipStream_t s) {
 #undef GEMM
 }
 
+// The tiles of `a` with K split over `ksplit` workgroups, then the
+// fixed-order reduction of their partials into C.
+int launch_split(PrefillGemmArgs a, int bm, int ksplit, hipStream_t s) {
+  a.ksplit = ksplit;
+  if (ksplit > 1) {
+    if (!a.part || (size_t)ksplit * a.t * a.n > a.part_cap)
+      return set_error(LLRS_E_INVALID, "prefill GEMM: split-K scratch of %zu floats is too small (%d x %d x %d)",
+                       a.part_cap, ksplit, a.t, a.n);
+  }
+  launch_tiles(a, bm, s);
+  if (ksplit > 1)
+    hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((a.n + 255) / 256), (unsigned)a.t), dim3(256), 0,
+                       s, a.c, a.ldc, a.bias, a.part, a.n, a.t, ksplit, a.accumulate);
+  return LLRS_OK;
+}
+
 }  // namespace
+
+size_t prefill_split_scratch_floats() { return (size_t)gemm_slots() * BN * 128; }
 
 int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
   if (g.k % 32 || g.lda % 8 || g.n <= 0 || g.k <= 0 || g.t <= 0)
@@ -565,8 +579,8 @@ int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
   // than half the slots split K over up to 8 workgroups (at least 6 K chunks
   // each).  Otherwise whole rounds of tiles run as they are, and a last
   // round that would fill at most half the slots runs as its own launch with
-  // K split over the slots.  The atomic adds of split K make the order of the
-  // split sums, and so the last bits of C, vary between runs.
+  // K split over the slots.  Split partials are reduced in split order, so C
+  // is the same bit for bit on every run.
   const int slots = gemm_slots();
   const int ntiles = (g.n + BN - 1) / BN;
   const int bm = (g.t >= 256 && ntiles >= kTile128Rows) ? 128 : 64;
@@ -586,12 +600,9 @@ int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
     r.c = g.c + (size_t)full * BN;
     r.bias = g.bias ? g.bias + (size_t)full * BN : nullptr;
     r.n = g.n - full * BN;
-    set_split(r, std::max(1, std::min({8, slots / (rem * mt), chunks / 6})), s);
-    launch_tiles(r, bm, s);
+    LLRS_TRY(launch_split(r, bm, std::max(1, std::min({8, slots / (rem * mt), chunks / 6})), s));
   } else {
-    PrefillGemmArgs a = g;
-    set_split(a, ks, s);
-    launch_tiles(a, bm, s);
+    LLRS_TRY(launch_split(g, bm, ks, s));
   }
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;

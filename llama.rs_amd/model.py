@@ -222,6 +222,13 @@ class KVCache:
                                  r.size, float(uniform), C.byref(t)))
         return int(t.value)
 
+    def tokens(self, start: int, n: int) -> np.ndarray:
+        """The device's token ids for positions [start, start + n) (position
+        p + 1 holds the greedy token of the logits computed at p)."""
+        out = np.zeros(max(n, 1), dtype=np.uint32)
+        _check(lib().llrs_read_tokens(self.handle, start, n, out.ctypes.data_as(U32P)))
+        return out[:n]
+
     def layer(self, layer: int, which: str, n_pos: int) -> np.ndarray:
         cfg = self.model.config()
         out = np.empty(n_pos * cfg.kv_width, dtype=np.float32)

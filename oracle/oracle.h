@@ -123,6 +123,13 @@ const float *oq_state_residual(const oq_state *s);
 const float *oq_state_k_cache(const oq_state *s, size_t layer);
 const float *oq_state_v_cache(const oq_state *s, size_t layer);
 
+/* Write access, for tests and the bench's CPU baseline: seeds a state with
+ * rows computed elsewhere (the GPU's prefilled cache), so that the oracle can
+ * check steps at depths whose own prefill it could not afford.  what: 0 = K
+ * rows of `layer`, 1 = V rows of `layer` (n floats from position 0), 2 = the
+ * logits (n = vocab).  Returns 0, or -1 on a bad layer / length. */
+int oq_state_load(oq_state *s, int what, size_t layer, const float *src, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -296,7 +296,7 @@ struct oq_model {
 };
 
 struct oq_state {
-  size_t max_seq_len, n_layers;
+  size_t max_seq_len, n_layers, kv_width, vocab;
   float **k_cache, **v_cache;
   float *hidden, *residual, *q, *k, *v, *attention, *projection, *gate, *up, *down, *scores,
       *rope_cos, *rope_sin, *logits;
@@ -475,6 +475,8 @@ oq_state *oq_state_new(const oq_model *m, size_t max_seq_len) {
   oq_state *s = (oq_state *)calloc(1, sizeof *s);
   s->max_seq_len = max_seq_len;
   s->n_layers = c->num_hidden_layers;
+  s->kv_width = c->kv_width;
+  s->vocab = c->vocab_size;
   s->k_cache = (float **)calloc(c->num_hidden_layers, sizeof(float *));
   s->v_cache = (float **)calloc(c->num_hidden_layers, sizeof(float *));
   for (size_t i = 0; i < c->num_hidden_layers; i++) {
@@ -726,3 +728,17 @@ const float *oq_state_logits(const oq_state *s) { return s->logits; }
 const float *oq_state_residual(const oq_state *s) { return s->residual; }
 const float *oq_state_k_cache(const oq_state *s, size_t layer) { return s->k_cache[layer]; }
 const float *oq_state_v_cache(const oq_state *s, size_t layer) { return s->v_cache[layer]; }
+
+int oq_state_load(oq_state *s, int what, size_t layer, const float *src, size_t n) {
+  if (what == 2) {
+    if (n != s->vocab) return fail("logits length %zu != vocab %zu", n, s->vocab);
+    memcpy(s->logits, src, n * sizeof(float));
+    return 0;
+  }
+  if (what != 0 && what != 1) return fail("unknown state part %d", what);
+  if (layer >= s->n_layers) return fail("layer %zu out of bounds", layer);
+  size_t kvw = s->kv_width;
+  if (n > s->max_seq_len * kvw) return fail("%zu floats exceed the layer's cache", n);
+  memcpy(what ? s->v_cache[layer] : s->k_cache[layer], src, n * sizeof(float));
+  return 0;
+}

@@ -69,6 +69,7 @@ class Oracle:
             "oq_state_residual": (F32P, [C.c_void_p]),
             "oq_state_k_cache": (F32P, [C.c_void_p, C.c_size_t]),
             "oq_state_v_cache": (F32P, [C.c_void_p, C.c_size_t]),
+            "oq_state_load": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t, F32P, C.c_size_t]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(l, name)
@@ -175,6 +176,18 @@ class OracleModel:
         p = f(self.state, layer)
         return np.ctypeslib.as_array(p, shape=(n_pos * self.cfg.kv_width,)).copy().reshape(
             n_pos, self.cfg.kv_width)
+
+    def load_kv(self, layer: int, which: str, rows: np.ndarray) -> None:
+        """Seeds the cache rows of `layer` from position 0 (e.g. with the GPU's)."""
+        r = np.ascontiguousarray(rows, dtype=np.float32).ravel()
+        if self.o.lib.oq_state_load(self.state, 0 if which == "k" else 1, layer,
+                                    r.ctypes.data_as(F32P), r.size):
+            raise RuntimeError(self.o.lib.oq_last_error().decode())
+
+    def load_logits(self, logits: np.ndarray) -> None:
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        if self.o.lib.oq_state_load(self.state, 2, 0, lg.ctypes.data_as(F32P), lg.size):
+            raise RuntimeError(self.o.lib.oq_last_error().decode())
 
     def argmax(self) -> int:
         lg = self.logits()

@@ -107,3 +107,36 @@ def test_validate_matvec_errors(llrs, backend):
 def test_backend_identity(backend):
     assert backend.name() == "hip-gfx950"
     assert backend.threads() >= 200  # compute units of an MI355X
+
+
+def outlier_activation(n: int, seed: int, kind: str) -> np.ndarray:
+    """Activations whose 16-element blocks mix scales: "spike" puts one element
+    10^3 times the others' scale in every block (the tuned kernels' int8 digits
+    are scaled per block by its largest |x|, so the small elements keep only
+    ~15 - 10 = 5 bits); "student_t" draws from a Student-t with 2 degrees of
+    freedom (heavy tails, infinite variance)."""
+    rng = np.random.default_rng(seed)
+    if kind == "spike":
+        x = rng.standard_normal(n, dtype=np.float32)
+        at = np.arange(0, n, 16) + rng.integers(0, 16, n // 16)
+        x[at] = np.float32(1e3) * np.sign(rng.standard_normal(at.size)).astype(np.float32)
+        return x
+    return rng.standard_t(2, n).astype(np.float32)
+
+
+@pytest.mark.parametrize("kind", ["spike", "student_t"])
+@pytest.mark.parametrize("ty", [12, 14, 8, 6, 2, 13, 30],
+                         ids=[NAMES[t] for t in [12, 14, 8, 6, 2, 13, 30]])
+@pytest.mark.parametrize("shape", [(18944, 3584), (3584, 18944)], ids=["up", "down"])
+def test_gemv_outlier_activations(llrs, backend, oracle, ty, shape, kind):
+    """The 1e-3 GEMV bar (src/quant.rs:458-648) holds for activations with
+    outliers, at the config 2 shapes."""
+    rows, cols = shape
+    print(f"[case] {NAMES[ty]} {rows}x{cols} {kind}", flush=True)
+    data = llrs.blocks.random_tensor_bytes(ty, rows, cols, seed=5)
+    x = outlier_activation(cols, seed=6, kind=kind)
+    dt = backend.upload(llrs.QuantTensor.from_owned(data, (rows, cols), ty))
+    y = np.empty(rows, np.float32)
+    backend.matvec(dt, x, y)
+    ref = oracle.matvec(data, ty, rows, cols, x)
+    assert_gemv_close(y, ref, f"{NAMES[ty]} {rows}x{cols} {kind}")

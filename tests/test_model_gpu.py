@@ -246,10 +246,16 @@ def test_config3_qwen05b_shape_greedy_parity(llrs, backend, oracle, tmp_path):
         assert llrs.gguf_read_tensor(tmp_path / "c3.gguf", name)[1].quant_type == qt, name
 
 
-def test_softmax_uniform_fallback_on_gpu(llrs, backend, oracle, tmp_path):
+@pytest.mark.parametrize("decode_path", ["persistent", "per_phase"])
+def test_softmax_uniform_fallback_on_gpu(llrs, backend, oracle, tmp_path, monkeypatch, decode_path):
     """A NaN query bias in layer 0 makes every score NaN: the GPU attention must
-    fall back to the plain V mean as softmax_inplace does (src/model.rs:305-312),
-    in the single-chunk case (one position) and across three merged chunks."""
+    fall back to the plain V mean as softmax_inplace does (src/model.rs:305-312).
+    Covered: one position (single chunk); a 70-token prompt fed token by token
+    through the decode step (from position 64 on, three 32-position chunks are
+    merged, each chunk's partial non-finite); the batched prefill's attention
+    tiles; then 8 decode steps from position 70, every step's logits against
+    the oracle's.  Once on the persistent decode kernel, once on the
+    launch-per-phase path."""
     cfg = tiny_cfg(llrs, seed=29, num_hidden_layers=2)
     path = tmp_path / "n.gguf"
     cfg.write_gguf(path)
@@ -261,15 +267,81 @@ def test_softmax_uniform_fallback_on_gpu(llrs, backend, oracle, tmp_path):
     raw[at:at + len(old)] = np.full(bias.size, np.nan, np.float32).tobytes()
     path.write_bytes(bytes(raw))
     prompt = np.random.default_rng(29).integers(0, cfg.vocab_size, 70).astype(np.uint32)
+    if decode_path == "per_phase":
+        monkeypatch.setenv("LLRS_NO_PERSISTENT", "1")
     model = llrs.ModelLoader.load_dynamic(path, backend)  # the patched file, not a rewrite
     kv, om = llrs.KVCache(model, 128), oracle.load(path)
-    for n in (1, len(prompt)):
-        model.prefill(prompt[:n], 0, kv)
-        om.new_state(128)
-        om.prefill(prompt[:n], 0)
+    assert kv.persistent == (decode_path == "persistent")
+
+    def check(what):
         lg, lo = kv.logits(), om.logits()
         assert np.isfinite(lo).all()
         err = float(np.abs(lg - lo).max())
-        print(f"[model] nan-q prompt {n}: logits max-abs err {err:.3e}", flush=True)
+        print(f"[model] nan-q {decode_path} {what}: logits max-abs err {err:.3e}", flush=True)
         assert err <= LOGIT_TOL
         assert kv.argmax() == om.argmax()
+
+    for n, tokenwise in ((1, False), (len(prompt), True), (len(prompt), False)):
+        if tokenwise:
+            monkeypatch.setenv("LLRS_PREFILL_TOKENWISE", "1")
+        model.prefill(prompt[:n], 0, kv)
+        monkeypatch.delenv("LLRS_PREFILL_TOKENWISE", raising=False)
+        om.new_state(128)
+        om.prefill(prompt[:n], 0)
+        check(f"prompt {n} ({'token by token' if tokenwise else 'batched'})")
+    for step in range(8):
+        tok = om.argmax()
+        pos = len(prompt) + step
+        model.forward_token(tok, pos, kv)
+        om.forward_token(tok, pos)
+        check(f"decode at {pos}")
+
+
+@pytest.mark.parametrize("flag", [0, 1], ids=["barrier", "attention_merge"])
+def test_wait_flag_reported_once_then_recovers(llrs, backend, tmp_path, flag):
+    """A device-side wait that gave up (set here from the host) fails the next
+    call with LLRS_E_HIP; the flag is then cleared, so a fresh prefill and
+    decode compute the same tokens as an untouched cache."""
+    cfg = tiny_cfg(llrs, seed=19)
+    cfg.write_gguf(tmp_path / "w.gguf")
+    model = llrs.ModelLoader.load_dynamic(tmp_path / "w.gguf", backend)
+    prompt = np.array([11, 22, 33, 44, 55], np.uint32)
+    ref = llrs.KVCache(model, 64)
+    model.prefill(prompt, 0, ref)
+    want = model.decode_greedy(len(prompt), 12, ref)
+    kv = llrs.KVCache(model, 64)
+    assert kv.persistent
+    model.prefill(prompt, 0, kv)
+    assert llrs.lib().llrs_kv_debug_set_wait_flag(kv.handle, flag) == 0
+    with pytest.raises(llrs.LlrsError, match="timed out"):
+        model.decode_greedy(len(prompt), 4, kv)
+    model.prefill(prompt, 0, kv)
+    np.testing.assert_array_equal(model.decode_greedy(len(prompt), 12, kv), want)
+    # llrs_kv_reset clears a pending flag too.
+    assert llrs.lib().llrs_kv_debug_set_wait_flag(kv.handle, flag) == 0
+    kv.reset()
+    model.prefill(prompt, 0, kv)
+    np.testing.assert_array_equal(model.decode_greedy(len(prompt), 12, kv), want)
+
+
+@pytest.mark.parametrize("n,ffn", [(40, 8192), (512, 18944)], ids=["split_k", "last_round_split"])
+def test_batched_prefill_is_deterministic(llrs, backend, tmp_path, n, ffn):
+    """Two batched prefills of one prompt leave bit-identical K/V rows and
+    logits: the split-K GEMM partials are reduced in a fixed order (the
+    reference is bit-reproducible for any thread count, src/backend.rs:143-162).
+    40 tokens split K over several workgroups for every matrix; 512 tokens
+    through FFN matrices of 18,944 rows run gate and up as a full round of
+    tiles plus a last round split over the slots."""
+    cfg = tiny_cfg(llrs, hidden_size=1024, num_attention_heads=8, num_key_value_heads=2,
+                   intermediate_size=ffn, num_hidden_layers=2, seed=37)
+    cfg.write_gguf(tmp_path / "d.gguf")
+    model = llrs.ModelLoader.load_dynamic(tmp_path / "d.gguf", backend)
+    prompt = np.random.default_rng(37).integers(0, cfg.vocab_size, n).astype(np.uint32)
+    kvs = [llrs.KVCache(model, 512) for _ in range(2)]
+    for kv in kvs:
+        model.prefill(prompt, 0, kv)
+    np.testing.assert_array_equal(kvs[0].logits().view(np.uint32), kvs[1].logits().view(np.uint32))
+    for layer in range(cfg.num_hidden_layers):
+        for which in ("k", "v"):
+            np.testing.assert_array_equal(kvs[0].layer(layer, which, n).view(np.uint32),
+                                          kvs[1].layer(layer, which, n).view(np.uint32))
