@@ -250,6 +250,17 @@ typedef struct llrs_sampling {
  * validate_sampling (src/engine.rs:327-338). */
 int llrs_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent, size_t n_recent,
                 float uniform, uint32_t *out_token);
+/* llrs_sample without any allocation, on any call: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under
+ * graph capture, serving loops, harnesses that forbid hipMalloc).  Its
+ * scratch (sort keys and indices, the repeat window, the radix sort's
+ * temporary storage: 8.3 MB) is one file-scope device array per GPU, held
+ * until the process ends, so the vocabulary is limited to 262,144 tokens and
+ * the window to 65,536 (larger inputs fail with LLRS_E_INVALID).  Every call
+ * on one GPU shares that array: calls that overlap on one GPU (two threads,
+ * two streams) race.  Same arguments, validation and results as llrs_sample. */
+int llrs_sample_noalloc(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent,
+                        size_t n_recent, float uniform, uint32_t *out_token);
 /* Readback for tests: InferenceBuffers::logits (src/cache.rs:76) and
  * KVCache::{k,v}_cache[layer][0 .. n) (src/cache.rs:5-7). */
 int llrs_read_logits(llrs_kv *kv, float *out, size_t n);

@@ -131,6 +131,7 @@ SIGNATURES = [
     ("llrs_decode_greedy", C.c_int, [P, P, SZ, SZ, U32P]),
     ("llrs_argmax", C.c_int, [P, U32P]),
     ("llrs_sample", C.c_int, [P, P, P, SZ, C.c_float, U32P]),
+    ("llrs_sample_noalloc", C.c_int, [P, P, P, SZ, C.c_float, U32P]),
     ("llrs_read_logits", C.c_int, [P, F32P, SZ]),
     ("llrs_read_kv", C.c_int, [P, SZ, C.c_int, F32P, SZ]),
     ("llrs_read_tokens", C.c_int, [P, SZ, SZ, U32P]),

@@ -1483,6 +1483,22 @@ int llrs_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent, 
   return sample_with(kv, opts, recent, n_recent, uniform, w, out_token);
 }
 
+int llrs_sample_noalloc(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent,
+                        size_t n_recent, float uniform, uint32_t *out_token) {
+  clear_error();
+  LLRS_TRY(validate_sample(kv, opts, recent, n_recent, uniform, out_token));
+  if (kv->m->cfg.vocab_size > (size_t)kNoAllocMaxVocab)
+    return set_error(LLRS_E_INVALID, "llrs_sample_noalloc: vocabulary %zu exceeds its limit of %d tokens",
+                     kv->m->cfg.vocab_size, kNoAllocMaxVocab);
+  if (n_recent > (size_t)kNoAllocMaxRecent)
+    return set_error(LLRS_E_INVALID, "llrs_sample_noalloc: repeat window %zu exceeds its limit of %d tokens",
+                     n_recent, kNoAllocMaxRecent);
+  LLRS_HIP(hipSetDevice(kv->m->b->device));
+  SampleScratch w;
+  LLRS_TRY(sample_noalloc_scratch(w));
+  return sample_with(kv, opts, recent, n_recent, uniform, w, out_token);
+}
+
 int llrs_read_logits(llrs_kv *kv, float *out, size_t n) {
   clear_error();
   if (!kv || !out) return set_error(LLRS_E_INVALID, "kv/out is NULL");

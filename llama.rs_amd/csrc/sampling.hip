@@ -16,6 +16,8 @@
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
+#include <mutex>
+
 #include "common.h"
 #include "sampling.h"
 
@@ -143,6 +145,55 @@ __global__ __launch_bounds__(kSelectThreads) void sample_select_kernel(
 }
 
 }  // namespace
+
+namespace {
+
+// The allocation-free sampler's scratch: keys, sorted keys, indices, sorted
+// indices (kNoAllocMaxVocab words each), the repeat window, the result word,
+// then the radix sort's temporary storage.  In host code `scratch` names a
+// host-side stand-in, never the device memory: kernels and copies get the
+// address hipGetSymbolAddress returns for the current device.
+constexpr size_t kNoAllocWords = 4 * (size_t)kNoAllocMaxVocab + kNoAllocMaxRecent + 64;
+constexpr size_t kNoAllocBytes = kNoAllocWords * 4 + kNoAllocSortBytes;
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_dev[kMaxDevices] = {};  // per device: its copy of `scratch`
+
+}  // namespace
+
+int sample_noalloc_scratch(SampleScratch &w) {
+  int dev = 0;
+  LLRS_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(LLRS_E_UNSUPPORTED, "device %d", dev);
+  uint8_t *base = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+      void *p = nullptr;
+      LLRS_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+      const size_t need = sample_sort_bytes(kNoAllocMaxVocab);
+      if (need > kNoAllocSortBytes)
+        return set_error(LLRS_E_UNSUPPORTED, "the radix sort needs %zu temporary bytes, %zu reserved", need,
+                         kNoAllocSortBytes);
+      g_scratch_dev[dev] = static_cast<uint8_t *>(p);
+    }
+    base = g_scratch_dev[dev];
+  }
+  uint32_t *words = reinterpret_cast<uint32_t *>(base);
+  w.n = kNoAllocMaxVocab;
+  w.max_recent = kNoAllocMaxRecent;
+  w.keys = words;
+  w.keys_sorted = words + kNoAllocMaxVocab;
+  w.idx = words + 2 * (size_t)kNoAllocMaxVocab;
+  w.idx_sorted = words + 3 * (size_t)kNoAllocMaxVocab;
+  w.recent = words + 4 * (size_t)kNoAllocMaxVocab;
+  w.token = w.recent + kNoAllocMaxRecent;
+  w.tmp = base + kNoAllocWords * 4;
+  w.tmp_bytes = kNoAllocSortBytes;
+  return LLRS_OK;
+}
 
 size_t sample_sort_bytes(int n) {
   size_t bytes = 0;

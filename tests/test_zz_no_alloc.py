@@ -1,0 +1,64 @@
+"""llrs_sample_noalloc: the sampler with its scratch in a file-scope device
+array (no allocation on any call) against llrs_sample (scratch allocated on
+first use), through the C ABI.
+
+Two calls in a row on the same GPU share that array: a 152,064-token
+vocabulary first, then a 1,000-token one (a smaller input, whose call must
+not see anything the larger one left).  Each call's token must equal
+llrs_sample's for the same options, window and uniform draw.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def noalloc(llrs, kv, opts, recent, u):
+    f = llrs.lib().llrs_sample_noalloc  # bound from include/llrs.h's signature
+    r = np.ascontiguousarray(np.asarray(recent, dtype=np.uint32))
+    o = llrs._Sampling(opts.temperature, opts.top_p, opts.top_k, opts.repetition_penalty)
+    t = C.c_uint32()
+    rc = f(kv.handle, C.byref(o), r.ctypes.data_as(C.c_void_p) if r.size else None, r.size, float(u),
+           C.byref(t))
+    if rc != 0:
+        raise llrs.LlrsError(rc, llrs.lib().llrs_last_error().decode())
+    return int(t.value)
+
+
+def model_kv(llrs, backend, vocab, seed):
+    cfg = llrs.SynthConfig(hidden_size=256, intermediate_size=512, num_attention_heads=4,
+                           num_key_value_heads=2, num_hidden_layers=1, vocab_size=vocab,
+                           max_position_embeddings=256, recipe=llrs.LoadQuantization.Q4KM,
+                           seed=seed, tie_word_embeddings=False)
+    model = llrs.HipQwen2Model.synthetic(backend, cfg)
+    kv = llrs.KVCache(model, 64)
+    model.prefill(np.arange(1, 9, dtype=np.uint32) * 37 % vocab, 0, kv)
+    return model, kv
+
+
+def test_sample_noalloc_matches_sample(llrs, backend):
+    rng = np.random.default_rng(91)
+    cases = [llrs.SamplingOptions(),
+             llrs.SamplingOptions(temperature=1.3, top_p=0.95, top_k=0, repetition_penalty=1.0),
+             llrs.SamplingOptions(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.1)]
+    for vocab, seed in ((152064, 3), (1000, 4)):  # the second call is the smaller input
+        model, kv = model_kv(llrs, backend, vocab, seed)
+        for opts in cases:
+            recent = rng.integers(0, vocab, 64).astype(np.uint32)
+            for _ in range(4):
+                u = float(rng.random())
+                a, b = noalloc(llrs, kv, opts, recent, u), kv.sample(opts, u, recent)
+                print(f"[noalloc] vocab {vocab} T={opts.temperature} u={u:.3f}: {a} vs {b}", flush=True)
+                assert a == b
+        # The window alone changes: the penalty must see the new one.
+        assert noalloc(llrs, kv, cases[2], [], 0.5) == kv.sample(cases[2], 0.5, [])
+
+
+def test_sample_noalloc_rejects_oversized_window(llrs, backend):
+    _, kv = model_kv(llrs, backend, 1000, 5)
+    with pytest.raises(llrs.LlrsError, match="repeat window"):
+        noalloc(llrs, kv, llrs.SamplingOptions(), np.zeros(65537, np.uint32), 0.5)
