@@ -5,17 +5,20 @@ Workload (benchmark config 5): a synthetic Qwen2.5-7B-shaped model (hidden
 3584, 28 layers, 28 Q / 4 KV heads, head_dim 128, FFN 18944, vocab 152064,
 untied LM head, rope_theta 1e6), random-init N(0, 0.02) weights quantized
 with the reference's q4km recipe (Q4_K q/k/o/gate/up, Q8_0 v/embeddings/LM
-head, Q6_K ffn_down), generated in HBM.  A 512-token random prompt is
-prefilled (an untimed warm-up, then the median of 3 timed prefills), then
-`--warmup` untimed and `--steps` timed greedy decode steps run; one step =
-one token through the whole model (the decode loop of
-InferenceEngine::benchmark_tokens, src/engine.rs:205-216), replayed from a
-captured hipGraph with the token and position kept on the device.
+head, Q6_K ffn_down), generated in HBM.  The protocol is llama-bench's
+(src/bin/llama-bench.rs:113-141): an untimed benchmark_tokens of 8 prompt
+tokens and 1 decode step (plus one untimed round with `--warmup` decode
+steps), then `--rounds` timed rounds of benchmark_tokens (src/engine.rs:
+189-223: reset, prefill the 512-token random prompt with the batched MFMA
+path, then `--steps` greedy decode steps, each one token through the whole
+model, replayed from a captured hipGraph with the token and position kept on
+the device), and the round that is the median by prefill + decode time.
 
-Prints ONE JSON line: decode tok/s as `value`, the whole-step HBM rate, the
-dominant kernel's roofline (HIP-event timing of its own launches) and the
-CPU baseline (the oracle's restated AVX2 path on this host's cores, on a
-bounded sample of the same model).  `--workload cfg3|cfg4` runs the 0.5B and
+Prints ONE JSON line: that round's decode tok/s as `value` (and llama-bench's
+keys under "llama_bench"), the whole-step HBM rate, the dominant kernel's
+roofline (HIP-event timing of its own launches) and the CPU baseline (the
+oracle's restated AVX2 path on this host's cores, at the GPU's decode
+positions, on a bounded sample of the same model).  `--workload cfg3|cfg4` runs the 0.5B and
 1.5B end-to-end configs the same way; `--gemv` runs configs 1 and 2;
 `--load` times the SafeTensors loader's load-time quantization.
 """
@@ -76,41 +79,61 @@ def kv_bytes_per_token(cfg, pos: int) -> int:
     return cfg.num_hidden_layers * 2 * ((pos + 1) * row + row)
 
 
-def cpu_baseline(llrs, model, seconds: float, label: str, log_prefix="cpu") -> dict:
-    """The oracle's restated AVX2 path (src/simd.rs) on all host threads, on the same
-    model bytes (exported from HBM), decoding from position 0 for ~`seconds`."""
+def cpu_baseline(llrs, model, kv, prompt_len: int, first_token: int, seconds: float, label: str) -> dict:
+    """The oracle's restated AVX2 path (src/simd.rs, the reference's default
+    backend) timed on this host's cores at the positions the GPU decodes: its
+    state is seeded with the GPU cache's K/V rows of the prompt (the GPU's
+    prefill), then it decodes greedily from position `prompt_len` with
+    `first_token`, each step attending over every earlier position as the
+    GPU's does.  Three samples: all host threads (the reference's default,
+    src/backend.rs:99-106), one thread, and the scalar path (the parity
+    oracle) on all threads, each for about `seconds` (one third for the
+    scalar one)."""
     sys.path.insert(0, str(ROOT / "tests"))
-    from oracle_ffi import AVX2, Oracle
+    from oracle_ffi import AVX2, SCALAR, Oracle
 
     threads = host_threads()
+    mc = model.config()
     shm = pathlib.Path("/dev/shm") if os.path.isdir("/dev/shm") else pathlib.Path("/tmp")
     path = shm / f"llrs_bench_{os.getpid()}.gguf"
+    rows = {(l, w): kv.layer(l, w, prompt_len) for l in range(mc.num_hidden_layers) for w in ("k", "v")}
+    out = {}
     try:
         t0 = time.perf_counter()
         model.export_gguf(path)
-        log(f"{log_prefix}: exported model to {path} in {time.perf_counter() - t0:.1f}s")
-        om = Oracle().load(path, kernel=AVX2, threads=threads)
-        om.new_state(160)  # the timed sample is at most 128 steps after position 0
-        t0 = time.perf_counter()
-        om.forward_token(1, 0, True)
-        first = time.perf_counter() - t0
-        n = int(max(2, min(128, seconds / max(first, 1e-3))))
-        log(f"{log_prefix}: first token {first:.2f}s; timing {n} tokens on {threads} threads")
-        tok = om.argmax()
-        t0 = time.perf_counter()
-        for p in range(1, n + 1):
-            om.forward_token(tok, p, True)
-            tok = om.argmax()
-        dt = time.perf_counter() - t0
-        del om
+        log(f"cpu: exported model to {path} in {time.perf_counter() - t0:.1f}s")
+        for name, kernel, th, budget in (("all", AVX2, threads, seconds), ("one", AVX2, 1, seconds),
+                                         ("scalar", SCALAR, threads, seconds / 3)):
+            om = Oracle().load(path, kernel=kernel, threads=th)
+            om.new_state(prompt_len + 130)
+            for (l, w), r in rows.items():
+                om.load_kv(l, w, r)
+            tok, n, t0 = first_token, 0, time.perf_counter()
+            while n < 128 and (n < 2 or time.perf_counter() - t0 < budget):
+                om.forward_token(tok, prompt_len + n, True)
+                tok = om.argmax()
+                n += 1
+            dt = time.perf_counter() - t0
+            out[name] = (n, dt, th)
+            log(f"cpu {name}: {n} steps at positions {prompt_len}-{prompt_len + n - 1} on {th} "
+                f"threads: {n / dt:.3f} tok/s")
+            del om
     finally:
         if path.exists():
             path.unlink()
-    return {"value": round(n / dt, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} greedy decode steps at positions 1-{n} of the same {label} model "
-                      f"(after 1 warm-up token at position 0), oracle's restated AVX2 path "
-                      f"(src/simd.rs) with the reference's row-parallel policy on {threads} "
-                      f"threads; the Rust reference itself cannot be built here"}
+    n, dt, th = out["all"]
+    n1, dt1, _ = out["one"]
+    ns, dts, _ = out["scalar"]
+    return {"value": round(n / dt, 4), "unit": "tok/s", "cores": th, "kind": "port",
+            "sample": f"{n} greedy decode steps at positions {prompt_len}-{prompt_len + n - 1} (the "
+                      f"GPU's decode positions) of the same {label} model, the oracle seeded with the "
+                      f"GPU's K/V rows of the {prompt_len}-token prompt; the oracle's restated AVX2 "
+                      f"path (src/simd.rs) with the reference's row-parallel policy on {th} threads; "
+                      f"the Rust reference itself cannot be built here",
+            "one_thread": {"value": round(n1 / dt1, 4), "cores": 1,
+                           "sample": f"{n1} steps from position {prompt_len}, AVX2 path"},
+            "scalar": {"value": round(ns / dts, 4), "cores": th,
+                       "sample": f"{ns} steps from position {prompt_len}, scalar path (the parity oracle)"}}
 
 
 COPY_BYTES = 256 << 20  # calibration copy: 256 MiB, 4 times
@@ -354,6 +377,7 @@ def main() -> int:
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg5")
     ap.add_argument("--steps", type=int, default=None, help="timed decode steps (workload default)")
     ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--rounds", type=int, default=3, help="timed benchmark_tokens rounds (median)")
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (workload default)")
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -403,42 +427,42 @@ def main() -> int:
     if args.projection_only:
         return projection_only(llrs, be, model, args.projection_only, args.profile_iters)
 
-    kv = llrs.KVCache(model, args.context)
+    engine = llrs.InferenceEngine(model, args.context)
+    kv = engine.kv_cache
     prompt = np.random.default_rng(wl["seed"]).integers(0, mc.vocab_size, args.prompt).astype(np.uint32)
-    # As llama-bench (src/bin/llama-bench.rs:113-126): an untimed warm-up
-    # (first launches, the prefill buffers' allocation), then the median of
-    # 3 timed prefills from position 0; the last one leaves the cache for
-    # the decode.
-    model.prefill(prompt, 0, kv)
-    rounds = []
-    for _ in range(3):
-        kv.reset()
+    # llama-bench's protocol (src/bin/llama-bench.rs:113-126): an untimed
+    # benchmark_tokens of the prompt's first 8 tokens and 1 decode step, then
+    # `rounds` timed benchmark_tokens (reset, prefill, `steps` greedy decode
+    # steps; src/engine.rs:189-223), and the round that is the median by
+    # prefill + decode time.  One more untimed round with `--warmup` decode
+    # steps comes first (the prefill buffers' allocation, graph capture).
+    engine.benchmark_tokens(prompt[:8], 1)
+    engine.benchmark_tokens(prompt, args.warmup)
+    results = []
+    for _ in range(args.rounds):
         be.synchronize()
-        t0 = time.perf_counter()
-        model.prefill(prompt, 0, kv)
-        be.synchronize()
-        rounds.append(time.perf_counter() - t0)
-    prefill_s = sorted(rounds)[1]
+        results.append(engine.benchmark_tokens(prompt, args.steps))
+    results.sort(key=lambda r: r.prefill_s + r.decode_s)
+    med = results[len(results) // 2]
+    prefill_s, dt, toks = med.prefill_s, med.decode_s, med.tokens
     pf_flops = prefill_flops(mc, args.prompt)
+    log(f"rounds (prefill ms, decode ms): "
+        + ", ".join(f"({r.prefill_s * 1e3:.1f}, {r.decode_s * 1e3:.1f})" for r in results))
     log(f"prefill {args.prompt} tokens in {prefill_s * 1e3:.1f} ms ({args.prompt / prefill_s:.1f} tok/s, "
         f"{pf_flops / prefill_s / 1e12:.1f} TFLOP/s = {100 * pf_flops / prefill_s / PEAK_F16_FLOPS:.2f}% "
         f"of the f16 MFMA peak)")
-
-    start = args.prompt
-    if args.warmup:
-        model.decode_greedy(start, args.warmup, kv)
-    be.synchronize()
-    t0 = time.perf_counter()
-    toks = model.decode_greedy(start + args.warmup, args.steps, kv)
-    be.synchronize()
-    dt = time.perf_counter() - t0
     tps = args.steps / dt
-    pos0 = start + args.warmup
+    pos0 = args.prompt
     bytes_tok = wbytes + sum(kv_bytes_per_token(mc, p) for p in range(pos0, pos0 + args.steps)) / args.steps
     hbm_gbs = bytes_tok * tps / 1e9
     log(f"decode {args.steps} steps in {dt * 1e3:.1f} ms: {tps:.1f} tok/s, "
         f"{hbm_gbs:.0f} GB/s ({100 * hbm_gbs / PEAK_HBM_GBS:.1f}% of peak); "
-        f"first tokens {toks[:6].tolist()}")
+        f"first tokens {list(toks[:6])}")
+    llama_bench = {"architecture": model.architecture(), "backend": be.name(), "threads": be.threads(),
+                   "load_ms": round(gen_s * 1e3, 3), "prompt_tokens": args.prompt,
+                   "prefill_ms": round(prefill_s * 1e3, 3), "prefill_tps": round(args.prompt / prefill_s, 3),
+                   "decode_tokens": args.steps, "decode_ms": round(dt * 1e3, 3),
+                   "decode_tps": round(tps, 3)}
 
     # On-device sampling (sample_current_logits, src/engine.rs:253-325) of the
     # last logits with the engine's default options: host-synchronous calls.
@@ -487,17 +511,22 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(llrs, model, args.cpu_seconds, f"{args.workload} {wl['recipe'].lower()}")
-        log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
+        cpu = cpu_baseline(llrs, model, kv, args.prompt, int(toks[0]), args.cpu_seconds,
+                           f"{args.workload} {wl['recipe'].lower()}")
+        log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads, "
+            f"{cpu['one_thread']['value']} on one, scalar {cpu['scalar']['value']}")
 
     out = {
         "metric": wl["metric"], "value": round(tps, 3), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * dt / args.steps, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8x2 activation digits . q4km weight codes -> int32, f32 scales and sums",
         "data": f"synthetic (random-init N(0,0.02) weights, {wl['recipe'].lower()}-quantized in HBM; "
                 "random prompt ids)",
         "config": {"workload": wl["desc"], "prompt_tokens": args.prompt, "decode_start_pos": pos0,
-                   "context": args.context, "global_batch": 1, "parallelism": "none"},
+                   "context": args.context, "global_batch": 1, "parallelism": "none",
+                   "protocol": f"llama-bench: warm-up, median of {args.rounds} rounds by prefill + decode"},
+        "llama_bench": llama_bench,
         "hbm_gbps": round(hbm_gbs, 1), "hbm_pct_peak": round(100 * hbm_gbs / PEAK_HBM_GBS, 2),
         "sample_us": round(sample_us, 1),
         "bytes_per_token": int(bytes_tok), "prefill_tps": round(args.prompt / prefill_s, 2),

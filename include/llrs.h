@@ -261,6 +261,35 @@ int llrs_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent, 
  * two streams) race.  Same arguments, validation and results as llrs_sample. */
 int llrs_sample_noalloc(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent,
                         size_t n_recent, float uniform, uint32_t *out_token);
+/* InferenceEngine::generate_with_metrics' token loop (src/engine.rs:115-186)
+ * on token ids (the tokenizer stays with the caller): reset the cache, seed
+ * the repeat window with the prompt's last repeat_last_n tokens (136-143),
+ * prefill, then up to min(max_new_tokens, context - n_prompt) times: sample
+ * the current logits (llrs_sample, with uniforms[i] as the i-th draw; unused
+ * and may be NULL when temperature is 0), record the token, remember it, stop
+ * if it is one of eos_ids (the EOS token is kept, as the reference pushes
+ * before checking), else forward it at the next position.  Fails as the
+ * reference does on an empty prompt and on a prompt that does not leave a
+ * position for decoding ("prompt has N tokens, but context is M").
+ * out_tokens holds max_new_tokens ids; result gets the counts and the
+ * prefill / decode wall time (InferenceMetrics, src/benchmark.rs:3-34). */
+typedef struct llrs_generation {
+  size_t prompt_tokens, generated_tokens;
+  double prefill_ms, decode_ms;
+  int stopped_on_eos;
+} llrs_generation;
+int llrs_generate(llrs_model *m, llrs_kv *kv, const uint32_t *prompt, size_t n_prompt,
+                  const llrs_sampling *opts, size_t repeat_last_n, const uint32_t *eos_ids,
+                  size_t n_eos, size_t max_new_tokens, const float *uniforms, uint32_t *out_tokens,
+                  llrs_generation *result);
+/* find_eos_tokens (src/engine.rs:340-387), host only: generation_config.json's
+ * eos_token_id (a number or an array) in the model's directory (the path
+ * itself if a directory, else its parent), then the ids of "<|im_end|>" and
+ * "<|endoftext|>" in tokenizer.json (added tokens first, then the model's
+ * vocabulary, as Tokenizer::token_to_id), sorted and deduplicated.
+ * tokenizer.json is required (InferenceEngine::from_path loads it first).
+ * *n_out = the count; out may be NULL with capacity 0 to query it. */
+int llrs_find_eos_tokens(const char *model_path, uint32_t *out, size_t capacity, size_t *n_out);
 /* Readback for tests: InferenceBuffers::logits (src/cache.rs:76) and
  * KVCache::{k,v}_cache[layer][0 .. n) (src/cache.rs:5-7). */
 int llrs_read_logits(llrs_kv *kv, float *out, size_t n);

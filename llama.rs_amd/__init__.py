@@ -71,6 +71,11 @@ class _Sampling(C.Structure):
                 ("repetition_penalty", C.c_float)]
 
 
+class _Generation(C.Structure):
+    _fields_ = [("prompt_tokens", C.c_size_t), ("generated_tokens", C.c_size_t),
+                ("prefill_ms", C.c_double), ("decode_ms", C.c_double), ("stopped_on_eos", C.c_int)]
+
+
 class _SynthConfig(C.Structure):
     _fields_ = [(n, C.c_size_t) for n in (
         "hidden_size", "intermediate_size", "num_attention_heads", "num_key_value_heads",
@@ -132,6 +137,8 @@ SIGNATURES = [
     ("llrs_argmax", C.c_int, [P, U32P]),
     ("llrs_sample", C.c_int, [P, P, P, SZ, C.c_float, U32P]),
     ("llrs_sample_noalloc", C.c_int, [P, P, P, SZ, C.c_float, U32P]),
+    ("llrs_generate", C.c_int, [P, P, U32P, SZ, P, SZ, U32P, SZ, SZ, F32P, U32P, P]),
+    ("llrs_find_eos_tokens", C.c_int, [C.c_char_p, U32P, SZ, C.POINTER(SZ)]),
     ("llrs_read_logits", C.c_int, [P, F32P, SZ]),
     ("llrs_read_kv", C.c_int, [P, SZ, C.c_int, F32P, SZ]),
     ("llrs_read_tokens", C.c_int, [P, SZ, SZ, U32P]),
@@ -392,8 +399,8 @@ __all__ = ["gguf_read_tensor", "safetensors_read_tensor", "model_format", "LlrsE
 from . import blocks  # noqa: E402
 from .model import (LlamaConfig, KVCache, HipQwen2Model, ModelLoader,  # noqa: E402
                     GgufLoader, SafetensorsLoader, hf_config, SynthConfig, InferenceEngine,
-                    Sampler, SamplingOptions)
+                    Sampler, SamplingOptions, find_eos_tokens, GenerationOutput)
 
 __all__ += ["LlamaConfig", "KVCache", "HipQwen2Model", "ModelLoader", "GgufLoader",
             "SafetensorsLoader", "hf_config", "SynthConfig", "InferenceEngine", "Sampler",
-            "SamplingOptions"]
+            "SamplingOptions", "find_eos_tokens", "GenerationOutput"]

@@ -32,8 +32,8 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-I", s
 HIP_FLAGS = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-munsafe-fp-atomics"]
 # The shared host/device encoders must evaluate f32 exactly as written.
-PER_FILE = {"quantize.hip": ["-ffp-contract=off"], "synth.cpp": ["-ffp-contract=off"],
-            "model.cpp": ["-ffp-contract=off"]}
+PER_FILE = {"quantize.hip": ["-ffp-contract=off"], "quantize_host.cpp": ["-ffp-contract=off"],
+            "synth.cpp": ["-ffp-contract=off"], "model.cpp": ["-ffp-contract=off"]}
 
 
 def sources():

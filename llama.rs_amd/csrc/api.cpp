@@ -17,16 +17,6 @@
 
 namespace llrs {
 
-static thread_local char g_error[1024];
-
-int set_error(int code, const char *fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_error, sizeof g_error, fmt, ap);
-  va_end(ap);
-  return code;
-}
-void clear_error() { g_error[0] = 0; }
 
 static int ensure_scratch(llrs_backend *b, size_t nx, size_t ny) {
   if (nx > b->x_cap) {
@@ -109,7 +99,6 @@ using namespace llrs;
 
 extern "C" {
 
-const char *llrs_last_error(void) { return g_error; }
 
 int llrs_backend_create(const llrs_backend_config *cfg, llrs_backend **out) {
   clear_error();

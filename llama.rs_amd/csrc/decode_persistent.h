@@ -45,6 +45,10 @@ inline size_t persistent_static_lds(int head_dim) {
   return 2 * (size_t)(kPersistentThreads / 64) * head_dim * 4 + 512;
 }
 
+// A type argument meaning "chosen per layer" (V of the Q/K/V launch and
+// ffn_down in the Q4_K family: the kernel reads each layer's type and branches).
+constexpr uint32_t kTypePerLayer = 0xffffffffu;
+
 // Whether the step's weight types and geometry have an instantiation.
 bool decode_persistent_supports(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, uint32_t t_gu,
                                 uint32_t t_down, int head_dim);

@@ -87,6 +87,8 @@ __device__ void bar_wait(unsigned *bar, unsigned *err, int nwg, unsigned k) {
 
 typedef const __attribute__((address_space(4))) PersistentLayer ConstLayer;
 
+template <uint32_t T> struct TypeC { static constexpr uint32_t value = T; };
+
 // LONG: the instantiation whose attention also has the multi-chunk items of
 // positions past 2,048 (the other one keeps the single-chunk path's register
 // allocation; it stays correct at any position, with more partials to merge).
@@ -116,13 +118,24 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
     // The phase objects are value-initialised: a member that one path leaves
     // unset would otherwise be carried in registers from the previous layer.
     {  // RMSNorm + Q/K/V (+ bias)
-      GemvPhase<TQ, TV, false, true> ph{};
-      ph.prefetch(L.qkv, wg, nwg);
-      if (k) bar_wait(p.bar, p.err, nwg, k);
-      STAMP(k, 0);
-      STAMP_PHASE(ph, k);
-      ph.finish(L.qkv, smem, red);
-      bar_arrive(p.bar, wg, k);
+      auto qkv = [&](auto tv) {
+        GemvPhase<TQ, decltype(tv)::value, false, true> ph{};
+        ph.prefetch(L.qkv, wg, nwg);
+        if (k) bar_wait(p.bar, p.err, nwg, k);
+        STAMP(k, 0);
+        STAMP_PHASE(ph, k);
+        ph.finish(L.qkv, smem, red);
+        bar_arrive(p.bar, wg, k);
+      };
+      if constexpr (TV == kTypePerLayer) {  // V's type, read per layer (a uniform branch)
+        switch (L.qkv.seg[L.qkv.nseg - 1].type) {
+          case LLRS_Q6_K: qkv(TypeC<LLRS_Q6_K>{}); break;
+          case LLRS_Q4_K: qkv(TypeC<LLRS_Q4_K>{}); break;
+          default: qkv(TypeC<LLRS_Q8_0>{}); break;
+        }
+      } else {
+        qkv(TypeC<TV>{});
+      }
       k++;
     }
     {  // RoPE, KV append, attention: one (head, chunk) item per wave
@@ -173,13 +186,23 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
       k++;
     }
     {  // ffn_down (+ residual)
-      GemvPhase<TD, TD, false, true> ph{};
-      ph.prefetch(L.down, wg, nwg);
-      bar_wait(p.bar, p.err, nwg, k);
-      STAMP(k, 0);
-      STAMP_PHASE(ph, k);
-      ph.finish(L.down, smem, red);
-      bar_arrive(p.bar, wg, k);
+      auto down = [&](auto td) {
+        GemvPhase<decltype(td)::value, decltype(td)::value, false, true> ph{};
+        ph.prefetch(L.down, wg, nwg);
+        bar_wait(p.bar, p.err, nwg, k);
+        STAMP(k, 0);
+        STAMP_PHASE(ph, k);
+        ph.finish(L.down, smem, red);
+        bar_arrive(p.bar, wg, k);
+      };
+      if constexpr (TD == kTypePerLayer) {
+        if (L.down.seg[0].type == LLRS_Q4_K)
+          down(TypeC<LLRS_Q4_K>{});
+        else
+          down(TypeC<LLRS_Q6_K>{});
+      } else {
+        down(TypeC<TD>{});
+      }
       k++;
     }
   }
@@ -228,7 +251,11 @@ bool decode_persistent_supports(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, uint
                        t_gu == LLRS_Q5_0 && t_down == LLRS_Q6_K;
   const bool q4k = t_qkv == LLRS_Q4_K && t_v == LLRS_Q4_K && t_o == LLRS_Q4_K && t_gu == LLRS_Q4_K &&
                    t_down == LLRS_Q4_K;
-  return q4km || q4km_q5 || q4k;
+  // Q4_K q/k/o/gate/up with V and ffn_down types chosen per layer (V: Q8_0,
+  // Q4_K or Q6_K; down: Q4_K or Q6_K), e.g. llama.cpp's Q4_K_M files.
+  const bool mixed = t_qkv == LLRS_Q4_K && t_o == LLRS_Q4_K && t_gu == LLRS_Q4_K &&
+                     t_v == kTypePerLayer && t_down == kTypePerLayer;
+  return q4km || q4km_q5 || q4k || mixed;
 }
 
 int decode_persistent_blocks_per_cu(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, uint32_t t_gu,
@@ -241,6 +268,9 @@ int decode_persistent_blocks_per_cu(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, 
     return occupancy_types<LLRS_Q5_0, LLRS_Q8_0, LLRS_Q5_0, LLRS_Q5_0, LLRS_Q6_K>(head_dim, lds, long_items, blocks);
   if (t_qkv == LLRS_Q4_K && t_v == LLRS_Q4_K)
     return occupancy_types<LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K>(head_dim, lds, long_items, blocks);
+  if (t_qkv == LLRS_Q4_K && t_v == kTypePerLayer)
+    return occupancy_types<LLRS_Q4_K, kTypePerLayer, LLRS_Q4_K, LLRS_Q4_K, kTypePerLayer>(head_dim, lds, long_items,
+                                                                                     blocks);
   return set_error(LLRS_E_UNSUPPORTED, "persistent decode: no instantiation for these weight types");
 }
 
@@ -256,6 +286,9 @@ int launch_decode_persistent(const PersistentArgs &p, uint32_t t_qkv, uint32_t t
     return launch_types<LLRS_Q5_0, LLRS_Q8_0, LLRS_Q5_0, LLRS_Q5_0, LLRS_Q6_K>(p, head_dim, grid, lds, s, long_items);
   if (t_qkv == LLRS_Q4_K && t_v == LLRS_Q4_K)
     return launch_types<LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K, LLRS_Q4_K>(p, head_dim, grid, lds, s, long_items);
+  if (t_qkv == LLRS_Q4_K && t_v == kTypePerLayer)
+    return launch_types<LLRS_Q4_K, kTypePerLayer, LLRS_Q4_K, LLRS_Q4_K, kTypePerLayer>(p, head_dim, grid, lds, s,
+                                                                                   long_items);
   return set_error(LLRS_E_UNSUPPORTED, "persistent decode: no instantiation for these weight types");
 }
 

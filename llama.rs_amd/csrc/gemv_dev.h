@@ -533,7 +533,6 @@ struct GemvPhase {
   int lane, wave, nw, wg, nwg, wrow0, wrow1, s0, base0;
   bool s0_is_ta;
   SegStream<TA, DUAL> A;
-  SegStream<TB, false> B;  // the last segment when its type differs (TB != TA)
 #ifdef LLRS_STAMPS
   // Timing build only: wall-clock stamps of this workgroup's phase, [1] when
   // the activation is staged, [2] when the weight streaming ends.
@@ -562,15 +561,12 @@ struct GemvPhase {
     base0 = 0;
     while (s0 + 1 < a.nseg && wrow0 >= base0 + a.seg[s0].rows) base0 += a.seg[s0++].rows;
     s0_is_ta = DUAL || TA == TB || s0 + 1 < a.nseg;
-    int lo, hi;
-    seg_range(a, s0, base0, lo, hi);
-    const FastSeg Sw = shifted(a.seg[s0], lo - base0);
     if (s0_is_ta) {
+      int lo, hi;
+      seg_range(a, s0, base0, lo, hi);
+      const FastSeg Sw = shifted(a.seg[s0], lo - base0);
       const FastSeg Uw = DUAL ? shifted(a.seg[1], lo - base0) : Sw;
       A.begin(Sw, Uw, lo, max(lo, hi), wave, nw, a.cols, lane);
-    } else if constexpr (!DUAL && TA != TB) {
-      // The workgroup's rows start in the last segment: its loads go first.
-      B.begin(Sw, Sw, lo, max(lo, hi), wave, nw, a.cols, lane);
     }
   }
 
@@ -629,10 +625,9 @@ struct GemvPhase {
         int lo, hi;
         seg_range(a, s, base, lo, hi);
         if (lo < hi) {
-          if (s != s0) {  // else begun by prefetch()
-            const FastSeg Sw = shifted(S, lo - base);
-            B.begin(Sw, Sw, lo, hi, wave, nw, a.cols, lane);
-          }
+          const FastSeg Sw = shifted(S, lo - base);
+          SegStream<TB, false> B;
+          B.begin(Sw, Sw, lo, hi, wave, nw, a.cols, lane);
           B.run(L, emitter(lo));
         }
       }

@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -832,22 +833,31 @@ static bool persistent_disabled() {
 }
 
 // Chooses the persistent decode kernel when every layer runs the tuned GEMV
-// with one set of weight types that has an instantiation, and uploads the
-// per-layer arguments it reads.
+// with weight types that have an instantiation (one set for every layer, or
+// Q4_K q/k/o/gate/up with V and ffn_down types varying by layer), and
+// uploads the per-layer arguments it reads.
 static int setup_persistent(llrs_model *m, llrs_kv *kv) {
   const llrs_model_config &c = m->cfg;
   if (persistent_disabled() || c.intermediate_size % 64) return LLRS_OK;
   const size_t nl = c.num_hidden_layers;
   uint32_t t[5] = {};
+  bool varies = false, mixable = true;
   for (size_t l = 0; l < nl; l++) {
     for (int w = P_QKV; w <= P_DOWN; w++)
       if (!use_fast(m, l, w)) return LLRS_OK;
     const DevLayer &L = m->layers[l];
     const uint32_t tl[5] = {L.q->type, L.v->type, L.o->type, L.gate->type, L.down->type};
     if (l == 0) memcpy(t, tl, sizeof t);
-    if (memcmp(t, tl, sizeof t)) return LLRS_OK;
+    if (tl[0] != t[0] || tl[2] != t[2] || tl[3] != t[3]) return LLRS_OK;
+    varies = varies || tl[1] != t[1] || tl[4] != t[4];
+    mixable = mixable && (tl[1] == LLRS_Q8_0 || tl[1] == LLRS_Q4_K || tl[1] == LLRS_Q6_K) &&
+              (tl[4] == LLRS_Q4_K || tl[4] == LLRS_Q6_K);
   }
-  if (!decode_persistent_supports(t[0], t[1], t[2], t[3], t[4], (int)c.head_dim)) return LLRS_OK;
+  if (varies || !decode_persistent_supports(t[0], t[1], t[2], t[3], t[4], (int)c.head_dim)) {
+    if (!mixable) return LLRS_OK;
+    t[1] = t[4] = kTypePerLayer;  // the Q4_K family's per-layer instantiation
+    if (!decode_persistent_supports(t[0], t[1], t[2], t[3], t[4], (int)c.head_dim)) return LLRS_OK;
+  }
   const int grid = m->b->cu_count;
   // Per-layer activation buffers (each slice 256-byte aligned, so no cache
   // line holds two buffers): q|k|v, attention output, residual after o_proj
@@ -1135,18 +1145,23 @@ static int prefill_batched(llrs_model *m, llrs_kv *kv, size_t start, size_t n) {
 // The repeat window's length limit of llrs_sample.
 constexpr size_t kMaxRecent = 65536;
 
-// Arguments of llrs_sample: validate_sampling (src/engine.rs:327-338) and the
-// draw.
-static int validate_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent,
-                           size_t n_recent, float uniform, uint32_t *out_token) {
-  if (!kv || !opts || !out_token || (n_recent && !recent))
-    return set_error(LLRS_E_INVALID, "kv/opts/recent/out is NULL");
+// validate_sampling (src/engine.rs:327-338).
+static int validate_sampling(const llrs_sampling *opts) {
   if (!std::isfinite(opts->temperature) || opts->temperature < 0.0f)
     return set_error(LLRS_E_INVALID, "temperature must be finite and non-negative");
   if (!std::isfinite(opts->top_p) || !(0.0f < opts->top_p && opts->top_p <= 1.0f))
     return set_error(LLRS_E_INVALID, "top_p must be in (0, 1]");
   if (!std::isfinite(opts->repetition_penalty) || opts->repetition_penalty <= 0.0f)
     return set_error(LLRS_E_INVALID, "repetition_penalty must be finite and positive");
+  return LLRS_OK;
+}
+
+// Arguments of llrs_sample: the options, the window and the draw.
+static int validate_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent,
+                           size_t n_recent, float uniform, uint32_t *out_token) {
+  if (!kv || !opts || !out_token || (n_recent && !recent))
+    return set_error(LLRS_E_INVALID, "kv/opts/recent/out is NULL");
+  LLRS_TRY(validate_sampling(opts));
   if (!std::isfinite(uniform) || uniform < 0.0f || uniform >= 1.0f)
     return set_error(LLRS_E_INVALID, "the uniform draw must be in [0, 1)");
   if (n_recent > kMaxRecent) return set_error(LLRS_E_INVALID, "repeat window %zu > %zu", n_recent, kMaxRecent);
@@ -1497,6 +1512,61 @@ int llrs_sample_noalloc(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *
   SampleScratch w;
   LLRS_TRY(sample_noalloc_scratch(w));
   return sample_with(kv, opts, recent, n_recent, uniform, w, out_token);
+}
+
+int llrs_generate(llrs_model *m, llrs_kv *kv, const uint32_t *prompt, size_t n_prompt,
+                  const llrs_sampling *opts, size_t repeat_last_n, const uint32_t *eos_ids,
+                  size_t n_eos, size_t max_new_tokens, const float *uniforms, uint32_t *out_tokens,
+                  llrs_generation *result) {
+  clear_error();
+  if (!m || !kv || kv->m != m) return set_error(LLRS_E_INVALID, "model/kv mismatch");
+  if (!opts || !result || (n_eos && !eos_ids) || (max_new_tokens && !out_tokens))
+    return set_error(LLRS_E_INVALID, "opts/result/eos_ids/out_tokens is NULL");
+  *result = llrs_generation{};
+  if (n_prompt == 0 || !prompt) return set_error(LLRS_E_INVALID, "the prompt is empty");
+  if (n_prompt >= kv->max_seq_len)
+    return set_error(LLRS_E_INVALID, "prompt has %zu tokens, but context is %zu", n_prompt,
+                     kv->max_seq_len);
+  // validate_sampling (src/engine.rs:327-338) before anything runs, and the
+  // window and draws this loop needs.
+  LLRS_TRY(validate_sampling(opts));
+  if (repeat_last_n > kMaxRecent)
+    return set_error(LLRS_E_INVALID, "repeat window %zu > %zu", repeat_last_n, kMaxRecent);
+  if (opts->temperature > 0.0f && max_new_tokens && !uniforms)
+    return set_error(LLRS_E_INVALID, "sampling with temperature > 0 needs one uniform draw per token");
+  // reset(), then the last repeat_last_n prompt tokens seed the window (src/engine.rs:136-143).
+  LLRS_TRY(llrs_kv_reset(kv));
+  std::vector<uint32_t> recent;
+  auto remember = [&](uint32_t t) {  // InferenceEngine::remember (src/engine.rs:243-251)
+    if (!repeat_last_n) return;
+    recent.push_back(t);
+    if (recent.size() > repeat_last_n) recent.erase(recent.begin());
+  };
+  for (size_t i = n_prompt > repeat_last_n ? n_prompt - repeat_last_n : 0; i < n_prompt; i++)
+    remember(prompt[i]);
+  using clock = std::chrono::steady_clock;
+  const auto t0 = clock::now();
+  LLRS_TRY(llrs_prefill(m, kv, prompt, n_prompt, 0));
+  const auto t1 = clock::now();
+  const size_t count = std::min(max_new_tokens, kv->max_seq_len - n_prompt);
+  size_t gen = 0;
+  for (size_t i = 0; i < count; i++) {
+    uint32_t tok = 0;
+    LLRS_TRY(llrs_sample(kv, opts, recent.data(), recent.size(), uniforms ? uniforms[i] : 0.0f, &tok));
+    out_tokens[gen++] = tok;
+    remember(tok);
+    if (std::find(eos_ids, eos_ids + n_eos, tok) != eos_ids + n_eos) {
+      result->stopped_on_eos = 1;
+      break;
+    }
+    LLRS_TRY(llrs_forward_token(m, kv, tok, n_prompt + gen - 1, LLRS_LOGITS_COMPUTE));
+  }
+  const auto t2 = clock::now();
+  result->prompt_tokens = n_prompt;
+  result->generated_tokens = gen;
+  result->prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+  result->decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+  return LLRS_OK;
 }
 
 int llrs_read_logits(llrs_kv *kv, float *out, size_t n) {

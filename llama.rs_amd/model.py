@@ -14,8 +14,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from . import (HipBackend, LlrsError, LoadQuantization, LogitsMode, _check, _f32, _ModelConfig,
-               _Sampling, _SynthConfig, lib, P, SZ, U32P)
+from . import (F32P, HipBackend, LlrsError, LoadQuantization, LogitsMode, _check, _f32, _Generation,
+               _ModelConfig, _Sampling, _SynthConfig, lib, P, SZ, U32P)
 
 
 @dataclass
@@ -300,15 +300,68 @@ class InferenceMetrics:
         return self.generated_tokens / self.decode_s if self.decode_s > 0 else 0.0
 
 
-class InferenceEngine:
-    """The benchmark half of engine::InferenceEngine (src/engine.rs:189-241)."""
+def find_eos_tokens(model_path) -> list[int]:
+    """find_eos_tokens (src/engine.rs:340-387): generation_config.json's
+    eos_token_id and the ids of <|im_end|> / <|endoftext|> in tokenizer.json."""
+    n = SZ()
+    _check(lib().llrs_find_eos_tokens(str(model_path).encode(), None, 0, C.byref(n)))
+    out = np.zeros(max(n.value, 1), dtype=np.uint32)
+    _check(lib().llrs_find_eos_tokens(str(model_path).encode(), out.ctypes.data_as(U32P), out.size,
+                                      C.byref(n)))
+    return [int(t) for t in out[:n.value]]
 
-    def __init__(self, model: HipQwen2Model, context_length: int = 4096):
+
+@dataclass
+class GenerationOutput:
+    """benchmark::GenerationOutput without the text (src/benchmark.rs): the
+    generated ids and the metrics."""
+    token_ids: list
+    metrics: InferenceMetrics
+    stopped_on_eos: bool
+
+
+class InferenceEngine:
+    """engine::InferenceEngine on token ids (src/engine.rs:36-241): the
+    benchmark loop and the generation loop; the tokenizer stays with the
+    caller (pass its ids, and the EOS ids from find_eos_tokens)."""
+
+    def __init__(self, model: HipQwen2Model, context_length: int = 4096,
+                 sampling: "SamplingOptions | None" = None, repeat_last_n: int = 64,
+                 eos_token_ids=()):
         ctx = min(context_length, model.config().max_position_embeddings)
         if ctx <= 0:
             raise LlrsError(-1, "context length must be positive")
         self.model = model
         self.kv_cache = KVCache(model, ctx)
+        self.sampling = sampling or SamplingOptions()
+        self.max_repeat_window = repeat_last_n
+        self.eos_token_ids = [int(t) for t in eos_token_ids]
+
+    def generate_with_metrics(self, prompt_tokens, max_new_tokens: int, uniforms=None) -> GenerationOutput:
+        """generate_with_metrics (src/engine.rs:115-186) on ids: `uniforms` are
+        the sampler's draws in [0, 1), one per generated token (the reference
+        takes them from rand::thread_rng); None draws them with numpy."""
+        prompt = np.ascontiguousarray(prompt_tokens, dtype=np.uint32)
+        if uniforms is None:
+            uniforms = np.random.default_rng().random(max(max_new_tokens, 1))
+        u = np.ascontiguousarray(uniforms, dtype=np.float32)
+        if u.size < max_new_tokens:
+            raise LlrsError(-1, "one uniform draw per generated token is needed")
+        eos = np.ascontiguousarray(self.eos_token_ids, dtype=np.uint32)
+        out = np.zeros(max(max_new_tokens, 1), dtype=np.uint32)
+        o = self.sampling
+        opts = _Sampling(o.temperature, o.top_p, o.top_k, o.repetition_penalty)
+        res = _Generation()
+        _check(lib().llrs_generate(self.model.handle, self.kv_cache.handle,
+                                   prompt.ctypes.data_as(U32P) if prompt.size else None, prompt.size,
+                                   C.byref(opts), self.max_repeat_window,
+                                   eos.ctypes.data_as(U32P) if eos.size else None, eos.size,
+                                   max_new_tokens, u.ctypes.data_as(F32P), out.ctypes.data_as(U32P),
+                                   C.byref(res)))
+        toks = [int(t) for t in out[:res.generated_tokens]]
+        m = InferenceMetrics(res.prompt_tokens, res.generated_tokens, res.prefill_ms / 1e3,
+                             res.decode_ms / 1e3, toks)
+        return GenerationOutput(toks, m, bool(res.stopped_on_eos))
 
     def benchmark_tokens(self, prompt_tokens, decode_tokens: int) -> InferenceMetrics:
         prompt = np.ascontiguousarray(prompt_tokens, dtype=np.uint32)

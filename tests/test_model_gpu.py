@@ -345,3 +345,74 @@ def test_batched_prefill_is_deterministic(llrs, backend, tmp_path, n, ffn):
         for which in ("k", "v"):
             np.testing.assert_array_equal(kvs[0].layer(layer, which, n).view(np.uint32),
                                           kvs[1].layer(layer, which, n).view(np.uint32))
+
+
+def write_mixed_q4km(llrs, tmp_path, cfg, v_types, down_types):
+    """A GGUF laid out like llama.cpp's Q4_K_M files (src/loader.rs:437-441
+    keeps such files' tensors verbatim): Q4_K embeddings and q/k/o/gate/up,
+    a Q6_K LM head, and per layer the given attn_v / ffn_down types.  The
+    weights are the synthetic F32 model's, quantized on the host."""
+    from gguf_write import qwen2_metadata, write_gguf
+    from hf_checkpoint import gguf_names
+    f32 = tmp_path / "f32.gguf"
+    llrs.SynthConfig(**{**cfg.__dict__, "recipe": llrs.LoadQuantization.NONE}).write_gguf(f32)
+    QT = llrs.QuantType
+    tensors = []
+    for name in gguf_names(cfg.num_hidden_layers, tied=False):
+        _, t = llrs.gguf_read_tensor(f32, name)
+        rows, cols = t.shape if len(t.shape) == 2 else (1, t.shape[0])
+        vals = np.frombuffer(t.data, np.float32)
+        ty = None
+        if name.endswith("attn_v.weight"):
+            ty = v_types[int(name.split(".")[1])]
+        elif name.endswith("ffn_down.weight"):
+            ty = down_types[int(name.split(".")[1])]
+        elif name == "output.weight":
+            ty = QT.Q6K
+        elif name.endswith(".weight") and rows > 1:
+            ty = QT.Q4K
+        if ty is None:
+            tensors.append((name, 0, rows, cols, bytes(t.data)))
+        else:
+            q = llrs.QuantTensor.quantize(ty, vals, rows, cols)
+            tensors.append((name, int(q.quant_type), rows, cols, bytes(q.data)))
+    path = tmp_path / "mixed.gguf"
+    write_gguf(path, qwen2_metadata(cfg), tensors)
+    return path
+
+
+@pytest.mark.parametrize("hidden", [256, 512], ids=["hd64", "hd128"])
+def test_persistent_decode_per_layer_type_mix(llrs, backend, oracle, tmp_path, monkeypatch, hidden):
+    """Layers whose attn_v and ffn_down types differ (Q4_K / Q6_K / Q8_0 V,
+    Q4_K / Q6_K down) select the persistent kernel's per-layer instantiation;
+    it matches the oracle over 32 greedy steps and the launch-per-phase path
+    bit for bit."""
+    QT = llrs.QuantType
+    cfg = tiny_cfg(llrs, hidden_size=hidden, intermediate_size=768, num_hidden_layers=4, seed=47)
+    v = [QT.Q6K, QT.Q4K, QT.Q8_0, QT.Q6K]
+    down = [QT.Q6K, QT.Q4K, QT.Q4K, QT.Q6K]
+    path = write_mixed_q4km(llrs, tmp_path, cfg, v, down)
+    for l in range(4):
+        assert llrs.gguf_read_tensor(path, f"blk.{l}.attn_v.weight")[1].quant_type == v[l]
+        assert llrs.gguf_read_tensor(path, f"blk.{l}.ffn_down.weight")[1].quant_type == down[l]
+    model = llrs.ModelLoader.load_dynamic(path, backend)
+    kv = llrs.KVCache(model, 96)
+    assert kv.persistent
+    om = oracle.load(path)
+    om.new_state(96)
+    prompt = np.random.default_rng(47).integers(0, cfg.vocab_size, 24).astype(np.uint32)
+    model.prefill(prompt, 0, kv)
+    om.prefill(prompt, 0)
+    assert float(np.abs(kv.logits() - om.logits()).max()) <= LOGIT_TOL
+    got = model.decode_greedy(len(prompt), 32, kv)
+    want = om.decode_greedy(len(prompt), 32)
+    print(f"[mixed] tokens {got[:8].tolist()}...", flush=True)
+    np.testing.assert_array_equal(got, want)
+    assert float(np.abs(kv.logits() - om.logits()).max()) <= LOGIT_TOL
+    monkeypatch.setenv("LLRS_NO_PERSISTENT", "1")
+    kv_s = llrs.KVCache(model, 96)
+    monkeypatch.delenv("LLRS_NO_PERSISTENT")
+    assert not kv_s.persistent
+    model.prefill(prompt, 0, kv_s)
+    np.testing.assert_array_equal(model.decode_greedy(len(prompt), 32, kv_s), got)
+    np.testing.assert_array_equal(kv_s.logits(), kv.logits())
