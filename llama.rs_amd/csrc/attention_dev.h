@@ -72,8 +72,13 @@ __device__ __forceinline__ bool merge_wait_over(unsigned long long &t0, unsigned
 // stored at device scope.  qs and kn are the wave's own LDS (HD floats each).
 // MULTI: the instantiation for attention_span(pos) > 1 (the other one
 // assumes single-chunk items and keeps their code straight-line).
-template <int HD, bool COH, bool MULTI>
-__device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, float *qs, float *kn) {
+struct NoWait {
+  __device__ void operator()() const {}
+};
+
+template <int HD, bool COH, bool MULTI, bool EARLY = false, class Wait = NoWait>
+__device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, float *qs, float *kn,
+                               Wait &&wait = Wait{}) {
   constexpr int KH = HD / 2;              // dimensions per score lane
   constexpr int NK4 = KH / 4;             // their float4s
   constexpr int VW = HD >= 64 ? HD / 64 : 1;  // V floats per lane
@@ -102,13 +107,7 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
   const int ri = lane & (KH - 1);
   const float *cs = a.rope + (size_t)pos * HD, *sn = cs + KH;
   const float *qx = a.q + (size_t)h * HD, *kx = a.k + kvh * HD, *vx = a.v + kvh * HD;
-  //    (q, k and v are read with ordinary loads: no workgroup of the launch
-  //    reads them before they are written.)
-  const float q_re = qx[ri], q_im = qx[ri + KH];
-  const float k_re = kx[ri], k_im = kx[ri + KH];
-  const float rc = cs[ri], rs = sn[ri];
   const int vd = (lane % VL) * VW, vr0 = lane / VL;
-  const VT vnew = *reinterpret_cast<const VT *>(vx + vd);
   float4 kr[NK4];
   VT vv[NVI];
   auto load_rows = [&](int s0, int s1) {
@@ -121,7 +120,32 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
       vv[i] = *reinterpret_cast<const VT *>(vc + (size_t)(p < s1 ? p : s0) * kvw + vd);
     }
   };
-  load_rows(c0, min(c0 + kChunk, pos + 1));
+  // This step's query, key and value (ordinary loads: no workgroup of the
+  // launch reads them before they are written).
+  float q_re, q_im, k_re, k_im, rc, rs;
+  VT vnew;
+  auto load_new = [&] {
+    q_re = qx[ri];
+    q_im = qx[ri + KH];
+    k_re = kx[ri];
+    k_im = kx[ri + KH];
+    rc = cs[ri];
+    rs = sn[ri];
+    vnew = *reinterpret_cast<const VT *>(vx + vd);
+  };
+  if constexpr (EARLY) {
+    // The cache rows before this step's position were written by earlier
+    // steps, so their loads go out before the caller waits for this step's
+    // query, key and value (`wait`: the persistent kernel's barrier; the row
+    // at pos is taken from those, not from the cache).
+    load_rows(c0, min(c0 + kChunk, pos + 1));
+    wait();
+    load_new();
+  } else {
+    wait();
+    load_new();
+    load_rows(c0, min(c0 + kChunk, pos + 1));
+  }
 
   // 2. Rotated query and new key in LDS; the group's first head appends the
   //    new key and value to the cache.

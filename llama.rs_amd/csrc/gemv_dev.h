@@ -28,6 +28,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "gemv.h"
 #include "quant_dev.h"
@@ -464,14 +466,16 @@ __device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&em
 #pragma unroll
   for (int i = 0; i < R; i++) acc[i] = acc2[i] = 0.f;
   int g = 0, it = 0;  // the current step's row group and unit iteration
-  // One step on buffers (c, cu_) while the next step's loads go to (n, nu_).
-  auto step = [&](Raw (&c)[R], Raw (&cu_)[RU], Raw (&n)[R], Raw (&nu_)[RU]) {
+  // One step on buffers (c, cu_); when `more` (a compile-time flag, so the
+  // loads stay branch-free and their waits exact) the next step's loads go
+  // to (n, nu_) first.
+  auto step = [&](auto more, Raw (&c)[R], Raw (&cu_)[RU], Raw (&n)[R], Raw (&nu_)[RU]) {
     int gn = g, itn = it + 1;
     if (itn == iters) {
       itn = 0;
       gn = g + 1;
     }
-    load(gn, itn, n, nu_);  // past the last step: a clamped, unused reload
+    if constexpr (decltype(more)::value) load(gn, itn, n, nu_);
     const int u0 = it * 64 + lane;
     const int u = min(u0, units - 1);
     const int r0 = group_row(g);
@@ -517,10 +521,20 @@ __device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&em
     it = itn;
   };
   // Unrolled by two with the buffers swapping roles: no register copies, so
-  // the in-flight loads never have to be waited for early.
-  for (int s = 0; s < steps; s += 2) {
-    step(cur, cu, nxt, nu);
-    if (s + 1 < steps) step(nxt, nu, cur, cu);
+  // the in-flight loads never have to be waited for early.  The last step
+  // loads nothing (the phase's closing barrier would wait for such loads).
+  using More = std::true_type;
+  using Last = std::false_type;
+  int s = 0;
+  for (; s + 2 < steps; s += 2) {
+    step(More{}, cur, cu, nxt, nu);
+    step(More{}, nxt, nu, cur, cu);
+  }
+  if (s + 2 == steps) {
+    step(More{}, cur, cu, nxt, nu);
+    step(Last{}, nxt, nu, cur, cu);
+  } else if (s + 1 == steps) {
+    step(Last{}, cur, cu, nxt, nu);
   }
 }
 
