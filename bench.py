@@ -167,7 +167,10 @@ def projection_only(llrs, be, model, which: str, iters: int) -> int:
     return 0
 
 
-TUNED_TYPES = ("Q4K", "Q6K", "Q8_0", "Q5_0")  # types the tuned GEMV takes; the rest run generic
+# Types the tuned digit GEMV takes; F32/F16/BF16 run the vectorized float
+# GEMV (16-byte loads, rows sharing x), ragged shapes the wave-per-row one.
+TUNED_TYPES = ("Q4K", "Q5K", "Q6K", "Q8_0", "Q5_0", "Q4_0", "Q4_1", "Q5_1")
+FLOAT_TYPES = ("F32", "F16", "BF16")
 
 
 def gemv_sweep(llrs, be) -> int:
@@ -212,7 +215,7 @@ def gemv_sweep(llrs, be) -> int:
             del ts
         alg = nbytes + 4 * (rows + cols)
         rec = {"config": cfg, "type": ty.name, "rows": rows, "cols": cols, "weight_bytes": nbytes,
-               "kernel": "tuned" if ty.name in TUNED_TYPES else "generic", "launches": n,
+               "kernel": "tuned" if ty.name in TUNED_TYPES else "float" if ty.name in FLOAT_TYPES else "generic", "launches": n,
                "copies": copies, "us": round(dt * 1e6, 2), "gbs": round(alg / dt / 1e9, 1),
                "frac": round(alg / dt / 1e9 / PEAK_HBM_GBS, 4)}
         log(f"{cfg} {ty.name:5s} {rows:6d} x {cols:5d} {nbytes / 1e6:8.2f} MB {rec['kernel']:7s} "

@@ -86,6 +86,25 @@ __device__ __forceinline__ int block_dot(int q0, int q1, int q2, int q3, const u
 
 template <uint32_t TY> struct Traits;
 
+// scale_min_k4 (src/quant.rs:338-347) of groups 2p, 2p+1 of a K-quant
+// header (d, dmin, 12 scale bytes) as byte pairs: groups < 4 keep 6 bits of
+// scales[g] / scales[g+4]; groups >= 4 join the nibbles of scales[g+4] with
+// the top two bits of scales[g-4] / scales[g].  Both forms are computed and
+// blended by a lane mask (a branch would run both sides under exec masking).
+__device__ __forceinline__ void k4_scales(const uint4 &hdr, int p, uint32_t &sc, uint32_t &mn) {
+  const int sh = (p & 1) * 16;
+  const uint32_t Y = hdr.y >> sh, Z = hdr.z >> sh, W = hdr.w >> sh;
+  const uint32_t hi_g = 0u - (uint32_t)(p >> 1);  // all ones for groups >= 4
+  sc = ((Y & 0x3f3fu) & ~hi_g) | (((W & 0x0f0fu) | ((Y >> 2) & 0x3030u)) & hi_g);
+  mn = ((Z & 0x3f3fu) & ~hi_g) | ((((W >> 4) & 0x0f0fu) | ((Z >> 2) & 0x3030u)) & hi_g);
+}
+
+// Bits 0..3 of t -> bit 4 of bytes 0..3 (a Q5 block's high bits of four
+// consecutive weights).
+__device__ __forceinline__ uint32_t spread4(uint32_t t) {
+  return ((t & 15u) * 0x00204081u & 0x01010101u) << 4;
+}
+
 // Q4_K: unit u = block u/4, sub-block pair p = u%4 (groups 2p, 2p+1 = 64
 // weights, x-blocks 4u .. 4u+3).  y += d*sc_g * sum(q x) - dmin*m_g * sum(x).
 template <> struct Traits<LLRS_Q4_K> {
@@ -112,16 +131,8 @@ template <> struct Traits<LLRS_Q4_K> {
     const int p = u & 3;
     const float d = f16_bits_to_f32((uint16_t)(r.hdr.x & 0xffff));
     const float dmin = f16_bits_to_f32((uint16_t)(r.hdr.x >> 16));
-    // scale_min_k4 of groups 2p, 2p+1 (src/quant.rs:338-347) as byte pairs:
-    // groups < 4 keep 6 bits of scales[g] / scales[g+4]; groups >= 4 join the
-    // nibbles of scales[g+4] with the top two bits of scales[g-4] / scales[g].
-    const int sh = (p & 1) * 16;
-    const uint32_t Y = r.hdr.y >> sh, Z = r.hdr.z >> sh, W = r.hdr.w >> sh;
-    // Both forms, blended by a lane mask (a branch here would run both sides
-    // under exec masking anyway).
-    const uint32_t hi_g = 0u - (uint32_t)(p >> 1);  // all ones for groups >= 4
-    const uint32_t sc = ((Y & 0x3f3fu) & ~hi_g) | (((W & 0x0f0fu) | ((Y >> 2) & 0x3030u)) & hi_g);
-    const uint32_t mn = ((Z & 0x3f3fu) & ~hi_g) | ((((W >> 4) & 0x0f0fu) | ((Z >> 2) & 0x3030u)) & hi_g);
+    uint32_t sc, mn;
+    k4_scales(r.hdr, p, sc, mn);
     // Blocks: group 2p = low nibbles of q0 then q1, group 2p+1 = high nibbles.
     const uint32_t m4 = 0x0f0f0f0fu;
     const int a0 = block_dot(r.q0.x & m4, r.q0.y & m4, r.q0.z & m4, r.q0.w & m4, D.g[0]);
@@ -242,9 +253,6 @@ template <> struct Traits<LLRS_Q5_0> {
       D.sx[e] = L.sx[s];
     }
   }
-  static __device__ __forceinline__ uint32_t spread4(uint32_t t) {  // bits 0..3 -> bit 4 of bytes
-    return ((t & 15u) * 0x00204081u & 0x01010101u) << 4;
-  }
   static __device__ __forceinline__ float dot(const Raw &r, int, const Dig &D) {
     const uint32_t qh = __builtin_amdgcn_alignbyte(r.w[1], r.w[0], r.sh);
     int qa[4], qb[4];
@@ -258,6 +266,139 @@ template <> struct Traits<LLRS_Q5_0> {
     const int I0 = block_dot(qa[0], qa[1], qa[2], qa[3], D.g[0]) - 16 * D.sx[0];
     const int I1 = block_dot(qb[0], qb[1], qb[2], qb[3], D.g[1]) - 16 * D.sx[1];
     return f16_bits_to_f32(r.d) * ((float)I0 * D.xs[0] + (float)I1 * D.xs[1]);
+  }
+};
+
+// Q4_0: unit u = block u (32 weights): d, 16 bytes of nibbles (weight j < 16
+// the low nibble of byte j, weight 16 + j its high nibble); d * (q - 8).
+template <> struct Traits<LLRS_Q4_0> {
+  static constexpr int kColsPerUnit = 32;
+  struct Raw { uint32_t w[5]; uint32_t sh; uint16_t d; };
+  struct Dig { uint4 g[2][2]; float xs[2]; int sx[2]; };
+  static __device__ __forceinline__ void load(const uint8_t *row, int u, Raw &r) {
+    const uint8_t *blk = row + (size_t)u * 18;
+    r.sh = (uint32_t)(reinterpret_cast<uintptr_t>(blk + 2) & 3);
+    const uint32_t *base = reinterpret_cast<const uint32_t *>(blk + 2 - r.sh);
+    u32x4a4 v0 = *reinterpret_cast<const u32x4a4 *>(base);
+    r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
+    r.w[4] = base[4];
+    r.d = ld_u16(blk);
+  }
+  static __device__ __forceinline__ void digits(const Lds &L, int u, Dig &D) {
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      int s = slot(2 * u + e, L.nb4);
+      dig_block(L, 2 * u + e, D.g[e]);
+      D.xs[e] = L.xs[s];
+      D.sx[e] = L.sx[s];
+    }
+  }
+  static __device__ __forceinline__ float dot(const Raw &r, int, const Dig &D) {
+    const uint32_t m4 = 0x0f0f0f0fu;
+    int qa[4], qb[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t v = __builtin_amdgcn_alignbyte(r.w[k + 1], r.w[k], r.sh);
+      qa[k] = (int)(v & m4);
+      qb[k] = (int)((v >> 4) & m4);
+    }
+    const int I0 = block_dot(qa[0], qa[1], qa[2], qa[3], D.g[0]) - 8 * D.sx[0];
+    const int I1 = block_dot(qb[0], qb[1], qb[2], qb[3], D.g[1]) - 8 * D.sx[1];
+    return f16_bits_to_f32(r.d) * ((float)I0 * D.xs[0] + (float)I1 * D.xs[1]);
+  }
+};
+
+// Q4_1 (20-byte blocks) and Q5_1 (24): unit u = block u (32 weights): d, m,
+// for Q5_1 32 high bits, then 16 bytes of nibbles; d * q + m.  The blocks and
+// so the rows are 4-byte aligned: fields load as dwords.
+template <uint32_t TY> struct TraitsQx1 {
+  static constexpr bool kQ5 = TY == LLRS_Q5_1;
+  static constexpr int kColsPerUnit = 32, kBytes = kQ5 ? 24 : 20;
+  struct Raw { uint32_t dm, qh, q[4]; };
+  struct Dig { uint4 g[2][2]; float xs[2]; float xsum; };
+  static __device__ __forceinline__ void load(const uint8_t *row, int u, Raw &r) {
+    const uint32_t *blk = reinterpret_cast<const uint32_t *>(row + (size_t)u * kBytes);
+    r.dm = blk[0];
+    r.qh = kQ5 ? blk[1] : 0u;
+    u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(blk + (kQ5 ? 2 : 1));
+    r.q[0] = v.x; r.q[1] = v.y; r.q[2] = v.z; r.q[3] = v.w;
+  }
+  static __device__ __forceinline__ void digits(const Lds &L, int u, Dig &D) {
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      dig_block(L, 2 * u + e, D.g[e]);
+      D.xs[e] = L.xs[slot(2 * u + e, L.nb4)];
+    }
+    D.xsum = L.xsum32[u];
+  }
+  static __device__ __forceinline__ float dot(const Raw &r, int, const Dig &D) {
+    const uint32_t m4 = 0x0f0f0f0fu;
+    int qa[4], qb[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      qa[k] = (int)(r.q[k] & m4);
+      qb[k] = (int)((r.q[k] >> 4) & m4);
+      if constexpr (kQ5) {
+        qa[k] |= (int)spread4(r.qh >> (4 * k));
+        qb[k] |= (int)spread4(r.qh >> (16 + 4 * k));
+      }
+    }
+    const int I0 = block_dot(qa[0], qa[1], qa[2], qa[3], D.g[0]);
+    const int I1 = block_dot(qb[0], qb[1], qb[2], qb[3], D.g[1]);
+    const float d = f16_bits_to_f32((uint16_t)(r.dm & 0xffff));
+    const float m = f16_bits_to_f32((uint16_t)(r.dm >> 16));
+    return d * ((float)I0 * D.xs[0] + (float)I1 * D.xs[1]) + m * D.xsum;
+  }
+};
+template <> struct Traits<LLRS_Q4_1> : TraitsQx1<LLRS_Q4_1> {};
+template <> struct Traits<LLRS_Q5_1> : TraitsQx1<LLRS_Q5_1> {};
+
+// Q5_K: as Q4_K with a plane of high bits: qh byte l holds bit g of weight l
+// of group g.  Unit u = block u/4, pair p = u%4: the pair's 32 nibble bytes
+// and all 32 qh bytes (both groups' bits).
+template <> struct Traits<LLRS_Q5_K> {
+  static constexpr int kColsPerUnit = 64;
+  struct Raw { uint4 hdr, q0, q1, h0, h1; };
+  struct Dig { uint4 g[4][2]; float xs[4]; float xsum[2]; };
+  static __device__ __forceinline__ void load(const uint8_t *row, int u, Raw &r) {
+    const uint8_t *blk = row + (size_t)(u >> 2) * 176;
+    const int p = u & 3;
+    r.hdr = *reinterpret_cast<const uint4 *>(blk);
+    r.h0 = *reinterpret_cast<const uint4 *>(blk + 16);
+    r.h1 = *reinterpret_cast<const uint4 *>(blk + 32);
+    r.q0 = *reinterpret_cast<const uint4 *>(blk + 48 + p * 32);
+    r.q1 = *reinterpret_cast<const uint4 *>(blk + 64 + p * 32);
+  }
+  static __device__ __forceinline__ void digits(const Lds &L, int u, Dig &D) {
+    Traits<LLRS_Q4_K>::Dig d4;
+    Traits<LLRS_Q4_K>::digits(L, u, d4);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      D.g[j][0] = d4.g[j][0];
+      D.g[j][1] = d4.g[j][1];
+      D.xs[j] = d4.xs[j];
+    }
+    D.xsum[0] = d4.xsum[0];
+    D.xsum[1] = d4.xsum[1];
+  }
+  static __device__ __forceinline__ float dot(const Raw &r, int u, const Dig &D) {
+    const int p = u & 3, ga = 2 * p, gb = 2 * p + 1;
+    const float d = f16_bits_to_f32((uint16_t)(r.hdr.x & 0xffff));
+    const float dmin = f16_bits_to_f32((uint16_t)(r.hdr.x >> 16));
+    uint32_t sc, mn;
+    k4_scales(r.hdr, p, sc, mn);
+    const uint32_t m4 = 0x0f0f0f0fu, b1 = 0x01010101u;
+    auto lo = [&](uint32_t q, uint32_t h) { return (int)((q & m4) | (((h >> ga) & b1) << 4)); };
+    auto hi = [&](uint32_t q, uint32_t h) { return (int)(((q >> 4) & m4) | (((h >> gb) & b1) << 4)); };
+    const int a0 = block_dot(lo(r.q0.x, r.h0.x), lo(r.q0.y, r.h0.y), lo(r.q0.z, r.h0.z), lo(r.q0.w, r.h0.w), D.g[0]);
+    const int a1 = block_dot(lo(r.q1.x, r.h1.x), lo(r.q1.y, r.h1.y), lo(r.q1.z, r.h1.z), lo(r.q1.w, r.h1.w), D.g[1]);
+    const int a2 = block_dot(hi(r.q0.x, r.h0.x), hi(r.q0.y, r.h0.y), hi(r.q0.z, r.h0.z), hi(r.q0.w, r.h0.w), D.g[2]);
+    const int a3 = block_dot(hi(r.q1.x, r.h1.x), hi(r.q1.y, r.h1.y), hi(r.q1.z, r.h1.z), hi(r.q1.w, r.h1.w), D.g[3]);
+    const float s0 = (float)a0 * D.xs[0] + (float)a1 * D.xs[1];
+    const float s1 = (float)a2 * D.xs[2] + (float)a3 * D.xs[3];
+    const float t = (float)(sc & 0xff) * s0 + (float)(sc >> 8) * s1;
+    const float m = (float)(mn & 0xff) * D.xsum[0] + (float)(mn >> 8) * D.xsum[1];
+    return d * t - dmin * m;
   }
 };
 
@@ -406,6 +547,7 @@ __device__ __forceinline__ float wave_sum2(float v0, float v1, int lane) {
 // loads in registers); dual gate/up steps hold two rows of each matrix.
 template <uint32_t TY, bool DUAL> struct RowsPerStep { static constexpr int value = DUAL ? 2 : 4; };
 template <> struct RowsPerStep<LLRS_Q6_K, false> { static constexpr int value = 2; };
+template <> struct RowsPerStep<LLRS_Q5_K, false> { static constexpr int value = 2; };
 
 // All dots of this wave's rows of one segment (and of `U` for SwiGLU),
 // streamed as (row group, unit-iteration) steps whose raw loads run one step

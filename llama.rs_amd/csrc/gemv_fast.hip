@@ -34,8 +34,8 @@ size_t fast_gemv_lds_bytes(const FastGemvArgs &a, int grid) {
 bool fast_gemv_supports(uint32_t type, size_t cols) {
   if (cols == 0 || cols % 64 || cols > 24576) return false;
   switch (type) {
-    case LLRS_Q4_K: case LLRS_Q6_K: return cols % 256 == 0;
-    case LLRS_Q8_0: case LLRS_Q5_0: return true;
+    case LLRS_Q4_K: case LLRS_Q5_K: case LLRS_Q6_K: return cols % 256 == 0;
+    case LLRS_Q8_0: case LLRS_Q5_0: case LLRS_Q4_0: case LLRS_Q4_1: case LLRS_Q5_1: return true;
     default: return false;
   }
 }
@@ -66,6 +66,7 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
     return LLRS_OK;                               \
   }
     DUAL1(LLRS_Q4_K) DUAL1(LLRS_Q5_0) DUAL1(LLRS_Q8_0) DUAL1(LLRS_Q6_K)
+    DUAL1(LLRS_Q4_0) DUAL1(LLRS_Q4_1) DUAL1(LLRS_Q5_1) DUAL1(LLRS_Q5_K)
 #undef DUAL1
   }
 #define PAIR(A, B)                                 \
@@ -77,6 +78,8 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
   PAIR(LLRS_Q4_K, LLRS_Q4_K) PAIR(LLRS_Q6_K, LLRS_Q6_K) PAIR(LLRS_Q8_0, LLRS_Q8_0)
   PAIR(LLRS_Q5_0, LLRS_Q5_0) PAIR(LLRS_Q4_K, LLRS_Q8_0) PAIR(LLRS_Q5_0, LLRS_Q8_0)
   PAIR(LLRS_Q4_K, LLRS_Q6_K) PAIR(LLRS_Q4_K, LLRS_Q5_0)
+  PAIR(LLRS_Q4_0, LLRS_Q4_0) PAIR(LLRS_Q4_1, LLRS_Q4_1) PAIR(LLRS_Q5_1, LLRS_Q5_1)
+  PAIR(LLRS_Q5_K, LLRS_Q5_K)
 #undef PAIR
   return set_error(LLRS_E_UNSUPPORTED, "no tuned GEMV for %s + %s", type_name(ta), type_name(tb));
 }
@@ -93,7 +96,8 @@ int fast_gemv_grid(int cu_count, int rows, int cols, bool dual, int part) {
 
 bool fast_gemv_supports_pair(uint32_t ta, uint32_t tb) {
   auto ok = [](uint32_t a, uint32_t b) {
-    return (a == b && (a == LLRS_Q4_K || a == LLRS_Q6_K || a == LLRS_Q8_0 || a == LLRS_Q5_0)) ||
+    return (a == b && (a == LLRS_Q4_K || a == LLRS_Q6_K || a == LLRS_Q8_0 || a == LLRS_Q5_0 ||
+                       a == LLRS_Q4_0 || a == LLRS_Q4_1 || a == LLRS_Q5_1 || a == LLRS_Q5_K)) ||
            (a == LLRS_Q4_K && (b == LLRS_Q8_0 || b == LLRS_Q6_K || b == LLRS_Q5_0)) ||
            (a == LLRS_Q5_0 && b == LLRS_Q8_0);
   };

@@ -177,6 +177,64 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t *__rest
   }
 }
 
+// F32 / F16 / BF16 rows whose length is a multiple of one 16-byte load
+// (4 or 8 elements): each wave owns R consecutive rows, its lanes take the
+// row's 16-byte chunks l, l + 64, ..., and every chunk of x (read once per
+// wave from L2) serves the R rows.  The loop is unrolled so that several
+// chunks' loads are in flight per lane.
+template <uint32_t TY, int R>
+__global__ __launch_bounds__(256) void gemv_float_kernel(const uint8_t *__restrict__ W, size_t row_bytes,
+                                                         int rows, int cols, const float *__restrict__ x,
+                                                         float *__restrict__ y,
+                                                         const float *__restrict__ bias, int accumulate) {
+  constexpr int E = TY == LLRS_F32 ? 4 : 8;  // elements per 16-byte load
+  const int lane = threadIdx.x & 63;
+  const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  if (r0 >= rows) return;
+  const int chunks = cols / E;
+  float acc[R];
+#pragma unroll
+  for (int i = 0; i < R; i++) acc[i] = 0.f;
+#pragma unroll 4
+  for (int c = lane; c < chunks; c += 64) {
+    uint4 w[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      const int r = min(r0 + i, rows - 1);  // rows past the end: a valid read, not stored
+      w[i] = *reinterpret_cast<const uint4 *>(W + (size_t)r * row_bytes + (size_t)c * 16);
+    }
+    float xv[E];
+#pragma unroll
+    for (int k = 0; k < E / 4; k++) {
+      const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)c * E + 4 * k);
+      xv[4 * k] = v.x;
+      xv[4 * k + 1] = v.y;
+      xv[4 * k + 2] = v.z;
+      xv[4 * k + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+      for (int e = 0; e < E; e++) {
+        float wv;
+        if constexpr (TY == LLRS_F32) wv = __uint_as_float(u[e]);
+        else if constexpr (TY == LLRS_F16) wv = f16_bits_to_f32((uint16_t)(u[e >> 1] >> (16 * (e & 1))));
+        else wv = bf16_bits_to_f32((uint16_t)(u[e >> 1] >> (16 * (e & 1))));
+        acc[i] += wv * xv[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const float a = wave_sum(acc[i]);
+    if (lane == 0 && r0 + i < rows) {
+      const float v = bias ? a + bias[r0 + i] : a;
+      y[r0 + i] = accumulate ? y[r0 + i] + v : v;
+    }
+  }
+}
+
 __global__ void dequant_row_kernel(const uint8_t *__restrict__ row, uint32_t ty, int cols,
                                    float *__restrict__ out) {
   int c = blockIdx.x * blockDim.x + threadIdx.x;
@@ -189,6 +247,31 @@ int launch_gemv_generic(const llrs_tensor *w, const float *x, float *y, const fl
   dim3 grid((unsigned)((w->rows + 3) / 4)), block(256);
   int rows = (int)w->rows, cols = (int)w->cols;
   int acc = accumulate ? 1 : 0;
+  const bool is_float = w->type == LLRS_F32 || w->type == LLRS_F16 || w->type == LLRS_BF16;
+  const int per_load = w->type == LLRS_F32 ? 4 : 8;
+  if (is_float && cols % per_load == 0 && w->row_bytes % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(w->dev) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+    // Four rows per wave for tall matrices; one otherwise, so that short
+    // wide ones still spread over the whole chip.
+    const bool four = rows >= 8192;
+    const dim3 g((unsigned)((rows + (four ? 15 : 3)) / (four ? 16 : 4)));
+#define F(T)                                                                                         \
+  case T:                                                                                            \
+    if (four)                                                                                        \
+      hipLaunchKernelGGL((gemv_float_kernel<T, 4>), g, block, 0, s, w->dev, w->row_bytes, rows, cols, \
+                         x, y, bias, acc);                                                           \
+    else                                                                                             \
+      hipLaunchKernelGGL((gemv_float_kernel<T, 1>), g, block, 0, s, w->dev, w->row_bytes, rows, cols, \
+                         x, y, bias, acc);                                                           \
+    break;
+    switch (w->type) {
+      F(LLRS_F32) F(LLRS_F16) F(LLRS_BF16)
+      default: break;
+    }
+#undef F
+    LLRS_HIP(hipGetLastError());
+    return LLRS_OK;
+  }
 #define L(T)                                                                                    \
   case T:                                                                                       \
     hipLaunchKernelGGL(gemv_generic_kernel<T>, grid, block, 0, s, w->dev, w->row_bytes, rows, \
