@@ -543,6 +543,29 @@ __device__ __forceinline__ float wave_sum2(float v0, float v1, int lane) {
   return k;
 }
 
+// The same within each 32-lane half of the wave (packed rows): half_sum4
+// returns the half's total of v[(lane >> 3) & 3], half_sum2 of
+// v[(lane >> 4) & 1].
+__device__ __forceinline__ float half_sum4(const float (&v)[4], int lane) {
+  bool a = lane & 16;
+  float s0 = a ? v[0] : v[2], s1 = a ? v[1] : v[3];
+  float k0 = a ? v[2] : v[0], k1 = a ? v[3] : v[1];
+  k0 += __shfl_xor(s0, 16, 64);
+  k1 += __shfl_xor(s1, 16, 64);
+  bool b = lane & 8;
+  float k = (b ? k1 : k0) + __shfl_xor(b ? k0 : k1, 8, 64);
+#pragma unroll
+  for (int o = 4; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
+  return k;
+}
+__device__ __forceinline__ float half_sum2(float v0, float v1, int lane) {
+  bool a = lane & 16;
+  float k = (a ? v1 : v0) + __shfl_xor(a ? v0 : v1, 16, 64);
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
+  return k;
+}
+
 // Rows per wave step for a type (kept small enough to double-buffer the raw
 // loads in registers); dual gate/up steps hold two rows of each matrix.
 template <uint32_t TY, bool DUAL> struct RowsPerStep { static constexpr int value = DUAL ? 2 : 4; };
@@ -555,23 +578,32 @@ template <> struct RowsPerStep<LLRS_Q5_K, false> { static constexpr int value = 
 // stride) * R.  begin() issues the first step's loads (it may run before
 // the activation digits exist); run() streams the rest; `emit(row_in_range,
 // y, y_up)` runs in one lane per row.
+//
+// Packed rows: when a row has at most 32 units (e.g. 1,536 columns of Q4_K,
+// 24 units), a group is 2R rows and each 32-lane half of the wave takes R of
+// them, lane & 31 being the unit: twice the rows per step, at the same
+// registers, where otherwise most lanes would idle.
 template <uint32_t TY, bool DUAL>
 struct SegStream {
   using T = Traits<TY>;
   static constexpr int R = RowsPerStep<TY, DUAL>::value;
   FastSeg S, U;
-  int row_lo, row_hi, first, stride, units, iters, steps, lane;
+  int row_lo, row_hi, first, stride, units, iters, steps, lane, gsz;
+  bool packed;
   typename T::Raw cur[R], nxt[R], cu[DUAL ? R : 1], nu[DUAL ? R : 1];
 
-  // First row of this wave's g-th row group.
-  __device__ __forceinline__ int group_row(int g) const { return row_lo + (first + g * stride) * R; }
+  // First row of this wave's g-th row group (of gsz rows: R, or 2R packed).
+  __device__ __forceinline__ int group_row(int g) const { return row_lo + (first + g * stride) * gsz; }
+  // First row of this lane's part of group g, and its unit at iteration it.
+  __device__ __forceinline__ int lane_row(int g) const { return group_row(g) + (packed ? (lane >> 5) * R : 0); }
+  __device__ __forceinline__ int lane_unit(int it) const { return packed ? (lane & 31) : it * 64 + lane; }
   // Loads are branch-free (indices past the segment are clamped onto its last
   // row and unit and their products discarded), so the compiler can count the
   // outstanding loads statically and wait only for the current step's.
   __device__ __forceinline__ void load(int g, int it, typename T::Raw (&dst)[R],
                                        typename T::Raw (&dstu)[DUAL ? R : 1]) {
-    const int u = min(it * 64 + lane, units - 1);
-    const int r0 = group_row(g);
+    const int u = min(lane_unit(it), units - 1);
+    const int r0 = lane_row(g);
 #pragma unroll
     for (int i = 0; i < R; i++) {
       const int r = min(r0 + i, row_hi - 1) - row_lo;
@@ -589,8 +621,10 @@ struct SegStream {
     stride = stride_;
     lane = lane_;
     units = cols / T::kColsPerUnit;
-    iters = (units + 63) / 64;
-    const int ngroups = (row_hi - row_lo + R - 1) / R;
+    packed = units <= 32;
+    iters = packed ? 1 : (units + 63) / 64;
+    gsz = packed ? 2 * R : R;
+    const int ngroups = (row_hi - row_lo + gsz - 1) / gsz;
     int nmine = first < ngroups ? (ngroups - first + stride - 1) / stride : 0;
     steps = __builtin_amdgcn_readfirstlane(nmine) * iters;
     if (steps > 0) load(0, 0, cur, cu);
@@ -618,9 +652,9 @@ __device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&em
       gn = g + 1;
     }
     if constexpr (decltype(more)::value) load(gn, itn, n, nu_);
-    const int u0 = it * 64 + lane;
+    const int u0 = lane_unit(it);
     const int u = min(u0, units - 1);
-    const int r0 = group_row(g);
+    const int r0 = lane_row(g);
     typename T::Dig D;
     T::digits(L, u, D);
 #pragma unroll
@@ -633,7 +667,32 @@ __device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&em
         acc2[i] += live ? d2 : 0.f;
       }
     }
-    if (itn == 0) {  // the row group is complete
+    if (itn == 0 && packed) {  // the row group is complete: per-half sums
+      if constexpr (DUAL) {
+        // gate rows 0, 1 in lane groups 0/8, up rows in 16/24 of each half.
+        float v[4] = {acc[0], acc[1], acc2[0], acc2[1]};
+        float t = half_sum4(v, lane);
+        float up = __shfl_xor(t, 16, 64);
+        if ((lane & 23) == 0) {  // lanes 0, 8, 32, 40
+          int r = r0 + ((lane >> 3) & 1);
+          if (r < row_hi) emit(r - row_lo, t, up);
+        }
+      } else if constexpr (R == 4) {
+        float t = half_sum4(acc, lane);
+        if ((lane & 7) == 0) {
+          int r = r0 + ((lane >> 3) & 3);
+          if (r < row_hi) emit(r - row_lo, t, 0.f);
+        }
+      } else {
+        float t = half_sum2(acc[0], acc[1], lane);
+        if ((lane & 15) == 0) {
+          int r = r0 + ((lane >> 4) & 1);
+          if (r < row_hi) emit(r - row_lo, t, 0.f);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < R; i++) acc[i] = acc2[i] = 0.f;
+    } else if (itn == 0) {  // the row group is complete
       if constexpr (DUAL) {
         // rows 0, 1 of gate and of up: gate sums land in lanes 0/16, up in 32/48.
         float v[4] = {acc[0], acc[1], acc2[0], acc2[1]};
