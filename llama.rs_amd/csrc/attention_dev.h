@@ -22,10 +22,10 @@ __device__ __forceinline__ int bounded_pos(const int *pos, int max_seq) {
 
 // ------------------------------------------------------------------ attention
 //
-// One wave per (query head, item of attention_span(pos) consecutive chunks
-// of kChunk positions: one chunk up to 2,048 positions); items past the
-// current position exit at once, so one grid (sized for the whole context)
-// serves every position of a captured graph.  Per chunk: split-half RoPE
+// One wave per (query head, item of attention_span(pos, nh) consecutive
+// chunks of kChunk positions: one chunk while every head's items fit the
+// wave slots); items past the current position exit at once, so one grid
+// (sized for the whole context) serves every position of a captured graph.  Per chunk: split-half RoPE
 // (src/model.rs:87-95) on the head's query, scores q.k * 1/sqrt(hd), softmax
 // partials (max, sum of exp) and exp-weighted V sums (src/model.rs:206-231,
 // softmax_inplace 298-313).  The chunk holding the current position also
@@ -40,7 +40,8 @@ __device__ __forceinline__ int bounded_pos(const int *pos, int max_seq) {
 // holding the current position) computes its own partial, then reads the
 // others' until every tag is this step's, and folds them with the running-max
 // rescaling of flash decoding.  One round trip on the merging path, none on
-// the others, no cache write-back.  A chunk whose scores are all -inf
+// the others, no cache write-back.  A head of more than kGroupFrom items
+// merges in two levels (groups of kGroup, see step 5 below).  A chunk whose scores are all -inf
 // contributes exp(-inf) = 0; without a finite positive total the weights fall
 // back to uniform, as softmax_inplace does.
 
@@ -70,7 +71,7 @@ __device__ __forceinline__ bool merge_wait_over(unsigned long long &t0, unsigned
 // One (query head, chunk) item, run by one wave.  COH: the output is read by
 // other workgroups of the same launch (the persistent decode kernel), so it is
 // stored at device scope.  qs and kn are the wave's own LDS (HD floats each).
-// MULTI: the instantiation for attention_span(pos) > 1 (the other one
+// MULTI: the instantiation for attention_span(pos, nh) > 1 (the other one
 // assumes single-chunk items and keeps their code straight-line).
 struct NoWait {
   __device__ void operator()() const {}
@@ -90,7 +91,7 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
 
   const int G = a.nh / a.nkv, kvw = a.nkv * HD;
   const int kvh = h / G;
-  const int S = MULTI ? attention_span(pos) : 1, span = S * kChunk;
+  const int S = MULTI ? attention_span(pos, a.nh) : 1, span = S * kChunk;
   const int c0 = chunk * span;  // this item: positions [c0, c0 + span), S sub-chunks
   if (c0 > pos) return;
   const int n_active = pos / span + 1;  // items of the head
@@ -264,97 +265,121 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
   }
 
   // 5. Every chunk but the last publishes [HD] O sums, [HD] V sums, max, sum.
+  //    Past kGroupFrom items a head merges in two levels: the last item of
+  //    each group of kGroup chunks also folds its group's other partials into
+  //    a group partial (slot max_chunks + group), and the head's last item
+  //    folds its own group's partials, then the group partials.
   const long stride = a.part_stride;
-  unsigned long long *const base = a.scratch + (size_t)h * a.max_chunks * stride;
+  unsigned long long *const base =
+      a.scratch + (size_t)h * (size_t)(a.max_chunks + attention_groups(a.max_chunks)) * stride;
+  unsigned long long *const gbase = base + (size_t)a.max_chunks * stride;
   const unsigned tag = a.tag;
-  if (chunk != n_active - 1) {
-    unsigned long long *part = base + (size_t)chunk * stride;
+  const bool last = chunk == n_active - 1;
+  const bool grouped = n_active > kGroupFrom;
+  const int grp = chunk / kGroup;
+  const bool leader = grouped && !last && chunk % kGroup == kGroup - 1;
+  auto publish = [&](unsigned long long *part, float mv, float lv, const float (&o)[VW], const float (&vsum)[VW]) {
     if (lane < VL) {
 #pragma unroll
       for (int k = 0; k < VW; k++) {
-        store_tagged(part + vd + k, O[k], tag);
-        store_tagged(part + HD + vd + k, Vs[k], tag);
+        store_tagged(part + vd + k, o[k], tag);
+        store_tagged(part + HD + vd + k, vsum[k], tag);
       }
     }
     if (lane == 0) {
-      store_tagged(part + 2 * HD, m, tag);
-      store_tagged(part + 2 * HD + 1, l, tag);
+      store_tagged(part + 2 * HD, mv, tag);
+      store_tagged(part + 2 * HD + 1, lv, tag);
     }
-    return;
+  };
+  if (!last) {
+    publish(base + (size_t)chunk * stride, m, l, O, Vs);
+    if (!leader) return;
   }
 
-  // 6. Merge (the last chunk), starting from its own partial.  The others'
-  //    statistics one per lane (64 chunks a round) load together with their
-  //    first OB O partials; a load round is repeated until every tag is this
-  //    step's.  The round's max by wave reduction, each chunk's weight
-  //    exp(m_c - M) in its lane, broadcast by readlane to weight the O
-  //    partials.  Rounds fold with the running-max rescaling; a chunk whose
+  // 6. Merge, starting from the own partial.  Partials `first .. first + n`
+  //    of `slots`: their statistics one per lane (64 a round) load together
+  //    with their first OB O partials; a load round is repeated until every
+  //    tag is this step's.  The round's max by wave reduction, each partial's
+  //    weight exp(m_c - M) in its lane, broadcast by readlane to weight the O
+  //    partials.  Rounds fold with the running-max rescaling; a partial whose
   //    max is -inf weighs 0.
   constexpr int OB = 32 / VW;  // O partials per load round
-  const int np = n_active - 1;
   float M = m, L = l, R[VW];
 #pragma unroll
   for (int k = 0; k < VW; k++) R[k] = O[k];
   unsigned long long t0 = 0;
-  for (int cb = 0; cb < np; cb += 64) {
-    const int nc = min(64, np - cb);
-    float ov[OB][VW], mm, ll;
-    const unsigned long long *pcl = base + (size_t)(cb + min(lane, nc - 1)) * stride;
-    while (true) {
-      bool ok = true;
+  const int g0 = grouped ? grp * kGroup : 0;  // the first chunk partial this item folds
+  // Level 0: chunk partials g0 .. chunk - 1 (the leader then publishes the
+  // group partial and returns); level 1 (the head's last item when grouped):
+  // group partials 0 .. grp - 1.  One loop, so the merge code exists once.
+  for (int level = 0; level < (grouped && !leader ? 2 : 1); level++) {
+    const unsigned long long *slots = level ? gbase : base + (size_t)g0 * stride;
+    const int np = level ? grp : chunk - g0;
+    for (int cb = 0; cb < np; cb += 64) {
+      const int nc = min(64, np - cb);
+      float ov[OB][VW], mm, ll;
+      const unsigned long long *pcl = slots + (size_t)(cb + min(lane, nc - 1)) * stride;
+      while (true) {
+        bool ok = true;
 #pragma unroll
-      for (int j = 0; j < OB; j++) {
-        const unsigned long long *pc = base + (size_t)(cb + min(j, nc - 1)) * stride + vd;
+        for (int j = 0; j < OB; j++) {
+          const unsigned long long *pc = slots + (size_t)(cb + min(j, nc - 1)) * stride + vd;
 #pragma unroll
-        for (int k = 0; k < VW; k++) ov[j][k] = load_tagged(pc + k, tag, ok);
+          for (int k = 0; k < VW; k++) ov[j][k] = load_tagged(pc + k, tag, ok);
+        }
+        mm = load_tagged(pcl + 2 * HD, tag, ok);
+        ll = load_tagged(pcl + 2 * HD + 1, tag, ok);
+        if (__all(ok) || merge_wait_over(t0, a.err)) break;
+        __builtin_amdgcn_s_sleep(1);
       }
-      mm = load_tagged(pcl + 2 * HD, tag, ok);
-      ll = load_tagged(pcl + 2 * HD + 1, tag, ok);
-      if (__all(ok) || merge_wait_over(t0, a.err)) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-    const bool in = lane < nc && mm != -INFINITY;
-    float Mr = in ? mm : -INFINITY;
+      const bool in = lane < nc && mm != -INFINITY;
+      float Mr = in ? mm : -INFINITY;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) Mr = fmaxf(Mr, __shfl_xor(Mr, o, 64));
-    const float w = in ? expf(mm - Mr) : 0.f;
-    float Lr = w * ll;
+      for (int o = 32; o > 0; o >>= 1) Mr = fmaxf(Mr, __shfl_xor(Mr, o, 64));
+      const float w = in ? expf(mm - Mr) : 0.f;
+      float Lr = w * ll;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) Lr += __shfl_xor(Lr, o, 64);
-    float Rr[VW];
+      for (int o = 32; o > 0; o >>= 1) Lr += __shfl_xor(Lr, o, 64);
+      float Rr[VW];
 #pragma unroll
-    for (int k = 0; k < VW; k++) Rr[k] = 0.f;
-    for (int jb = 0; jb < nc; jb += OB) {
-      if (jb > 0) {
-        while (true) {
-          bool ok = true;
+      for (int k = 0; k < VW; k++) Rr[k] = 0.f;
+      for (int jb = 0; jb < nc; jb += OB) {
+        if (jb > 0) {
+          while (true) {
+            bool ok = true;
 #pragma unroll
-          for (int j = 0; j < OB; j++) {
-            const unsigned long long *pc = base + (size_t)(cb + min(jb + j, nc - 1)) * stride + vd;
+            for (int j = 0; j < OB; j++) {
+              const unsigned long long *pc = slots + (size_t)(cb + min(jb + j, nc - 1)) * stride + vd;
 #pragma unroll
-            for (int k = 0; k < VW; k++) ov[j][k] = load_tagged(pc + k, tag, ok);
+              for (int k = 0; k < VW; k++) ov[j][k] = load_tagged(pc + k, tag, ok);
+            }
+            if (__all(ok) || merge_wait_over(t0, a.err)) break;
+            __builtin_amdgcn_s_sleep(1);
           }
-          if (__all(ok) || merge_wait_over(t0, a.err)) break;
-          __builtin_amdgcn_s_sleep(1);
+        }
+#pragma unroll
+        for (int j = 0; j < OB; j++) {
+          if (jb + j >= nc) break;
+          const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jb + j));
+#pragma unroll
+          for (int k = 0; k < VW; k++) Rr[k] += wj * ov[j][k];
         }
       }
+      if (Mr != -INFINITY) {
+        const float Mn = fmaxf(M, Mr);
+        const float sa = M == -INFINITY ? 0.f : expf(M - Mn), sb = expf(Mr - Mn);
+        L = L * sa + Lr * sb;
 #pragma unroll
-      for (int j = 0; j < OB; j++) {
-        if (jb + j >= nc) break;
-        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jb + j));
-#pragma unroll
-        for (int k = 0; k < VW; k++) Rr[k] += wj * ov[j][k];
+        for (int k = 0; k < VW; k++) R[k] = R[k] * sa + Rr[k] * sb;
+        M = Mn;
       }
     }
-    if (Mr != -INFINITY) {
-      const float Mn = fmaxf(M, Mr);
-      const float sa = M == -INFINITY ? 0.f : expf(M - Mn), sb = expf(Mr - Mn);
-      L = L * sa + Lr * sb;
-#pragma unroll
-      for (int k = 0; k < VW; k++) R[k] = R[k] * sa + Rr[k] * sb;
-      M = Mn;
-    }
   }
+  if (leader) {  // the group partial; the V sums stay in the chunk slots
+    publish(gbase + (size_t)grp * stride, M, L, R, Vs);
+    return;
+  }
+  const int np = n_active - 1;  // the chunk partials (the uniform fallback reads their V sums)
   if (lane < VL) {
     if (isfinite(L) && L > 0.f) {
 #pragma unroll

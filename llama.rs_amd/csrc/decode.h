@@ -9,14 +9,22 @@ namespace llrs {
 
 // Decode attention items.
 constexpr int kChunk = 32;  // positions per wave: lane = (half of the head, position)
-// Sub-chunks per attention item at position pos: one up to kMaxParts
-// chunks, then as many as keep a head's partials at most kMaxParts, so that
-// the merge reads at most kMaxParts partials however long the context.
-constexpr int kMaxParts = 64;
-__host__ __device__ inline int attention_span(int pos) {
-  const int n = pos / kChunk + 1;
-  return (n + kMaxParts - 1) / kMaxParts;
+// Sub-chunks per attention item at position pos for nh query heads: one
+// while the items of all heads fit kItemSlots (the persistent kernel's 256
+// workgroups x 8 waves on this part, so every wave takes at most one item),
+// then as many as bring them back within it: an item's sub-chunks load one
+// after another, but a wave's items do too, with a merge wait each.
+constexpr int kItemSlots = 2048;
+__host__ __device__ inline int attention_span(int pos, int nh) {
+  const long n = (long)(pos / kChunk + 1) * (nh > 0 ? nh : 1);
+  return (int)((n + kItemSlots - 1) / kItemSlots);
 }
+// A head of more than kGroupFrom items merges in two levels: groups of
+// kGroup items are folded by their last item, then the group partials by
+// the head's last item (one round of loads per level instead of one per 16
+// partials).
+constexpr int kGroup = 16, kGroupFrom = 64;
+__host__ __device__ inline int attention_groups(int max_chunks) { return (max_chunks + kGroup - 1) / kGroup; }
 
 // Fused RoPE + KV append + GQA attention of one layer.
 struct AttnArgs {
@@ -25,8 +33,9 @@ struct AttnArgs {
   const int *pos;
   float *k_cache, *v_cache;  // this layer's [max_seq][kv_width]
   float *out;                // [nh * hd]
-  // Chunk partials, attention_scratch_words(nh, hd, max_seq) words: each value
-  // with the tag of the (step, layer) that wrote it in the high half.
+  // Chunk partials then group partials per head, attention_scratch_words(nh,
+  // hd, max_seq) words: each value with the tag of the (step, layer) that
+  // wrote it in the high half.
   unsigned long long *scratch;
   const unsigned *epoch;     // step counter, advanced by the embedding kernel
   unsigned *err;             // set when a merge gave up waiting for a partial

@@ -79,7 +79,7 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
   // first, so the chunk that merges a head always starts after the chunks it
   // waits for.
   const int pos = bounded_pos(a.pos, a.max_seq);
-  if (attention_span(pos) > 1)
+  if (attention_span(pos, a.nh) > 1)
     attention_item<HD, false, true>(a, blockIdx.x, blockIdx.y, pos, qs, kn);
   else
     attention_item<HD, false, false>(a, blockIdx.x, blockIdx.y, pos, qs, kn);
@@ -171,7 +171,8 @@ int launch_rmsnorm(const float *in, const float *w, float *out, int n, float eps
 long attention_part_stride(int hd) { return 2L * hd + 2; }
 
 size_t attention_scratch_words(int nh, int hd, int max_seq) {
-  return (size_t)nh * (size_t)attention_chunks(max_seq) * (size_t)attention_part_stride(hd);
+  const int chunks = attention_chunks(max_seq);
+  return (size_t)nh * (size_t)(chunks + attention_groups(chunks)) * (size_t)attention_part_stride(hd);
 }
 
 int attention_chunks(int max_seq) { return (max_seq + kChunk - 1) / kChunk; }

@@ -62,6 +62,6 @@ int decode_persistent_blocks_per_cu(uint32_t t_qkv, uint32_t t_v, uint32_t t_o, 
                                     uint32_t t_down, int head_dim, size_t lds, bool long_items,
                                     int *blocks);
 // Whether a step at position pos should launch the long_items instantiation.
-inline bool persistent_long_items(size_t pos) { return attention_span((int)pos) > 1; }
+inline bool persistent_long_items(size_t pos, int nh) { return attention_span((int)pos, nh) > 1; }
 
 }  // namespace llrs

@@ -90,8 +90,9 @@ typedef const __attribute__((address_space(4))) PersistentLayer ConstLayer;
 template <uint32_t T> struct TypeC { static constexpr uint32_t value = T; };
 
 // LONG: the instantiation whose attention also has the multi-chunk items of
-// positions past 2,048 (the other one keeps the single-chunk path's register
-// allocation; it stays correct at any position, with more partials to merge).
+// long contexts (attention_span > 1); the other one keeps the single-chunk
+// path's register allocation, and stays correct at any position, with more
+// partials to merge.
 template <uint32_t TQ, uint32_t TV, uint32_t TO, uint32_t TGU, uint32_t TD, int HD, bool LONG>
 __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(PersistentArgs p) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
   // Item i: XCD x = i % 8, r = i / 8, head j = r % G of pair q * 8 + x with
   // q = r / G; pair = chunk * nkv + kv head.
   const int G = p.attn.nh / p.attn.nkv;
-  const int span = LONG ? attention_span(pos) : 1;
+  const int span = LONG ? attention_span(pos, p.attn.nh) : 1;
   const int n_pairs = p.attn.nkv * (pos / (span * kChunk) + 1);
   const int n_items = (n_pairs + 7) / 8 * 8 * G;
   const unsigned epoch = *p.attn.epoch;  // advanced by this step's embedding launch

@@ -791,7 +791,7 @@ static bool use_graphs() {
 // One step at position pos (known to the host; the graph reads it from the
 // device), replayed from a captured hipGraph (captured on first use).
 static int run_step(llrs_model *m, llrs_kv *kv, int mode, size_t pos) {
-  const bool lng = persistent_long_items(pos);
+  const bool lng = persistent_long_items(pos, (int)m->cfg.num_attention_heads);
   if (!use_graphs()) return enqueue_step(m, kv, mode, lng);
   hipStream_t s = m->b->stream;
   const int gi = mode + 2 * (lng ? 1 : 0);
@@ -1638,7 +1638,7 @@ int llrs_profile_projection(llrs_model *m, llrs_kv *kv, int which, int iters, do
     for (int it = -1; it < iters && rc == LLRS_OK && e == hipSuccess; it++) {  // round -1 warms
       rc = enqueue_embed(m, kv);
       if (rc == LLRS_OK) e = hipEventRecord(ev[2 * (it + 1)], s);
-      if (rc == LLRS_OK && e == hipSuccess) rc = enqueue_layers(m, kv, persistent_long_items((size_t)saved_pos));
+      if (rc == LLRS_OK && e == hipSuccess) rc = enqueue_layers(m, kv, persistent_long_items((size_t)saved_pos, (int)m->cfg.num_attention_heads));
       if (rc == LLRS_OK && e == hipSuccess) e = hipEventRecord(ev[2 * (it + 1) + 1], s);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(s);

@@ -89,13 +89,12 @@ def test_head_dim_128_long_context(llrs, backend, oracle, tmp_path):
     compare_run(llrs, backend, oracle, cfg, tmp_path / "l.gguf", prompt, 32, 512)
 
 
-def test_attention_items_of_two_chunks(llrs, backend, oracle, tmp_path):
-    """Past 64 chunks (2,048 positions) an attention item covers consecutive
-    chunks, folded in the wave with the running-max rescaling, so a head
-    merges at most 64 partials.  The decode runs from position 2,030 across
-    2,048: single-chunk items (and the persistent launch without the
-    multi-chunk path) first, items of two chunks after.  (Seed 43: the
-    oracle's top-2 logit gap stays above 4.5e-3 on every step.)"""
+def test_attention_merge_in_two_levels(llrs, backend, oracle, tmp_path):
+    """Past 64 chunks (2,048 positions) a head's partials merge in two levels:
+    the last chunk of each group of 16 folds its group, the head's last chunk
+    its own group and then the group partials.  The decode runs from position
+    2,030 across 2,048: one-level merges first, two-level after.  (Seed 43:
+    the oracle's top-2 logit gap stays above 4.5e-3 on every step.)"""
     cfg = tiny_cfg(llrs, hidden_size=1024, num_attention_heads=8, num_key_value_heads=2,
                    intermediate_size=1024, num_hidden_layers=1, vocab_size=600,
                    max_position_embeddings=4096, seed=43)
@@ -416,3 +415,51 @@ def test_persistent_decode_per_layer_type_mix(llrs, backend, oracle, tmp_path, m
     model.prefill(prompt, 0, kv_s)
     np.testing.assert_array_equal(model.decode_greedy(len(prompt), 32, kv_s), got)
     np.testing.assert_array_equal(kv_s.logits(), kv.logits())
+
+
+@pytest.mark.timeout(300)
+def test_attention_past_32k_positions(llrs, backend, oracle, tmp_path):
+    """Past 1,024 chunks (32,768 positions) an attention item covers two
+    consecutive chunks (the persistent kernel's multi-chunk instantiation),
+    still merged in two levels.  A 32,760-token prompt goes through the
+    batched prefill; the oracle is seeded with the GPU's K/V rows of positions
+    0..32,749 and computes the last 10 prompt positions itself; then 16 steps
+    cross position 32,768 token by token, both sides fed the oracle's greedy
+    token (teacher forcing), logits compared at every step and tokens
+    wherever the oracle's top-2 gap exceeds 2e-3."""
+    cfg = tiny_cfg(llrs, hidden_size=1024, num_attention_heads=8, num_key_value_heads=2,
+                   intermediate_size=1024, num_hidden_layers=1, vocab_size=600,
+                   max_position_embeddings=40000, seed=45)
+    ctx, n_prompt, own = 32800, 32760, 10
+    path = tmp_path / "k32.gguf"
+    model, kv, om = make_pair(llrs, backend, oracle, cfg, path, ctx)
+    assert kv.persistent
+    prompt = np.random.default_rng(45).integers(0, cfg.vocab_size, n_prompt).astype(np.uint32)
+    model.prefill(prompt, 0, kv)
+    seed_to = n_prompt - own
+    for which in ("k", "v"):
+        om.load_kv(0, which, kv.layer(0, which, seed_to))
+    for i in range(seed_to, n_prompt):
+        om.forward_token(int(prompt[i]), i, i + 1 == n_prompt)
+    err = float(np.abs(kv.logits() - om.logits()).max())
+    print(f"[k32] prefill logits err {err:.2e}", flush=True)
+    assert err <= LOGIT_TOL
+    tok, checked = om.argmax(), 0
+    for i in range(16):
+        p = n_prompt + i
+        model.forward_token(tok, p, kv)
+        om.forward_token(tok, p, True)
+        lg, lo = kv.logits(), om.logits()
+        err = float(np.abs(lg - lo).max())
+        top2 = np.sort(lo.astype(np.float64))[-2:]
+        print(f"[k32] position {p} logits err {err:.2e} oracle gap {top2[1] - top2[0]:.2e}", flush=True)
+        assert err <= LOGIT_TOL
+        if top2[1] - top2[0] > 2e-3:
+            assert kv.argmax() == om.argmax()
+            checked += 1
+        tok = om.argmax()
+    assert checked >= 8
+    n = n_prompt + 16
+    for which in ("k", "v"):
+        a, b = kv.layer(0, which, n)[n_prompt:], om.kv(0, which, n)[n_prompt:]
+        assert float(np.abs(a - b).max()) <= 1e-3 * max(1.0, float(np.abs(b).max()))
