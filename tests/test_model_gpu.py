@@ -419,9 +419,11 @@ def test_persistent_decode_per_layer_type_mix(llrs, backend, oracle, tmp_path, m
 
 @pytest.mark.timeout(300)
 def test_attention_past_32k_positions(llrs, backend, oracle, tmp_path):
-    """Past 1,024 chunks (32,768 positions) an attention item covers two
-    consecutive chunks (the persistent kernel's multi-chunk instantiation),
-    still merged in two levels.  A 32,760-token prompt goes through the
+    """At 32K positions with 8 heads an attention item covers
+    ceil(chunks x heads / 2,048) consecutive chunks: four up to position
+    32,767 (256 items per head), five from 32,768 (205), the persistent
+    kernel's multi-chunk instantiation, each head merged in two levels.  A
+    32,760-token prompt goes through the
     batched prefill; the oracle is seeded with the GPU's K/V rows of positions
     0..32,749 and computes the last 10 prompt positions itself; then 16 steps
     cross position 32,768 token by token, both sides fed the oracle's greedy
