@@ -667,14 +667,10 @@ int gemm_slots() {
 }
 
 // The eight-wave kernel unless LLRS_PREFILL_GEMM=4 asks for the four-wave one
-// (for comparisons).
+// (for comparisons; read at every launch, so a test can switch it).
 bool eight_waves() {
-  static int v = -1;
-  if (v < 0) {
-    const char *e = getenv("LLRS_PREFILL_GEMM");
-    v = (e && strcmp(e, "4") == 0) ? 0 : 1;
-  }
-  return v == 1;
+  const char *e = getenv("LLRS_PREFILL_GEMM");
+  return !(e && strcmp(e, "4") == 0);
 }
 
 void launch_tiles(const PrefillGemmArgs &a, int bm, hipStream_t s) {

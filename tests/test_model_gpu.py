@@ -346,6 +346,37 @@ def test_batched_prefill_is_deterministic(llrs, backend, tmp_path, n, ffn):
                                           kvs[1].layer(layer, which, n).view(np.uint32))
 
 
+@pytest.mark.parametrize("n,recipe", [(40, "Q4KM"), (300, "Q4KM"), (256, "Q4K")],
+                         ids=["40_q4km", "300_q4km", "256_q4k"])
+def test_prefill_gemm_kernels_agree(llrs, backend, tmp_path, monkeypatch, n, recipe):
+    """The eight-wave prefill GEMM (the default) and the four-wave one
+    (LLRS_PREFILL_GEMM=4) run the same MFMA sequence per output, so a batched
+    prefill leaves bit-identical K/V rows and logits with either: 64- and
+    128-token tiles, split K, a ragged last token tile, and the Q4_K, Q6_K,
+    Q8_0 and Q5_0 stagings (hidden 384 puts the q4km recipe on its Q5_0
+    fallback)."""
+    hidden = 384 if n == 300 else 1024
+    cfg = tiny_cfg(llrs, hidden_size=hidden, num_attention_heads=hidden // 128 * 2,
+                   num_key_value_heads=2, intermediate_size=2048, num_hidden_layers=2, seed=41,
+                   recipe=getattr(llrs.LoadQuantization, recipe))
+    cfg.write_gguf(tmp_path / "g.gguf")
+    model = llrs.ModelLoader.load_dynamic(tmp_path / "g.gguf", backend)
+    prompt = np.random.default_rng(41).integers(0, cfg.vocab_size, n).astype(np.uint32)
+    kvs = []
+    for kernel in ("8", "4"):
+        monkeypatch.setenv("LLRS_PREFILL_GEMM", kernel)
+        kv = llrs.KVCache(model, 512)
+        model.prefill(prompt, 0, kv)
+        kvs.append(kv)
+    monkeypatch.delenv("LLRS_PREFILL_GEMM")
+    print(f"[prefill-kernels] n={n} {recipe}: logits[:3] {kvs[0].logits()[:3]}", flush=True)
+    np.testing.assert_array_equal(kvs[0].logits().view(np.uint32), kvs[1].logits().view(np.uint32))
+    for layer in range(cfg.num_hidden_layers):
+        for which in ("k", "v"):
+            np.testing.assert_array_equal(kvs[0].layer(layer, which, n).view(np.uint32),
+                                          kvs[1].layer(layer, which, n).view(np.uint32))
+
+
 def write_mixed_q4km(llrs, tmp_path, cfg, v_types, down_types):
     """A GGUF laid out like llama.cpp's Q4_K_M files (src/loader.rs:437-441
     keeps such files' tensors verbatim): Q4_K embeddings and q/k/o/gate/up,
