@@ -19,6 +19,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <initializer_list>
 #include <thread>
 #include <new>
 #include <string>
@@ -102,6 +103,8 @@ struct llrs_kv {
   float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_g = nullptr,
         *pf_u = nullptr;
   llrs::f16 *pf_h = nullptr, *pf_hl = nullptr;  // GEMM inputs as f16 hi + lo pairs
+  llrs::f16 *pf_xs = nullptr, *pf_xsl = nullptr;  // their 32-column sums (Q4_K products), [pf_cap][pf_ldxs]
+  int pf_ldxs = 0;
   float *pf_part = nullptr;                     // split-K partial tiles of the prefill GEMMs
   size_t pf_part_cap = 0;                       // floats
 };
@@ -1072,15 +1075,41 @@ static int prefill_buffers(llrs_kv *kv) {
   LLRS_TRY(A((void **)&kv->pf_u, T * F * 4));
   LLRS_TRY(A((void **)&kv->pf_h, T * (H > F ? H : F) * 2));
   LLRS_TRY(A((void **)&kv->pf_hl, T * (H > F ? H : F) * 2));
+  // Room for a Q4_K product's reads past the last sum (k/32 + 56 columns).
+  kv->pf_ldxs = (int)(((H > F ? H : F) / 32 + 56 + 7) / 8 * 8);
+  LLRS_TRY(A((void **)&kv->pf_xs, T * kv->pf_ldxs * 2));
+  LLRS_TRY(A((void **)&kv->pf_xsl, T * kv->pf_ldxs * 2));
+  LLRS_HIP(hipMemset(kv->pf_xs, 0, T * kv->pf_ldxs * 2));
+  LLRS_HIP(hipMemset(kv->pf_xsl, 0, T * kv->pf_ldxs * 2));
   kv->pf_part_cap = prefill_split_scratch_floats();
   LLRS_TRY(A((void **)&kv->pf_part, kv->pf_part_cap * 4));
   kv->pf_cap = T;
   return LLRS_OK;
 }
 
+// Whether the Q4_K integer-code product will read activation sums of `ws`'s input.
+static bool needs_xsum(std::initializer_list<const llrs_tensor *> ws) {
+  if (!prefill_k4_enabled()) return false;
+  for (const llrs_tensor *w : ws)
+    if (w->type == LLRS_Q4_K) return true;
+  return false;
+}
+
+// The activation sums of a/a_lo (k columns) that Q4_K products of this input read.
+static int prefill_xsum(llrs_kv *kv, const f16 *a, const f16 *a_lo, int k, int T, hipStream_t s) {
+  return launch_xsum_f16(a, a_lo, k, k, T, kv->pf_xs, kv->pf_xsl, kv->pf_ldxs, s);
+}
+
+// `xsum`: prefill_xsum has run on this input (Q4_K weights then take the integer-code product).
 static int prefill_gemm(llrs_kv *kv, const llrs_tensor *w, const f16 *a, const f16 *a_lo, int lda,
-                        float *c, int ldc, const float *bias, int T, bool accumulate, hipStream_t s) {
+                        float *c, int ldc, const float *bias, int T, bool accumulate, bool xsum,
+                        hipStream_t s) {
   PrefillGemmArgs g{};
+  if (xsum && w->type == LLRS_Q4_K) {
+    g.xs = kv->pf_xs;
+    g.xs_lo = kv->pf_xsl;
+    g.ldxs = kv->pf_ldxs;
+  }
   g.part = kv->pf_part;
   g.part_cap = kv->pf_part_cap;
   g.a = a;
@@ -1122,17 +1151,25 @@ static int prefill_batched(llrs_model *m, llrs_kv *kv, size_t start, size_t n) {
       const DevLayer &L = m->layers[l];
       float *kc = kv->k_cache + l * layer_stride, *vc = kv->v_cache + l * layer_stride;
       LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.attn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s));
-      LLRS_TRY(prefill_gemm(kv, L.q, kv->pf_h, kv->pf_hl, H, kv->pf_q, H, L.bq, T, false, s));
-      LLRS_TRY(prefill_gemm(kv, L.k, kv->pf_h, kv->pf_hl, H, kv->pf_k, KV, L.bk, T, false, s));
-      LLRS_TRY(prefill_gemm(kv, L.v, kv->pf_h, kv->pf_hl, H, kv->pf_v, KV, L.bv, T, false, s));
+      bool xs = needs_xsum({L.q, L.k, L.v});
+      if (xs) LLRS_TRY(prefill_xsum(kv, kv->pf_h, kv->pf_hl, H, T, s));
+      LLRS_TRY(prefill_gemm(kv, L.q, kv->pf_h, kv->pf_hl, H, kv->pf_q, H, L.bq, T, false, xs, s));
+      LLRS_TRY(prefill_gemm(kv, L.k, kv->pf_h, kv->pf_hl, H, kv->pf_k, KV, L.bk, T, false, xs, s));
+      LLRS_TRY(prefill_gemm(kv, L.v, kv->pf_h, kv->pf_hl, H, kv->pf_v, KV, L.bv, T, false, xs, s));
       LLRS_TRY(launch_rope_append(kv->pf_q, kv->pf_k, kv->pf_v, kv->rope, T, st, nh, nkv, hd, kc, vc, s));
       LLRS_TRY(launch_attention_rows(kv->pf_q, kc, vc, T, st, nh, nkv, hd, scale, kv->pf_h, kv->pf_hl, s));
-      LLRS_TRY(prefill_gemm(kv, L.o, kv->pf_h, kv->pf_hl, H, kv->pf_x, H, nullptr, T, true, s));
+      xs = needs_xsum({L.o});
+      if (xs) LLRS_TRY(prefill_xsum(kv, kv->pf_h, kv->pf_hl, H, T, s));
+      LLRS_TRY(prefill_gemm(kv, L.o, kv->pf_h, kv->pf_hl, H, kv->pf_x, H, nullptr, T, true, xs, s));
       LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.ffn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s));
-      LLRS_TRY(prefill_gemm(kv, L.gate, kv->pf_h, kv->pf_hl, H, kv->pf_g, F, nullptr, T, false, s));
-      LLRS_TRY(prefill_gemm(kv, L.up, kv->pf_h, kv->pf_hl, H, kv->pf_u, F, nullptr, T, false, s));
+      xs = needs_xsum({L.gate, L.up});
+      if (xs) LLRS_TRY(prefill_xsum(kv, kv->pf_h, kv->pf_hl, H, T, s));
+      LLRS_TRY(prefill_gemm(kv, L.gate, kv->pf_h, kv->pf_hl, H, kv->pf_g, F, nullptr, T, false, xs, s));
+      LLRS_TRY(prefill_gemm(kv, L.up, kv->pf_h, kv->pf_hl, H, kv->pf_u, F, nullptr, T, false, xs, s));
       LLRS_TRY(launch_swiglu_f16(kv->pf_g, kv->pf_u, kv->pf_h, kv->pf_hl, (size_t)T * F, s));
-      LLRS_TRY(prefill_gemm(kv, L.down, kv->pf_h, kv->pf_hl, F, kv->pf_x, H, nullptr, T, true, s));
+      xs = needs_xsum({L.down});
+      if (xs) LLRS_TRY(prefill_xsum(kv, kv->pf_h, kv->pf_hl, F, T, s));
+      LLRS_TRY(prefill_gemm(kv, L.down, kv->pf_h, kv->pf_hl, F, kv->pf_x, H, nullptr, T, true, xs, s));
     }
     last_rows = (size_t)T;
   }

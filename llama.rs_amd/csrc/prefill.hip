@@ -18,7 +18,9 @@
 // Precision: f32 operands are carried as f16 pairs, v = hi + lo with hi =
 // f16(v) and lo = f16(v - hi) (22 significant bits), and each product is
 // hi*hi + hi*lo + lo*hi (the lo*lo term is below f32 rounding of the sum), so
-// the GEMM is close to an f32 GEMM rather than an f16 one.
+// the GEMM is close to an f32 GEMM rather than an f16 one.  Q4_K weights take
+// prefill_gemm_k4_kernel instead: their integer codes are exact f16 values,
+// so one weight plane and two MFMAs per product suffice.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -420,6 +422,282 @@ __global__ __launch_bounds__(512) void prefill_gemm8_kernel(PrefillGemmArgs g) {
     }
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// The Q4_K product with the weight codes as exact f16 integers.  A Q4_K
+// weight is d * sc * q - dmin * m (value_at, src/quant.rs:349-456): q < 16 per
+// column, sc and m < 64 per 32-column sub-block s, d and dmin per 256-column
+// super-block b.  sc * q <= 945 is an exact f16, so
+//   y = sum_b d_b * sum_{j in b} (sc q)_j x_j  -  sum_s (dmin m)_s * xsum_s
+// with xsum_s the sum of the activations over sub-block s.  The first sum is
+// an MFMA product of one exact weight plane with the activations' hi and lo
+// planes: two MFMAs where an f32 weight (hi + lo) needs three, and half the
+// weight staging and LDS traffic.  Its accumulators are kept in units of the
+// row's current d: at each super-block they are scaled by d_prev / d_b (a
+// super-block with d = 0 contributes nothing and keeps the unit), and by the
+// last d at the end.  The second sum is a K/32-long product of -dmin * m (an
+// exact f32, as hi + lo) with xsum (hi + lo, xsum_f16_kernel), run after the
+// first on the same tile, LDS and accumulators, three MFMAs per step.  The
+// layout, roles and tiles are those of prefill_gemm8_kernel; K splits into
+// whole super-blocks.  Integer and f16 arithmetic on the codes is exact, so
+// the result differs from the f32 weights' only in f32 rounding.
+template <int BM, int TG>
+__global__ __launch_bounds__(512) void prefill_gemm_k4_kernel(PrefillGemmArgs g) {
+  // TG token groups x 8/TG row groups of waves: a wave multiplies TW tokens x RW rows.
+  constexpr int TW = BM / TG, RW = BN * TG / 8, MI = TW / 16, NJ = RW / 16;
+  constexpr int APT = BM / 4, TPR = 64 / APT;
+  extern __shared__ __align__(16) f16 lds[];
+  f16 *As = lds, *Al = As + BM * LS, *Ws = Al + BM * LS, *Wl = Ws + BN * LS;
+  // Per weight row of the tile: the rescale of the current super-block and the current unit.
+  float *ratio = reinterpret_cast<float *>(Wl + BN * LS), *unit = ratio + BN;
+  const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM;
+  const int per = ((g.k >> 8) + g.ksplit - 1) / g.ksplit * 256;
+  const int kb = blockIdx.z * per, ke = min(g.k, kb + per);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % TG, wn = wave / TG;
+  const bool wstage = wave < 4;
+  const int st = tid & 255;
+  f32x4 acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int ar = st / TPR, ac = (st % TPR) * APT;
+  const int wr = st >> 1, wc = (st & 1) * 32;
+  const bool a_ok = t0 + ar < g.t, w_ok = n0 + wr < g.n;
+  const int arow = a_ok ? t0 + ar : 0;
+  const uint8_t *wrow = g.w + (size_t)(w_ok ? n0 + wr : 0) * g.row_bytes;
+  union Pre {
+    struct { half8 ah[APT / 8], al[APT / 8]; } a;
+    struct { uint4 hdr, q0, q1; } w;  // d, dmin, 12 scale bytes; the sub-block pair's 32 code bytes
+    uint4 mh[4];                      // the headers of four super-blocks (second sum)
+  } pre;
+
+  // ---- First sum: the exact codes, rescaled per super-block ----
+  auto load_codes = [&](int k0) {  // k0: a multiple of 64 with k0 + 64 <= ke
+    if (wstage) {
+      const uint8_t *b = wrow + (size_t)(k0 >> 8) * 144;
+      const int pair = (k0 & 255) >> 6;
+      pre.w.hdr = *reinterpret_cast<const uint4 *>(b);
+      pre.w.q0 = *reinterpret_cast<const uint4 *>(b + 16 + pair * 32);
+      pre.w.q1 = *reinterpret_cast<const uint4 *>(b + 32 + pair * 32);
+    } else {
+      const size_t o = (size_t)arow * g.lda + k0 + ac;
+#pragma unroll
+      for (int h = 0; h < APT / 8; h++) {
+        pre.a.ah[h] = *reinterpret_cast<const half8 *>(g.a + o + 8 * h);
+        pre.a.al[h] = *reinterpret_cast<const half8 *>(g.a_lo + o + 8 * h);
+      }
+    }
+  };
+  float u = 1.f;  // a row's current unit (kept by its wc == 0 staging thread)
+  if (kb < ke) load_codes(kb);
+  for (int k0 = kb; k0 < ke; k0 += KC) {
+    __syncthreads();  // the previous chunk's MFMAs have read LDS
+    if (wstage) {
+      const int sub = ((k0 + wc) & 255) >> 5;  // sub < 4 is uniform: k0 is
+      const uint32_t s[3] = {pre.w.hdr.y, pre.w.hdr.z, pre.w.hdr.w};
+      const int sc = sub < 4 ? (byte_of(s, sub) & 63)
+                             : ((byte_of(s, sub + 4) & 0x0f) | ((byte_of(s, sub - 4) >> 6) << 4));
+      const float d = f16_bits_to_f32((uint16_t)(pre.w.hdr.x & 0xffff));
+      const bool live = d != 0.f;  // NaN d is live and makes the row NaN, as in f32
+      if ((k0 & 255) == 0 && wc == 0) {
+        ratio[wr] = live ? u / d : 1.f;
+        if (live) u = d;
+        unit[wr] = u;
+      }
+      // (1024 + q) from the f16 bit pattern 0x6400 | q, then (1024 + q) * sc -
+      // 1024 * sc = sc * q, exact in one fma.
+      const f16 sch = (f16)(float)((w_ok && live) ? sc : 0);
+      const half2v f = {sch, sch}, c = {(f16)(-1024.f * (float)sch), (f16)(-1024.f * (float)sch)};
+      const uint32_t w[8] = {pre.w.q0.x, pre.w.q0.y, pre.w.q0.z, pre.w.q0.w,
+                             pre.w.q1.x, pre.w.q1.y, pre.w.q1.z, pre.w.q1.w};
+      const int shift = (sub & 1) * 4;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        half8 h;
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+          const uint32_t v = (w[2 * q + p] >> shift) & 0x0f0f0f0fu;  // four codes, a byte each
+          const uint32_t lo = (v & 0xffu) | ((v << 8) & 0xff0000u) | 0x64006400u;
+          const uint32_t hi = ((v >> 16) & 0xffu) | ((v >> 8) & 0xff0000u) | 0x64006400u;
+          const half2v a = __builtin_elementwise_fma(__builtin_bit_cast(half2v, lo), f, c);
+          const half2v b = __builtin_elementwise_fma(__builtin_bit_cast(half2v, hi), f, c);
+          h[4 * p] = a[0];
+          h[4 * p + 1] = a[1];
+          h[4 * p + 2] = b[0];
+          h[4 * p + 3] = b[1];
+        }
+        *reinterpret_cast<half8 *>(Ws + wr * LS + wc + 8 * q) = h;
+      }
+    } else {
+      const half8 z = half8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int h = 0; h < APT / 8; h++) {
+        *reinterpret_cast<half8 *>(As + ar * LS + ac + 8 * h) = a_ok ? pre.a.ah[h] : z;
+        *reinterpret_cast<half8 *>(Al + ar * LS + ac + 8 * h) = a_ok ? pre.a.al[h] : z;
+      }
+    }
+    __syncthreads();
+    if (k0 + KC < ke) load_codes(k0 + KC);  // in flight during the MFMAs below
+    if ((k0 & 255) == 0) {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const float r = ratio[wn * RW + 16 * j + (lane & 15)];
+#pragma unroll
+        for (int i = 0; i < MI; i++) acc[i][j] *= r;
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < KC; ks += 32) {
+      half8 af[MI], al[MI], bf[NJ];
+#pragma unroll
+      for (int i = 0; i < MI; i++) {
+        const int o = (wm * TW + 16 * i + (lane & 15)) * LS + ks + 8 * (lane >> 4);
+        af[i] = *reinterpret_cast<const half8 *>(As + o);
+        al[i] = *reinterpret_cast<const half8 *>(Al + o);
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; j++)
+        bf[j] = *reinterpret_cast<const half8 *>(Ws + (wn * RW + 16 * j + (lane & 15)) * LS + ks +
+                                                 8 * (lane >> 4));
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+  }
+  if (kb < ke) {
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      const float d = unit[wn * RW + 16 * j + (lane & 15)];
+#pragma unroll
+      for (int i = 0; i < MI; i++) acc[i][j] *= d;
+    }
+  }
+
+  // ---- Second sum: - (dmin m)_s * xsum_s over this range's sub-blocks ----
+  const int mb = kb >> 5, me = ke >> 5;  // multiples of 8
+  auto load_mins = [&](int m0) {
+    if (wstage) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int s0 = m0 + wc + 8 * i;
+        pre.mh[i] = s0 < me ? *reinterpret_cast<const uint4 *>(wrow + (size_t)(s0 >> 3) * 144)
+                            : uint4{0, 0, 0, 0};
+      }
+    } else {
+      // Columns up to m0 + 64 <= K/32 + 56 < ldxs: in the buffer; those past
+      // the range are zeroed below.
+      const size_t o = (size_t)arow * g.ldxs + m0 + ac;
+#pragma unroll
+      for (int h = 0; h < APT / 8; h++) {
+        pre.a.ah[h] = *reinterpret_cast<const half8 *>(g.xs + o + 8 * h);
+        pre.a.al[h] = *reinterpret_cast<const half8 *>(g.xs_lo + o + 8 * h);
+      }
+    }
+  };
+  if (mb < me) load_mins(mb);
+  for (int m0 = mb; m0 < me; m0 += KC) {
+    const int mc = min(KC, me - m0);  // a multiple of 8
+    __syncthreads();
+    if (wstage) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const bool in = w_ok && m0 + wc + 8 * i < me;
+        const float dmin = f16_bits_to_f32((uint16_t)(pre.mh[i].x >> 16));
+        const uint32_t s[3] = {pre.mh[i].y, pre.mh[i].z, pre.mh[i].w};
+        half8 h, l;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {  // scale_min_k4 (src/quant.rs:338-347), the m half
+          const int m = e < 4 ? (byte_of(s, e + 4) & 63) : ((byte_of(s, e + 4) >> 4) | ((byte_of(s, e) >> 6) << 4));
+          f16 a, b;
+          split_f16(in ? -(dmin * (float)m) : 0.f, a, b);
+          h[e] = a;
+          l[e] = b;
+        }
+        *reinterpret_cast<half8 *>(Ws + wr * LS + wc + 8 * i) = h;
+        *reinterpret_cast<half8 *>(Wl + wr * LS + wc + 8 * i) = l;
+      }
+    } else {
+      const half8 z = half8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int h = 0; h < APT / 8; h++) {
+        const bool in = a_ok && ac + 8 * h < mc;
+        *reinterpret_cast<half8 *>(As + ar * LS + ac + 8 * h) = in ? pre.a.ah[h] : z;
+        *reinterpret_cast<half8 *>(Al + ar * LS + ac + 8 * h) = in ? pre.a.al[h] : z;
+      }
+    }
+    __syncthreads();
+    if (m0 + KC < me) load_mins(m0 + KC);
+    for (int ks = 0; ks < mc; ks += 32) {
+      half8 af[MI], al[MI], bf[NJ], bl[NJ];
+#pragma unroll
+      for (int i = 0; i < MI; i++) {
+        const int o = (wm * TW + 16 * i + (lane & 15)) * LS + ks + 8 * (lane >> 4);
+        af[i] = *reinterpret_cast<const half8 *>(As + o);
+        al[i] = *reinterpret_cast<const half8 *>(Al + o);
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const int o = (wn * RW + 16 * j + (lane & 15)) * LS + ks + 8 * (lane >> 4);
+        bf[j] = *reinterpret_cast<const half8 *>(Ws + o);
+        bl[j] = *reinterpret_cast<const half8 *>(Wl + o);
+      }
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bl[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+  }
+  // D layout: lane holds column (lane & 15) and rows 4 * (lane >> 4) + e.
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      const int n = n0 + wn * RW + 16 * j + (lane & 15);
+      if (n >= g.n) continue;
+      const float bias = (!g.accumulate && g.bias) ? g.bias[n] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int t = t0 + wm * TW + 16 * i + 4 * (lane >> 4) + e;
+        if (t >= g.t) continue;
+        if (g.ksplit > 1) {
+          g.part[((size_t)blockIdx.z * g.t + t) * g.n + n] = acc[i][j][e];
+        } else {
+          float *c = g.c + (size_t)t * g.ldc + n;
+          *c = g.accumulate ? *c + acc[i][j][e] : acc[i][j][e] + bias;
+        }
+      }
+    }
+}
+
+// xs + xs_lo [t][s] = the sum over j < 32 of a[t][32 s + j] + a_lo[t][32 s + j]
+// (in that order, in f32), as an f16 pair, for s < nsub.
+__global__ void xsum_f16_kernel(const f16 *__restrict__ a, const f16 *__restrict__ a_lo, int lda,
+                                int nsub, f16 *__restrict__ xs, f16 *__restrict__ xs_lo, int ldxs) {
+  const int s = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  if (s >= nsub) return;
+  const half8 *p = reinterpret_cast<const half8 *>(a + (size_t)t * lda + 32 * s);
+  const half8 *q = reinterpret_cast<const half8 *>(a_lo + (size_t)t * lda + 32 * s);
+  float sum = 0.f;
+#pragma unroll
+  for (int h = 0; h < 4; h++) {
+    const half8 x = p[h], y = q[h];
+#pragma unroll
+    for (int e = 0; e < 8; e++) sum += (float)x[e] + (float)y[e];
+  }
+  split_f16(sum, xs[(size_t)t * ldxs + s], xs_lo[(size_t)t * ldxs + s]);
+}
+
 __global__ void embed_rows_kernel(const uint8_t *__restrict__ emb, uint32_t ty, size_t row_bytes,
                                   int H, uint32_t vocab, const uint32_t *__restrict__ tok, int T,
                                   float *__restrict__ x) {
@@ -677,6 +955,14 @@ void launch_tiles(const PrefillGemmArgs &a, int bm, hipStream_t s) {
   const dim3 grid((unsigned)((a.n + BN - 1) / BN), (unsigned)((a.t + bm - 1) / bm), (unsigned)a.ksplit);
   const size_t lds = (size_t)2 * (bm + BN) * LS * sizeof(f16);
   const bool w8 = eight_waves();
+  if (a.type == LLRS_Q4_K && a.xs) {
+    const size_t lds4 = lds + 2 * BN * sizeof(float);
+    if (bm == 128)
+      hipLaunchKernelGGL((prefill_gemm_k4_kernel<128, 4>), grid, dim3(512), lds4, s, a);
+    else
+      hipLaunchKernelGGL((prefill_gemm_k4_kernel<64, 4>), grid, dim3(512), lds4, s, a);
+    return;
+  }
 
 #define GEMM(T)                                                                         \
   if (w8 && bm == 128)                                                                  \
@@ -717,10 +1003,29 @@ int launch_split(PrefillGemmArgs a, int bm, int ksplit, hipStream_t s) {
 
 size_t prefill_split_scratch_floats() { return (size_t)gemm_slots() * BN * 128; }
 
+bool prefill_k4_enabled() {
+  const char *e = getenv("LLRS_PREFILL_Q4K");
+  return eight_waves() && !(e && strcmp(e, "f32") == 0);
+}
+
+int launch_xsum_f16(const f16 *a, const f16 *a_lo, int lda, int k, int T, f16 *xs, f16 *xs_lo, int ldxs,
+                    hipStream_t s) {
+  if (k % 32 || lda % 8 || T <= 0 || ldxs < k / 32)
+    return set_error(LLRS_E_UNSUPPORTED, "activation sums over %d columns (lda %d, ldxs %d)", k, lda, ldxs);
+  const int nsub = k / 32;
+  hipLaunchKernelGGL(xsum_f16_kernel, dim3((unsigned)((nsub + 63) / 64), (unsigned)T), dim3(64), 0, s, a,
+                     a_lo, lda, nsub, xs, xs_lo, ldxs);
+  LLRS_HIP(hipGetLastError());
+  return LLRS_OK;
+}
+
 int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
   if (g.k % 32 || g.lda % 8 || g.n <= 0 || g.k <= 0 || g.t <= 0)
     return set_error(LLRS_E_UNSUPPORTED, "prefill GEMM shape %d x %d (lda %d) is not supported", g.n,
                      g.k, g.lda);
+  if (g.xs && (g.type != LLRS_Q4_K || g.k % 256 || g.ldxs % 8 || g.ldxs < g.k / 32 + 56))
+    return set_error(LLRS_E_UNSUPPORTED, "prefill GEMM: activation sums (ldxs %d) for a type %u product of %d columns",
+                     g.ldxs, g.type, g.k);
   // 128-token tiles when there are enough of them (the dequantized weight
   // tile then serves twice the tokens), else 64.  Products with fewer tiles
   // than half the slots split K over up to 8 workgroups (at least 6 K chunks

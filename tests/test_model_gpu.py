@@ -349,8 +349,9 @@ def test_batched_prefill_is_deterministic(llrs, backend, tmp_path, n, ffn):
 @pytest.mark.parametrize("n,recipe", [(40, "Q4KM"), (300, "Q4KM"), (256, "Q4K")],
                          ids=["40_q4km", "300_q4km", "256_q4k"])
 def test_prefill_gemm_kernels_agree(llrs, backend, tmp_path, monkeypatch, n, recipe):
-    """The eight-wave prefill GEMM (the default) and the four-wave one
-    (LLRS_PREFILL_GEMM=4) run the same MFMA sequence per output, so a batched
+    """The eight-wave prefill GEMM and the four-wave one (LLRS_PREFILL_GEMM=4)
+    run the same MFMA sequence per output on f32 weights (hi + lo planes;
+    LLRS_PREFILL_Q4K=f32 keeps Q4_K on that product too), so a batched
     prefill leaves bit-identical K/V rows and logits with either: 64- and
     128-token tiles, split K, a ragged last token tile, and the Q4_K, Q6_K,
     Q8_0 and Q5_0 stagings (hidden 384 puts the q4km recipe on its Q5_0
@@ -363,18 +364,95 @@ def test_prefill_gemm_kernels_agree(llrs, backend, tmp_path, monkeypatch, n, rec
     model = llrs.ModelLoader.load_dynamic(tmp_path / "g.gguf", backend)
     prompt = np.random.default_rng(41).integers(0, cfg.vocab_size, n).astype(np.uint32)
     kvs = []
+    monkeypatch.setenv("LLRS_PREFILL_Q4K", "f32")
     for kernel in ("8", "4"):
         monkeypatch.setenv("LLRS_PREFILL_GEMM", kernel)
         kv = llrs.KVCache(model, 512)
         model.prefill(prompt, 0, kv)
         kvs.append(kv)
     monkeypatch.delenv("LLRS_PREFILL_GEMM")
+    monkeypatch.delenv("LLRS_PREFILL_Q4K")
     print(f"[prefill-kernels] n={n} {recipe}: logits[:3] {kvs[0].logits()[:3]}", flush=True)
     np.testing.assert_array_equal(kvs[0].logits().view(np.uint32), kvs[1].logits().view(np.uint32))
     for layer in range(cfg.num_hidden_layers):
         for which in ("k", "v"):
             np.testing.assert_array_equal(kvs[0].layer(layer, which, n).view(np.uint32),
                                           kvs[1].layer(layer, which, n).view(np.uint32))
+
+
+def write_q4k_zero_d(llrs, tmp_path, cfg):
+    """The synthetic model with every matrix quantized to Q4_K on the host, then
+    d (the first f16 of a 256-column block) set to 0 in chosen blocks of q, o,
+    gate and ffn_down (dmin kept): in row r the blocks b with (r + b) % 5 == 0,
+    and every block of rows 3 and 4.  value_at (src/quant.rs:349-456) then
+    gives -dmin * m for all 256 columns of such a block."""
+    from gguf_write import qwen2_metadata, write_gguf
+    from hf_checkpoint import gguf_names
+    f32 = tmp_path / "f32.gguf"
+    llrs.SynthConfig(**{**cfg.__dict__, "recipe": llrs.LoadQuantization.NONE}).write_gguf(f32)
+    tensors, zeroed = [], 0
+    for name in gguf_names(cfg.num_hidden_layers, tied=False):
+        _, t = llrs.gguf_read_tensor(f32, name)
+        rows, cols = t.shape if len(t.shape) == 2 else (1, t.shape[0])
+        if rows == 1 or not name.endswith(".weight"):
+            tensors.append((name, 0, rows, cols, bytes(t.data)))
+            continue
+        q = llrs.QuantTensor.quantize(llrs.QuantType.Q4K, np.frombuffer(t.data, np.float32), rows, cols)
+        data = bytearray(q.data)
+        if any(name.endswith(s) for s in ("attn_q.weight", "attn_output.weight", "ffn_gate.weight",
+                                          "ffn_down.weight")):
+            nb, rb = cols // 256, cols // 256 * 144
+            for r in range(rows):
+                for b in range(nb):
+                    if (r + b) % 5 == 0 or r in (3, 4):
+                        data[r * rb + b * 144:r * rb + b * 144 + 2] = b"\x00\x00"
+                        zeroed += 1
+        tensors.append((name, int(q.quant_type), rows, cols, bytes(data)))
+    assert zeroed > 0
+    path = tmp_path / "zero_d.gguf"
+    write_gguf(path, qwen2_metadata(cfg), tensors)
+    return path
+
+
+@pytest.mark.parametrize("n", [40, 300], ids=["64_token_tiles", "128_token_tiles"])
+def test_prefill_q4k_integer_codes(llrs, backend, oracle, tmp_path, monkeypatch, n):
+    """The Q4_K prefill product on the integer codes (sc * q as exact f16, d
+    applied per 256-column block, the dmin * m term from 32-column activation
+    sums) on a Q4_K model whose q, o, gate and ffn_down have blocks with d = 0,
+    among them the first and the last block of a row and whole rows: within
+    the logits bar of the oracle (and K/V within 1e-3), within 1e-3 of the
+    f32-weight product (LLRS_PREFILL_Q4K=f32), and bit-identical from run to
+    run.  Hidden 1,024 (4 blocks a row) and FFN 2,048 (ffn_down: 8 a row)."""
+    cfg = tiny_cfg(llrs, hidden_size=1024, num_attention_heads=8, num_key_value_heads=2,
+                   intermediate_size=2048, num_hidden_layers=2, seed=53,
+                   recipe=llrs.LoadQuantization.Q4K)
+    path = write_q4k_zero_d(llrs, tmp_path, cfg)
+    model = llrs.ModelLoader.load_dynamic(path, backend)
+    om = oracle.load(path)
+    om.new_state(512)
+    prompt = np.random.default_rng(53).integers(0, cfg.vocab_size, n).astype(np.uint32)
+    kvs = []
+    for mode in ("int", "int", "f32"):
+        if mode == "f32":
+            monkeypatch.setenv("LLRS_PREFILL_Q4K", "f32")
+        kv = llrs.KVCache(model, 512)
+        model.prefill(prompt, 0, kv)
+        kvs.append(kv)
+    monkeypatch.delenv("LLRS_PREFILL_Q4K")
+    om.prefill(prompt, 0)
+    lo = om.logits()
+    err = float(np.abs(kvs[0].logits() - lo).max())
+    diff = float(np.abs(kvs[0].logits() - kvs[2].logits()).max())
+    print(f"[q4k-int] n={n} logits err vs oracle {err:.3e}, vs f32 product {diff:.3e}", flush=True)
+    assert err <= LOGIT_TOL
+    assert diff <= 1e-3
+    assert kvs[0].argmax() == om.argmax()
+    np.testing.assert_array_equal(kvs[0].logits().view(np.uint32), kvs[1].logits().view(np.uint32))
+    for layer in range(cfg.num_hidden_layers):
+        for which in ("k", "v"):
+            a, b = kvs[0].layer(layer, which, n), om.kv(layer, which, n)
+            assert float(np.abs(a - b).max()) <= 1e-3 * max(1.0, float(np.abs(b).max()))
+            np.testing.assert_array_equal(a.view(np.uint32), kvs[1].layer(layer, which, n).view(np.uint32))
 
 
 def write_mixed_q4km(llrs, tmp_path, cfg, v_types, down_types):
