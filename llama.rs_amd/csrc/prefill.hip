@@ -172,6 +172,34 @@ __device__ __forceinline__ void split_f16(float v, f16 &hi, f16 &lo) {
   lo = (f16)(v - (float)hi);
 }
 
+// A wave's MI x NJ accumulator blocks of 16 x 16 (tokens tb + 16 i + ..., rows
+// nb + 16 j + ...; D layout: lane holds row (lane & 15) and tokens
+// 4 * (lane >> 4) + e) into C: C (=|+=) acc (+ bias), or with K split the
+// split's partial tile into `part` (split_reduce_kernel adds them up).
+template <int MI, int NJ>
+__device__ __forceinline__ void store_tile(const PrefillGemmArgs &g, const f32x4 (&acc)[MI][NJ], int nb, int tb,
+                                           int lane) {
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      const int n = nb + 16 * j + (lane & 15);
+      if (n >= g.n) continue;
+      const float bias = (!g.accumulate && g.bias) ? g.bias[n] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int t = tb + 16 * i + 4 * (lane >> 4) + e;
+        if (t >= g.t) continue;
+        if (g.ksplit > 1) {
+          g.part[((size_t)blockIdx.z * g.t + t) * g.n + n] = acc[i][j][e];
+        } else {
+          float *c = g.c + (size_t)t * g.ldc + n;
+          *c = g.accumulate ? *c + acc[i][j][e] : acc[i][j][e] + bias;
+        }
+      }
+    }
+}
+
 // BM tokens x BN weight rows per workgroup (BM = 64 or 128).
 template <uint32_t TY, int BM>
 __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
@@ -270,26 +298,7 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
         }
     }
   }
-  // D layout: lane holds column (lane & 15) and rows 4 * (lane >> 4) + e.
-#pragma unroll
-  for (int i = 0; i < MI; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int n = n0 + wn * 64 + 16 * j + (lane & 15);
-      if (n >= g.n) continue;
-      const float bias = (!g.accumulate && g.bias) ? g.bias[n] : 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int t = t0 + wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + e;
-        if (t >= g.t) continue;
-        if (g.ksplit > 1) {
-          g.part[((size_t)blockIdx.z * g.t + t) * g.n + n] = acc[i][j][e];
-        } else {
-          float *c = g.c + (size_t)t * g.ldc + n;
-          *c = g.accumulate ? *c + acc[i][j][e] : acc[i][j][e] + bias;
-        }
-      }
-    }
+  store_tile<MI, 4>(g, acc, n0 + wn * 64, t0 + wm * (BM / 2), lane);
 }
 
 // The same tile, products and LDS layout with eight waves, so that two
@@ -400,26 +409,7 @@ __global__ __launch_bounds__(512) void prefill_gemm8_kernel(PrefillGemmArgs g) {
         }
     }
   }
-  // D layout: lane holds column (lane & 15) and rows 4 * (lane >> 4) + e.
-#pragma unroll
-  for (int i = 0; i < MI; i++)
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-      const int n = n0 + wn * 32 + 16 * j + (lane & 15);
-      if (n >= g.n) continue;
-      const float bias = (!g.accumulate && g.bias) ? g.bias[n] : 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int t = t0 + wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + e;
-        if (t >= g.t) continue;
-        if (g.ksplit > 1) {
-          g.part[((size_t)blockIdx.z * g.t + t) * g.n + n] = acc[i][j][e];
-        } else {
-          float *c = g.c + (size_t)t * g.ldc + n;
-          *c = g.accumulate ? *c + acc[i][j][e] : acc[i][j][e] + bias;
-        }
-      }
-    }
+  store_tile<MI, NJ>(g, acc, n0 + wn * 32, t0 + wm * (BM / 2), lane);
 }
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
@@ -658,26 +648,7 @@ __global__ __launch_bounds__(512) void prefill_gemm_k4_kernel(PrefillGemmArgs g)
         }
     }
   }
-  // D layout: lane holds column (lane & 15) and rows 4 * (lane >> 4) + e.
-#pragma unroll
-  for (int i = 0; i < MI; i++)
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-      const int n = n0 + wn * RW + 16 * j + (lane & 15);
-      if (n >= g.n) continue;
-      const float bias = (!g.accumulate && g.bias) ? g.bias[n] : 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int t = t0 + wm * TW + 16 * i + 4 * (lane >> 4) + e;
-        if (t >= g.t) continue;
-        if (g.ksplit > 1) {
-          g.part[((size_t)blockIdx.z * g.t + t) * g.n + n] = acc[i][j][e];
-        } else {
-          float *c = g.c + (size_t)t * g.ldc + n;
-          *c = g.accumulate ? *c + acc[i][j][e] : acc[i][j][e] + bias;
-        }
-      }
-    }
+  store_tile<MI, NJ>(g, acc, n0 + wn * RW, t0 + wm * TW, lane);
 }
 
 // xs + xs_lo [t][s] = the sum over j < 32 of a[t][32 s + j] + a_lo[t][32 s + j]
@@ -779,7 +750,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float *__restrict__ q,
 // weigh 0 and their V rows are clamped to rows the tile may read.  The
 // uniform fallback applies when no finite positive total remains.
 template <int HD>
-__global__ __launch_bounds__(256) void attention_tile_kernel(const float *__restrict__ q,
+__global__ __launch_bounds__(256, 3) void attention_tile_kernel(const float *__restrict__ q,
                                                              const float *__restrict__ k_cache,
                                                              const float *__restrict__ v_cache,
                                                              int T, int start, int nh, int nkv,
@@ -807,15 +778,16 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(const float *__rest
   for (int t = 0; t < NT; t++) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float M = -INFINITY, L = 0.f;
   const int nb = pmax / 16 + 1;
-  for (int b = wave; b < nb; b += 4) {
-    const int key0 = b * 16;
-    float kk[DPL];
-    {
-      const float *kp = kc + (size_t)min(key0 + i, pmax) * kvw;
+  // The K rows of a block are loaded as soon as the previous block's scores
+  // are computed and its V rows once its output products are issued, so each
+  // load's latency overlaps the other half of an iteration.
+  float kk[DPL], vv[4][NT];
+  auto load_k = [&](int key0) {
+    const float *kp = kc + (size_t)min(key0 + i, pmax) * kvw;
 #pragma unroll
-      for (int d = 0; d < DPL; d += 4) *reinterpret_cast<float4 *>(kk + d) = *reinterpret_cast<const float4 *>(kp + d);
-    }
-    float vv[4][NT];
+    for (int d = 0; d < DPL; d += 4) *reinterpret_cast<float4 *>(kk + d) = *reinterpret_cast<const float4 *>(kp + d);
+  };
+  auto load_v = [&](int key0) {
 #pragma unroll
     for (int s = 0; s < 4; s++) {
       const float *vp = vc + (size_t)min(key0 + 4 * g + s, pmax) * kvw;
@@ -829,9 +801,19 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(const float *__rest
           vv[s][t] = vp[t];
       }
     }
-    f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  if (wave < nb) {
+    load_k(wave * 16);
+    load_v(wave * 16);
+  }
+  for (int b = wave; b < nb; b += 4) {
+    const int key0 = b * 16;
+    // Two independent chains over the head dims (d mod 2), summed at the end.
+    f32x4 sp[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int d = 0; d < DPL; d++) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[d], qv[d], st, 0, 0, 0);
+    for (int d = 0; d < DPL; d++) sp[d & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[d], qv[d], sp[d & 1], 0, 0, 0);
+    const f32x4 st = sp[0] + sp[1];
+    if (b + 4 < nb) load_k(key0 + 64);
     float sc[4], mc = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -857,6 +839,7 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(const float *__rest
 #pragma unroll
       for (int s = 0; s < 4; s++) o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[s][t], pw[s], o[t], 0, 0, 0);
     }
+    if (b + 4 < nb) load_v(key0 + 64);
   }
   L += __shfl_xor(L, 16, 64);
   L += __shfl_xor(L, 32, 64);
@@ -912,6 +895,7 @@ __global__ void swiglu_f16_kernel(const float *__restrict__ g, const float *__re
 }
 
 __global__ void set_pos_kernel(int *pos, int value) { *pos = value; }
+
 
 // C[t][j] = (C[t][j] when accumulating, else bias[j] or 0) + the split-K
 // partials of splits 0, 1, ..., ksplit - 1, added in that order.
