@@ -1150,9 +1150,9 @@ static int prefill_batched(llrs_model *m, llrs_kv *kv, size_t start, size_t n) {
     for (size_t l = 0; l < c.num_hidden_layers; l++) {
       const DevLayer &L = m->layers[l];
       float *kc = kv->k_cache + l * layer_stride, *vc = kv->v_cache + l * layer_stride;
-      LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.attn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s));
       bool xs = needs_xsum({L.q, L.k, L.v});
-      if (xs) LLRS_TRY(prefill_xsum(kv, kv->pf_h, kv->pf_hl, H, T, s));
+      LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.attn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s,
+                                       xs ? kv->pf_xs : nullptr, kv->pf_xsl, kv->pf_ldxs));
       LLRS_TRY(prefill_gemm(kv, L.q, kv->pf_h, kv->pf_hl, H, kv->pf_q, H, L.bq, T, false, xs, s));
       LLRS_TRY(prefill_gemm(kv, L.k, kv->pf_h, kv->pf_hl, H, kv->pf_k, KV, L.bk, T, false, xs, s));
       LLRS_TRY(prefill_gemm(kv, L.v, kv->pf_h, kv->pf_hl, H, kv->pf_v, KV, L.bv, T, false, xs, s));
@@ -1161,14 +1161,14 @@ static int prefill_batched(llrs_model *m, llrs_kv *kv, size_t start, size_t n) {
       xs = needs_xsum({L.o});
       if (xs) LLRS_TRY(prefill_xsum(kv, kv->pf_h, kv->pf_hl, H, T, s));
       LLRS_TRY(prefill_gemm(kv, L.o, kv->pf_h, kv->pf_hl, H, kv->pf_x, H, nullptr, T, true, xs, s));
-      LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.ffn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s));
       xs = needs_xsum({L.gate, L.up});
-      if (xs) LLRS_TRY(prefill_xsum(kv, kv->pf_h, kv->pf_hl, H, T, s));
+      LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.ffn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s,
+                                       xs ? kv->pf_xs : nullptr, kv->pf_xsl, kv->pf_ldxs));
       LLRS_TRY(prefill_gemm(kv, L.gate, kv->pf_h, kv->pf_hl, H, kv->pf_g, F, nullptr, T, false, xs, s));
       LLRS_TRY(prefill_gemm(kv, L.up, kv->pf_h, kv->pf_hl, H, kv->pf_u, F, nullptr, T, false, xs, s));
-      LLRS_TRY(launch_swiglu_f16(kv->pf_g, kv->pf_u, kv->pf_h, kv->pf_hl, (size_t)T * F, s));
       xs = needs_xsum({L.down});
-      if (xs) LLRS_TRY(prefill_xsum(kv, kv->pf_h, kv->pf_hl, F, T, s));
+      LLRS_TRY(launch_swiglu_f16(kv->pf_g, kv->pf_u, kv->pf_h, kv->pf_hl, (size_t)T * F, F, s,
+                                 xs ? kv->pf_xs : nullptr, kv->pf_xsl, kv->pf_ldxs));
       LLRS_TRY(prefill_gemm(kv, L.down, kv->pf_h, kv->pf_hl, F, kv->pf_x, H, nullptr, T, true, xs, s));
     }
     last_rows = (size_t)T;

@@ -51,9 +51,11 @@ int launch_xsum_f16(const f16 *a, const f16 *a_lo, int lda, int k, int T, f16 *x
 
 // x[t][:] = embedding row of tok[t] (bit-exact dequant), t < T.
 int launch_embed_rows(const llrs_tensor *emb, const uint32_t *tok, int T, float *x, hipStream_t s);
-// out + out_lo [t][:] = x[t] * (1/sqrt(mean(x[t]^2) + eps) * w) as f16 pairs.
+// out + out_lo [t][:] = x[t] * (1/sqrt(mean(x[t]^2) + eps) * w) as f16 pairs;
+// with xs set, also their 32-column sums as launch_xsum_f16 gives them (up
+// to f32 summation order).
 int launch_rmsnorm_rows_f16(const float *x, const float *w, f16 *out, f16 *out_lo, int T, int H,
-                            float eps, hipStream_t s);
+                            float eps, hipStream_t s, f16 *xs = nullptr, f16 *xs_lo = nullptr, int ldxs = 0);
 // Split-half RoPE of q (in place) and k at positions start + t, and the K/V
 // cache rows of those positions.
 int launch_rope_append(float *q, const float *k, const float *v, const float *rope, int T, int start,
@@ -63,8 +65,10 @@ int launch_rope_append(float *q, const float *k, const float *v, const float *ro
 int launch_attention_rows(const float *q, const float *k_cache, const float *v_cache, int T,
                           int start, int nh, int nkv, int hd, float scale, f16 *out, f16 *out_lo,
                           hipStream_t s);
-// out + out_lo [i] = silu(g[i]) * u[i] as f16 pairs, i < n.
-int launch_swiglu_f16(const float *g, const float *u, f16 *out, f16 *out_lo, size_t n, hipStream_t s);
+// out + out_lo [i] = silu(g[i]) * u[i] as f16 pairs, i < n (rows of `cols`);
+// with xs set, also their 32-column sums per row.
+int launch_swiglu_f16(const float *g, const float *u, f16 *out, f16 *out_lo, size_t n, int cols, hipStream_t s,
+                      f16 *xs = nullptr, f16 *xs_lo = nullptr, int ldxs = 0);
 int launch_set_pos(int *pos, int value, hipStream_t s);
 
 }  // namespace llrs

@@ -680,16 +680,40 @@ __global__ void embed_rows_kernel(const uint8_t *__restrict__ emb, uint32_t ty, 
 }
 
 // RMSNorm::forward (src/model.rs:65-73) per token row, rounded to f16.
+// With xs set (H a multiple of 32), also the activation sums of the output
+// that Q4_K products read: xs + xs_lo [row][s] = the sum of (hi + lo) over
+// columns 32 s ... 32 s + 31 (a 32-lane half-wave of one pass), as f16 pairs.
+__device__ __forceinline__ void half_wave_xsum(float v, int col, f16 *xs, f16 *xs_lo) {
+#pragma unroll
+  for (int m = 16; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  if ((threadIdx.x & 31) == 0) split_f16(v, xs[col >> 5], xs_lo[col >> 5]);
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_rows_f16_kernel(const float *__restrict__ x,
                                                                const float *__restrict__ w,
                                                                f16 *__restrict__ out,
                                                                f16 *__restrict__ out_lo, int H,
-                                                               float eps) {
+                                                               float eps, f16 *__restrict__ xs,
+                                                               f16 *__restrict__ xs_lo, int ldxs) {
 #pragma clang fp contract(off)
+  constexpr int kPer = 32;  // values a thread holds in registers (rows up to 8,192)
   __shared__ float red[4];
   const float *xr = x + (size_t)blockIdx.x * H;
+  const bool held = H <= kPer * 256;
+  float xv[kPer];
   float s = 0.f;
-  for (int i = threadIdx.x; i < H; i += blockDim.x) s += xr[i] * xr[i];
+  if (held) {  // every load issued before the first is used
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+      const int i = k * 256 + threadIdx.x;
+      xv[k] = i < H ? xr[i] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; k++)
+      if (k * 256 + threadIdx.x < H) s += xv[k] * xv[k];
+  } else {
+    for (int i = threadIdx.x; i < H; i += 256) s += xr[i] * xr[i];
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
@@ -697,7 +721,25 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_f16_kernel(const float *__re
   const float tot = red[0] + red[1] + red[2] + red[3];
   const float inv = 1.0f / sqrtf(tot / (float)H + eps);
   f16 *o = out + (size_t)blockIdx.x * H, *ol = out_lo + (size_t)blockIdx.x * H;
-  for (int i = threadIdx.x; i < H; i += blockDim.x) split_f16(xr[i] * (inv * w[i]), o[i], ol[i]);
+  auto emit = [&](int i, float xi) {  // i0 + threadIdx.x: whole passes, so the sums' shuffles see every lane
+    float v = 0.f;
+    if (i < H) {
+      f16 h, l;
+      split_f16(xi * (inv * w[i]), h, l);
+      o[i] = h;
+      ol[i] = l;
+      v = (float)h + (float)l;
+    }
+    if (xs && i - (int)(threadIdx.x & 31) < H)
+      half_wave_xsum(v, i, xs + (size_t)blockIdx.x * ldxs, xs_lo + (size_t)blockIdx.x * ldxs);
+  };
+  if (held) {
+#pragma unroll
+    for (int k = 0; k < kPer; k++)
+      if (k * 256 < H) emit(k * 256 + threadIdx.x, xv[k]);
+  } else {
+    for (int i0 = 0; i0 < H; i0 += 256) emit(i0 + threadIdx.x, i0 + threadIdx.x < H ? xr[i0 + threadIdx.x] : 0.f);
+  }
 }
 
 // Split-half RoPE (src/model.rs:87-95) of the row's query heads (in place)
@@ -884,13 +926,27 @@ __global__ __launch_bounds__(256, 3) void attention_tile_kernel(const float *__r
   }
 }
 
-__global__ void swiglu_f16_kernel(const float *__restrict__ g, const float *__restrict__ u,
-                                  f16 *__restrict__ out, f16 *__restrict__ out_lo, size_t n) {
+// With xs set (cols, the row length, a multiple of 32): the activation sums
+// of the output as rmsnorm_rows_f16_kernel writes them.
+__global__ __launch_bounds__(256) void swiglu_f16_kernel(const float *__restrict__ g, const float *__restrict__ u,
+                                                         f16 *__restrict__ out, f16 *__restrict__ out_lo,
+                                                         size_t n, int cols, f16 *__restrict__ xs,
+                                                         f16 *__restrict__ xs_lo, int ldxs) {
 #pragma clang fp contract(off)
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  float v = 0.f;
   if (i < n) {
     const float x = g[i];
-    split_f16((x / (1.0f + expf(-x))) * u[i], out[i], out_lo[i]);
+    f16 h, l;
+    split_f16((x / (1.0f + expf(-x))) * u[i], h, l);
+    out[i] = h;
+    out_lo[i] = l;
+    v = (float)h + (float)l;
+  }
+  const size_t i32 = i & ~(size_t)31;  // the half-wave's first element: n is a multiple of 32 with xs
+  if (xs && i32 < n) {
+    const size_t row = i32 / (size_t)cols;
+    half_wave_xsum(v, (int)(i32 - row * cols), xs + row * ldxs, xs_lo + row * ldxs);
   }
 }
 
@@ -1053,8 +1109,11 @@ int launch_embed_rows(const llrs_tensor *emb, const uint32_t *tok, int T, float 
 }
 
 int launch_rmsnorm_rows_f16(const float *x, const float *w, f16 *out, f16 *out_lo, int T, int H,
-                            float eps, hipStream_t s) {
-  hipLaunchKernelGGL(rmsnorm_rows_f16_kernel, dim3(T), dim3(256), 0, s, x, w, out, out_lo, H, eps);
+                            float eps, hipStream_t s, f16 *xs, f16 *xs_lo, int ldxs) {
+  if (xs && (H % 32 || ldxs < H / 32))
+    return set_error(LLRS_E_UNSUPPORTED, "activation sums over %d columns (ldxs %d)", H, ldxs);
+  hipLaunchKernelGGL(rmsnorm_rows_f16_kernel, dim3(T), dim3(256), 0, s, x, w, out, out_lo, H, eps, xs, xs_lo,
+                     ldxs);
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;
 }
@@ -1088,9 +1147,12 @@ int launch_attention_rows(const float *q, const float *k_cache, const float *v_c
   return LLRS_OK;
 }
 
-int launch_swiglu_f16(const float *g, const float *u, f16 *out, f16 *out_lo, size_t n, hipStream_t s) {
+int launch_swiglu_f16(const float *g, const float *u, f16 *out, f16 *out_lo, size_t n, int cols, hipStream_t s,
+                      f16 *xs, f16 *xs_lo, int ldxs) {
+  if (xs && (cols <= 0 || cols % 32 || n % (size_t)cols || ldxs < cols / 32))
+    return set_error(LLRS_E_UNSUPPORTED, "activation sums over rows of %d columns (ldxs %d)", cols, ldxs);
   hipLaunchKernelGGL(swiglu_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, u, out,
-                     out_lo, n);
+                     out_lo, n, cols, xs, xs_lo, ldxs);
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;
 }
