@@ -105,6 +105,7 @@ struct llrs_kv {
   llrs::f16 *pf_h = nullptr, *pf_hl = nullptr;  // GEMM inputs as f16 hi + lo pairs
   llrs::f16 *pf_xs = nullptr, *pf_xsl = nullptr;  // their 32-column sums (Q4_K products), [pf_cap][pf_ldxs]
   int pf_ldxs = 0;
+  llrs::PrefillKvF16 pf_kvf{};  // one layer's K/V rows as f16 hi/lo planes (prefill attention)
   float *pf_part = nullptr;                     // split-K partial tiles of the prefill GEMMs
   size_t pf_part_cap = 0;                       // floats
 };
@@ -1081,6 +1082,15 @@ static int prefill_buffers(llrs_kv *kv) {
   LLRS_TRY(A((void **)&kv->pf_xsl, T * kv->pf_ldxs * 2));
   LLRS_HIP(hipMemset(kv->pf_xs, 0, T * kv->pf_ldxs * 2));
   LLRS_HIP(hipMemset(kv->pf_xsl, 0, T * kv->pf_ldxs * 2));
+  {
+    const size_t np = (kv->max_seq_len + 15) / 16 * 16, n = np * KV * 2;
+    kv->pf_kvf.positions = (int)np;
+    kv->pf_kvf.kvw = (int)KV;
+    LLRS_TRY(A((void **)&kv->pf_kvf.kh, n));
+    LLRS_TRY(A((void **)&kv->pf_kvf.kl, n));
+    LLRS_TRY(A((void **)&kv->pf_kvf.vh, n));
+    LLRS_TRY(A((void **)&kv->pf_kvf.vl, n));
+  }
   kv->pf_part_cap = prefill_split_scratch_floats();
   LLRS_TRY(A((void **)&kv->pf_part, kv->pf_part_cap * 4));
   kv->pf_cap = T;
@@ -1157,7 +1167,8 @@ static int prefill_batched(llrs_model *m, llrs_kv *kv, size_t start, size_t n) {
       LLRS_TRY(prefill_gemm(kv, L.k, kv->pf_h, kv->pf_hl, H, kv->pf_k, KV, L.bk, T, false, xs, s));
       LLRS_TRY(prefill_gemm(kv, L.v, kv->pf_h, kv->pf_hl, H, kv->pf_v, KV, L.bv, T, false, xs, s));
       LLRS_TRY(launch_rope_append(kv->pf_q, kv->pf_k, kv->pf_v, kv->rope, T, st, nh, nkv, hd, kc, vc, s));
-      LLRS_TRY(launch_attention_rows(kv->pf_q, kc, vc, T, st, nh, nkv, hd, scale, kv->pf_h, kv->pf_hl, s));
+      LLRS_TRY(launch_attention_rows(kv->pf_q, kc, vc, T, st, nh, nkv, hd, scale, kv->pf_h, kv->pf_hl, s,
+                                     &kv->pf_kvf));
       xs = needs_xsum({L.o});
       if (xs) LLRS_TRY(prefill_xsum(kv, kv->pf_h, kv->pf_hl, H, T, s));
       LLRS_TRY(prefill_gemm(kv, L.o, kv->pf_h, kv->pf_hl, H, kv->pf_x, H, nullptr, T, true, xs, s));

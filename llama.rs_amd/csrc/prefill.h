@@ -60,11 +60,20 @@ int launch_rmsnorm_rows_f16(const float *x, const float *w, f16 *out, f16 *out_l
 // cache rows of those positions.
 int launch_rope_append(float *q, const float *k, const float *v, const float *rope, int T, int start,
                        int nh, int nkv, int hd, float *k_cache, float *v_cache, hipStream_t s);
+// Scratch for the f16 attention: one layer's K and V rows as hi/lo planes in
+// blocks of 16 positions (positions x kvw halves a plane; positions a
+// multiple of 16 and at least the rows attended, rounded up to 16).
+struct PrefillKvF16 {
+  f16 *kh, *kl, *vh, *vl;
+  int positions, kvw;
+};
 // Causal GQA attention of the T query rows (positions start + t) over the
-// cache, out + out_lo [T][nh*hd] (f16 pairs).
+// cache, out + out_lo [T][nh*hd] (f16 pairs).  With kvf (head_dim >= 32 and
+// unless LLRS_PREFILL_ATTN=f32) the products run as f16 hi/lo MFMAs on a copy
+// of the cache rows in kvf; otherwise as f32 MFMAs on the cache.
 int launch_attention_rows(const float *q, const float *k_cache, const float *v_cache, int T,
                           int start, int nh, int nkv, int hd, float scale, f16 *out, f16 *out_lo,
-                          hipStream_t s);
+                          hipStream_t s, const PrefillKvF16 *kvf = nullptr);
 // out + out_lo [i] = silu(g[i]) * u[i] as f16 pairs, i < n (rows of `cols`);
 // with xs set, also their 32-column sums per row.
 int launch_swiglu_f16(const float *g, const float *u, f16 *out, f16 *out_lo, size_t n, int cols, hipStream_t s,

@@ -926,6 +926,218 @@ __global__ __launch_bounds__(256, 3) void attention_tile_kernel(const float *__r
   }
 }
 
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+
+// One layer's cache rows of positions [0, P) as f16 hi/lo planes for
+// attention_f16_kernel, in blocks of 16 positions (16 * kvw halves a block
+// and plane) laid out so that each MFMA operand load of a 16-key block reads
+// one contiguous run:
+//   K: [block][dim / 32][position % 16][dim % 32]
+//   V: [block][dim][position % 16]      (V transposed within the block)
+// Positions P .. P16 - 1 (P16 = P rounded up to 16) are zeros, so every block
+// a query tile reads holds finite values.  kvw is a multiple of 32.  A
+// workgroup moves one block of 16 positions x 64 dims, V through LDS.
+__device__ __forceinline__ size_t kblk_index(int pos, int dim, int kvw) {
+  return (size_t)(pos >> 4) * 16 * kvw + (size_t)(dim >> 5) * 512 + (pos & 15) * 32 + (dim & 31);
+}
+__device__ __forceinline__ size_t vblk_index(int pos, int dim, int kvw) {
+  return (size_t)(pos >> 4) * 16 * kvw + (size_t)dim * 16 + (pos & 15);
+}
+
+__global__ __launch_bounds__(256) void kv_split_f16_kernel(const float *__restrict__ k,
+                                                           const float *__restrict__ v, int kvw, int P,
+                                                           f16 *__restrict__ kh, f16 *__restrict__ kl,
+                                                           f16 *__restrict__ vh, f16 *__restrict__ vl) {
+  __shared__ float tile[16][65];
+  const int p0 = blockIdx.x * 16, d0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int pl = ty * 4 + r, pos = p0 + pl, dim = d0 + tx;
+    float kx = 0.f, vx = 0.f;
+    if (pos < P && dim < kvw) {
+      kx = k[(size_t)pos * kvw + dim];
+      vx = v[(size_t)pos * kvw + dim];
+    }
+    if (dim < kvw) {
+      const size_t o = kblk_index(pos, dim, kvw);
+      split_f16(kx, kh[o], kl[o]);
+    }
+    tile[pl][tx] = vx;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 4; r++) {  // 16 consecutive positions of 16 consecutive dims: 512 contiguous bytes
+    const int pl = threadIdx.x & 15, dl = r * 16 + (threadIdx.x >> 4), dim = d0 + dl;
+    if (dim < kvw) {
+      const size_t o = vblk_index(p0 + pl, dim, kvw);
+      split_f16(tile[pl][dl], vh[o], vl[o]);
+    }
+  }
+}
+
+// attention_tile_kernel's tiles, order, online softmax and merge with f16
+// matrix products: q, K, V and the softmax weights as hi + lo pairs and three
+// MFMAs per product (hi*hi, hi*lo, lo*hi), accumulated in f32.  Scores: S^T =
+// K Q^T in v_mfma_f32_16x16x32_f16 steps of 32 head dims (K rows from kh/kl);
+// output: O^T = V^T P^T in v_mfma_f32_16x16x16_f16 steps of 16 keys (V^T rows
+// from vth/vtl, 16 output dims a tile).  One score step covers 32 dims where
+// the f32 kernel's covers 4, which moves the kernel off the matrix cores'
+// f32 rate.  HD >= 32.
+template <int HD>
+__global__ __launch_bounds__(256, 3) void attention_f16_kernel(const float *__restrict__ q,
+                                                            const f16 *__restrict__ kh,
+                                                            const f16 *__restrict__ kl,
+                                                            const f16 *__restrict__ vh,
+                                                            const f16 *__restrict__ vl,
+                                                            const float *__restrict__ v_cache, int T,
+                                                            int start, int nh, int nkv, float scale,
+                                                            f16 *__restrict__ out, f16 *__restrict__ out_lo) {
+  constexpr int NC = HD / 32;  // 32-dim score steps
+  constexpr int NT = HD / 16;  // 16-dim output tiles
+  __shared__ float so[4][16][HD + 4];
+  __shared__ float sm[4][16], sl[4][16];
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * 16;  // the longest tiles start first
+  const int h = blockIdx.y, kvh = h / (nh / nkv), kvw = nkv * HD;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+  const int pmax = start + min(q0 + 15, T - 1);
+  const int pq = start + min(q0 + i, T - 1);  // rows past T mask as the last row
+  half8 qh[NC], ql[NC];
+  {
+    const float *qp = q + (size_t)min(q0 + i, T - 1) * nh * HD + h * HD + 8 * g;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      const float4 a = *reinterpret_cast<const float4 *>(qp + 32 * c);
+      const float4 b = *reinterpret_cast<const float4 *>(qp + 32 * c + 4);
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        f16 hi, lo;
+        split_f16(x[e], hi, lo);
+        qh[c][e] = hi;
+        ql[c][e] = lo;
+      }
+    }
+  }
+  // Lane (i, g): K of key 16 b + i, dims 32 c + 8 g ...; V^T row (dim) 16 t + i,
+  // keys 16 b + 4 g ... (kv_split_f16_kernel's block layout; 16 * kvw halves a block).
+  const size_t ko = (size_t)kvh * (HD / 32) * 512 + i * 32 + 8 * g;
+  const size_t vo = (size_t)(kvh * HD + i) * 16 + 4 * g;
+  f32x4 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float M = -INFINITY, L = 0.f;
+  const int nb = pmax / 16 + 1;
+  half8 kah[NC], kal[NC];
+  half4v vah[NT], val[NT];
+  auto load_k = [&](int key0) {
+    const size_t r = (size_t)key0 * kvw + ko;  // key0 / 16 blocks of 16 * kvw
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      kah[c] = *reinterpret_cast<const half8 *>(kh + r + 512 * c);
+      kal[c] = *reinterpret_cast<const half8 *>(kl + r + 512 * c);
+    }
+  };
+  auto load_v = [&](int key0) {
+    const size_t r = (size_t)key0 * kvw + vo;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      vah[t] = *reinterpret_cast<const half4v *>(vh + r + 256 * t);
+      val[t] = *reinterpret_cast<const half4v *>(vl + r + 256 * t);
+    }
+  };
+  if (wave < nb) {
+    load_k(wave * 16);
+    load_v(wave * 16);
+  }
+  for (int b = wave; b < nb; b += 4) {
+    const int key0 = b * 16;
+    f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kal[c], qh[c], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kah[c], ql[c], s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kah[c], qh[c], s0, 0, 0, 0);
+    }
+    const f32x4 st = s0 + s1;
+    if (b + 4 < nb) load_k(key0 + 64);
+    float sc[4], mc = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      sc[r] = key0 + 4 * g + r <= pq ? st[r] * scale : -INFINITY;
+      mc = fmaxf(mc, sc[r]);
+    }
+    mc = fmaxf(mc, __shfl_xor(mc, 16, 64));
+    mc = fmaxf(mc, __shfl_xor(mc, 32, 64));
+    const float Mn = fmaxf(M, mc);
+    const bool live = Mn != -INFINITY;
+    const float alpha = live ? expf(M - Mn) : 1.f;
+    float ls = 0.f;
+    half4v ph, pl;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float pw = live ? expf(sc[r] - Mn) : 0.f;
+      ls += pw;
+      f16 hi, lo;
+      split_f16(pw, hi, lo);
+      ph[r] = hi;
+      pl[r] = lo;
+    }
+    L = L * alpha + ls;
+    M = Mn;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      o[t] *= alpha;
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(val[t], ph, o[t], 0, 0, 0);
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vah[t], pl, o[t], 0, 0, 0);
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vah[t], ph, o[t], 0, 0, 0);
+    }
+    if (b + 4 < nb) load_v(key0 + 64);
+  }
+  L += __shfl_xor(L, 16, 64);
+  L += __shfl_xor(L, 32, 64);
+  if (g == 0) {
+    sm[wave][i] = M;
+    sl[wave][i] = L;
+  }
+  // D layout of O^T: lane (i, g) holds query i, dims 16 t + 4 g + r.
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) so[wave][i][16 * t + 4 * g + r] = o[t][r];
+  __syncthreads();
+  // Merge: thread -> query qi, dims c*NT ... c*NT + NT - 1.
+  const int qi = threadIdx.x >> 4, c = threadIdx.x & 15;
+  if (q0 + qi >= T) return;
+  float Mt = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; w++) Mt = fmaxf(Mt, sm[w][qi]);
+  float Lt = 0.f, acc[NT];
+#pragma unroll
+  for (int e = 0; e < NT; e++) acc[e] = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    const float mw = sm[w][qi];
+    const float f = mw == -INFINITY ? 0.f : expf(mw - Mt);
+    Lt += sl[w][qi] * f;
+#pragma unroll
+    for (int e = 0; e < NT; e++) acc[e] += so[w][qi][c * NT + e] * f;
+  }
+  const int p = start + q0 + qi;
+  const size_t at = (size_t)(q0 + qi) * nh * HD + h * HD + c * NT;
+  if (isfinite(Lt) && Lt > 0.f) {
+#pragma unroll
+    for (int e = 0; e < NT; e++) split_f16(acc[e] / Lt, out[at + e], out_lo[at + e]);
+  } else {
+    const float *vp = v_cache + (size_t)kvh * HD + c * NT;
+    for (int e = 0; e < NT; e++) {
+      float vs = 0.f;
+      for (int j = 0; j <= p; j++) vs += vp[(size_t)j * kvw + e];
+      split_f16(vs / (float)(p + 1), out[at + e], out_lo[at + e]);
+    }
+  }
+}
+
 // With xs set (cols, the row length, a multiple of 32): the activation sums
 // of the output as rmsnorm_rows_f16_kernel writes them.
 __global__ __launch_bounds__(256) void swiglu_f16_kernel(const float *__restrict__ g, const float *__restrict__ u,
@@ -1126,12 +1338,37 @@ int launch_rope_append(float *q, const float *k, const float *v, const float *ro
   return LLRS_OK;
 }
 
+bool prefill_attention_f16() {
+  const char *e = getenv("LLRS_PREFILL_ATTN");
+  return !(e && strcmp(e, "f32") == 0);
+}
+
 int launch_attention_rows(const float *q, const float *k_cache, const float *v_cache, int T,
                           int start, int nh, int nkv, int hd, float scale, f16 *out, f16 *out_lo,
-                          hipStream_t s) {
+                          hipStream_t s, const PrefillKvF16 *kvf) {
   if (T <= 0 || nkv <= 0 || nh % nkv)
     return set_error(LLRS_E_UNSUPPORTED, "attention over %d rows with %d/%d heads", T, nh, nkv);
   const dim3 grid((unsigned)((T + 15) / 16), (unsigned)nh);
+  if (kvf && hd >= 32 && prefill_attention_f16()) {
+    const int kvw = nkv * hd, P = start + T;
+    if (((P + 15) & ~15) > kvf->positions || kvf->kvw != kvw || kvw % 32)
+      return set_error(LLRS_E_INVALID, "prefill attention: f16 K/V scratch of %d positions x %d for %d x %d",
+                       kvf->positions, kvf->kvw, P, kvw);
+    hipLaunchKernelGGL(kv_split_f16_kernel, dim3((unsigned)((P + 15) / 16), (unsigned)((kvw + 63) / 64)),
+                       dim3(256), 0, s, k_cache, v_cache, kvw, P, kvf->kh, kvf->kl, kvf->vh, kvf->vl);
+#define ATT16(D)                                                                                      \
+  hipLaunchKernelGGL(attention_f16_kernel<D>, grid, dim3(256), 0, s, q, kvf->kh, kvf->kl, kvf->vh, kvf->vl, \
+                     v_cache, T, start, nh, nkv, scale, out, out_lo)
+    switch (hd) {
+      case 32: ATT16(32); break;
+      case 64: ATT16(64); break;
+      case 128: ATT16(128); break;
+      default: return set_error(LLRS_E_UNSUPPORTED, "attention head_dim %d is not supported", hd);
+    }
+#undef ATT16
+    LLRS_HIP(hipGetLastError());
+    return LLRS_OK;
+  }
 #define ATT(D)                                                                                   \
   hipLaunchKernelGGL(attention_tile_kernel<D>, grid, dim3(256), 0, s, q, k_cache, v_cache, T, start, \
                      nh, nkv, scale, out, out_lo)
