@@ -1099,7 +1099,7 @@ static int prefill_buffers(llrs_kv *kv) {
 
 // Whether the Q4_K integer-code product will read activation sums of `ws`'s input.
 static bool needs_xsum(std::initializer_list<const llrs_tensor *> ws) {
-  if (!prefill_k4_enabled()) return false;
+  if (!prefill_codes_enabled()) return false;
   for (const llrs_tensor *w : ws)
     if (w->type == LLRS_Q4_K) return true;
   return false;

@@ -32,7 +32,7 @@ struct PrefillGemmArgs {
   size_t part_cap;  // floats
   // Q4_K weights: when set, the per-sub-block sums of the activations
   // (launch_xsum_f16 of a/a_lo, [T][ldxs], ldxs >= k/32 + 56) and the product
-  // runs on the Q4_K codes as exact integers (prefill_k4_enabled()).
+  // runs on the Q4_K codes as exact integers (prefill_codes_enabled()).
   const f16 *xs, *xs_lo;
   int ldxs;
 };
@@ -41,10 +41,10 @@ struct PrefillGemmArgs {
 // 128 x 128 tile per workgroup slot.
 size_t prefill_split_scratch_floats();
 int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s);
-// Whether Q4_K products run on the integer codes (the default; LLRS_PREFILL_Q4K=f32
-// or the four-wave GEMM, LLRS_PREFILL_GEMM=4, select the f32-weight product).
-// Read at every call.
-bool prefill_k4_enabled();
+// Whether Q4_K and Q6_K products run on their integer codes (the default;
+// LLRS_PREFILL_CODES=f32 or the four-wave GEMM, LLRS_PREFILL_GEMM=4, select
+// the f32-weight product).  Read at every call.
+bool prefill_codes_enabled();
 // xs + xs_lo [t][s] = sum_{j<32} (a + a_lo)[t][32 s + j] as f16 pairs, s < k/32, t < T.
 int launch_xsum_f16(const f16 *a, const f16 *a_lo, int lda, int k, int T, f16 *xs, f16 *xs_lo, int ldxs,
                     hipStream_t s);

@@ -301,6 +301,67 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
   store_tile<MI, 4>(g, acc, n0 + wn * 64, t0 + wm * (BM / 2), lane);
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// One staging thread's 32 Q6_K weights of a row (columns col .. col + 31, within
+// one 32-column quarter of a 128-column half) on their integer codes.  A Q6_K
+// weight is d * sc * (q - 32) (value_at, src/quant.rs:349-456): q a 6-bit
+// code, sc an int8 per 16 columns, d per 256-column block.  sc * (q - 32) is
+// an integer of magnitude at most 4,096: hi = its f16 rounding and lo = the
+// remainder (-1, 0 or 1, exact), from packed f16 arithmetic on 1024 + q (the
+// bit pattern 0x6400 | q): q - 32 is exact, hi one product, lo one fma.  d is
+// applied to the accumulators per 256-column block (`first`: this thread
+// keeps the row's unit u and publishes the block's rescale d_prev / d and the
+// unit; a block with d = 0 is staged as zeros and keeps the unit), as in
+// prefill_gemm_k4_kernel.  The three MFMAs per product stay (lo*x_hi is needed
+// where |sc * (q - 32)| > 2,048); the staging drops from ~14 VALU operations
+// per weight to ~3 per two.
+__device__ __forceinline__ void stage_q6k_codes(const Deq<LLRS_Q6_K>::Raw &r, int col, bool w_ok, bool first,
+                                                float &u, float *ratio, float *unit, f16 *ws, f16 *wl) {
+#pragma clang fp contract(off)
+  const float d = f16_bits_to_f32(r.d);
+  const bool live = d != 0.f;  // NaN d is live and makes the row NaN, as in f32
+  if (first) {
+    *ratio = live ? u / d : 1.f;
+    if (live) u = d;
+    *unit = u;
+  }
+  const int quarter = (col >> 5) & 3;
+  const bool use = w_ok && live;
+  const f16 s0 = (f16)(float)(use ? (int)(int8_t)(r.s2 & 0xff) : 0);
+  const f16 s1 = (f16)(float)(use ? (int)(int8_t)(r.s2 >> 8) : 0);
+  const half2v off = {(f16)-1056.f, (f16)-1056.f};
+#pragma unroll
+  for (int k2 = 0; k2 < 4; k2++) {  // columns 8 k2 .. 8 k2 + 7
+    half8 hv, lv;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int k = 2 * k2 + p;  // columns 4k .. 4k + 3
+      const uint32_t l = realign(r.ql, k, r.shl), h = realign(r.qh, k, r.shh);
+      const uint32_t lo4 = (quarter < 2 ? l : l >> 4) & 0x0f0f0f0fu;
+      const uint32_t hi2 = (h >> (2 * quarter)) & 0x03030303u;
+      const uint32_t q = lo4 | (hi2 << 4);  // four 6-bit codes, a byte each
+      const uint32_t pa = (q & 0xffu) | ((q << 8) & 0xff0000u) | 0x64006400u;
+      const uint32_t pb = ((q >> 16) & 0xffu) | ((q >> 8) & 0xff0000u) | 0x64006400u;
+      const f16 sc = k < 4 ? s0 : s1;
+      const half2v scv = {sc, sc};
+      const half2v xa = __builtin_bit_cast(half2v, pa) + off, xb = __builtin_bit_cast(half2v, pb) + off;
+      const half2v ha = xa * scv, hb = xb * scv;
+      const half2v la = __builtin_elementwise_fma(xa, scv, -ha), lb = __builtin_elementwise_fma(xb, scv, -hb);
+      hv[4 * p] = ha[0];
+      hv[4 * p + 1] = ha[1];
+      hv[4 * p + 2] = hb[0];
+      hv[4 * p + 3] = hb[1];
+      lv[4 * p] = la[0];
+      lv[4 * p + 1] = la[1];
+      lv[4 * p + 2] = lb[0];
+      lv[4 * p + 3] = lb[1];
+    }
+    *reinterpret_cast<half8 *>(ws + 8 * k2) = hv;
+    *reinterpret_cast<half8 *>(wl + 8 * k2) = lv;
+  }
+}
+
 // The same tile, products and LDS layout with eight waves, so that two
 // workgroups per CU put four waves on each SIMD (the four-wave kernel's two
 // leave the matrix cores waiting on the staging chain's latency).  Waves 0-3
@@ -311,16 +372,20 @@ __global__ __launch_bounds__(256) void prefill_gemm_kernel(PrefillGemmArgs g) {
 // to 128 registers.  Each output is the same sequence of MFMAs as in the
 // four-wave kernel.  Measured 4-5% faster per product (7B shape, 512
 // tokens); LLRS_PREFILL_GEMM=4 selects the four-wave kernel.
-template <uint32_t TY, int BM>
+template <uint32_t TY, int BM, bool CODES>
 __global__ __launch_bounds__(512) void prefill_gemm8_kernel(PrefillGemmArgs g) {
+  static_assert(!CODES || TY == LLRS_Q6_K, "integer-code staging is written for Q6_K");
   constexpr int MI = BM / 32;    // 16-token MFMA blocks per wave (BM/2 tokens)
   constexpr int NJ = 2;          // 16-row MFMA blocks per wave (32 rows)
   constexpr int APT = BM / 4;    // activation halves per staging thread and plane
   constexpr int TPR = 64 / APT;  // staging threads per activation row
   extern __shared__ __align__(16) f16 lds[];
   f16 *As = lds, *Al = As + BM * LS, *Ws = Al + BM * LS, *Wl = Ws + BN * LS;
+  // CODES: per weight row, the rescale of the current 256-column block and the current unit.
+  float *ratio = reinterpret_cast<float *>(Wl + BN * LS), *unit = ratio + BN;
   const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM;
-  const int per = ((g.k + KC - 1) / KC + g.ksplit - 1) / g.ksplit * KC;
+  const int per = CODES ? ((g.k >> 8) + g.ksplit - 1) / g.ksplit * 256
+                        : ((g.k + KC - 1) / KC + g.ksplit - 1) / g.ksplit * KC;
   const int kb = blockIdx.z * per, ke = min(g.k, kb + per);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;  // BM/2 tokens x 32 rows
@@ -353,11 +418,21 @@ __global__ __launch_bounds__(512) void prefill_gemm8_kernel(PrefillGemmArgs g) {
       }
     }
   };
+  float u = 1.f;  // CODES: a row's current unit (kept by its wc == 0 staging thread)
   if (kb < ke) load_chunk(kb);
   for (int k0 = kb; k0 < ke; k0 += KC) {
-    const int kc = min(KC, ke - k0);  // 32 or 64
+    const int kc = min(KC, ke - k0);  // 32 or 64 (64 with CODES)
     __syncthreads();  // the previous chunk's MFMAs have read LDS
-    if (wstage) {
+    bool staged = false;
+    if constexpr (CODES) {
+      if (wstage) {
+        stage_q6k_codes(pre.raw, k0 + wc, w_ok, (k0 & 255) == 0 && wc == 0, u, ratio + wr, unit + wr,
+                        Ws + wr * LS + wc, Wl + wr * LS + wc);
+        staged = true;
+      }
+    }
+    if (staged) {
+    } else if (wstage) {
       float v[32];
       Deq<TY>::decode(pre.raw, min(k0 + wc, ke - 32), v);  // the columns load_chunk read
       const bool in = w_ok && wc < kc;
@@ -385,6 +460,14 @@ __global__ __launch_bounds__(512) void prefill_gemm8_kernel(PrefillGemmArgs g) {
     }
     __syncthreads();
     if (k0 + KC < ke) load_chunk(k0 + KC);  // in flight during the MFMAs below
+    if (CODES && (k0 & 255) == 0) {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const float r = ratio[wn * 32 + 16 * j + (lane & 15)];
+#pragma unroll
+        for (int i = 0; i < MI; i++) acc[i][j] *= r;
+      }
+    }
     for (int ks = 0; ks < kc; ks += 32) {
       half8 af[MI], al[MI], bf[NJ], bl[NJ];
 #pragma unroll
@@ -409,10 +492,17 @@ __global__ __launch_bounds__(512) void prefill_gemm8_kernel(PrefillGemmArgs g) {
         }
     }
   }
+  if (CODES && kb < ke) {
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      const float d = unit[wn * 32 + 16 * j + (lane & 15)];
+#pragma unroll
+      for (int i = 0; i < MI; i++) acc[i][j] *= d;
+    }
+  }
   store_tile<MI, NJ>(g, acc, n0 + wn * 32, t0 + wm * (BM / 2), lane);
 }
 
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 // The Q4_K product with the weight codes as exact f16 integers.  A Q4_K
 // weight is d * sc * q - dmin * m (value_at, src/quant.rs:349-456): q < 16 per
@@ -1216,11 +1306,19 @@ void launch_tiles(const PrefillGemmArgs &a, int bm, hipStream_t s) {
     return;
   }
 
+  if (a.type == LLRS_Q6_K && w8 && prefill_codes_enabled()) {
+    const size_t lds6 = lds + 2 * BN * sizeof(float);
+    if (bm == 128)
+      hipLaunchKernelGGL((prefill_gemm8_kernel<LLRS_Q6_K, 128, true>), grid, dim3(512), lds6, s, a);
+    else
+      hipLaunchKernelGGL((prefill_gemm8_kernel<LLRS_Q6_K, 64, true>), grid, dim3(512), lds6, s, a);
+    return;
+  }
 #define GEMM(T)                                                                         \
   if (w8 && bm == 128)                                                                  \
-    hipLaunchKernelGGL((prefill_gemm8_kernel<T, 128>), grid, dim3(512), lds, s, a);    \
+    hipLaunchKernelGGL((prefill_gemm8_kernel<T, 128, false>), grid, dim3(512), lds, s, a); \
   else if (w8)                                                                          \
-    hipLaunchKernelGGL((prefill_gemm8_kernel<T, 64>), grid, dim3(512), lds, s, a);     \
+    hipLaunchKernelGGL((prefill_gemm8_kernel<T, 64, false>), grid, dim3(512), lds, s, a);  \
   else if (bm == 128)                                                                   \
     hipLaunchKernelGGL((prefill_gemm_kernel<T, 128>), grid, dim3(256), lds, s, a);     \
   else                                                                                  \
@@ -1255,8 +1353,8 @@ int launch_split(PrefillGemmArgs a, int bm, int ksplit, hipStream_t s) {
 
 size_t prefill_split_scratch_floats() { return (size_t)gemm_slots() * BN * 128; }
 
-bool prefill_k4_enabled() {
-  const char *e = getenv("LLRS_PREFILL_Q4K");
+bool prefill_codes_enabled() {
+  const char *e = getenv("LLRS_PREFILL_CODES");
   return eight_waves() && !(e && strcmp(e, "f32") == 0);
 }
 

@@ -351,7 +351,7 @@ def test_batched_prefill_is_deterministic(llrs, backend, tmp_path, n, ffn):
 def test_prefill_gemm_kernels_agree(llrs, backend, tmp_path, monkeypatch, n, recipe):
     """The eight-wave prefill GEMM and the four-wave one (LLRS_PREFILL_GEMM=4)
     run the same MFMA sequence per output on f32 weights (hi + lo planes;
-    LLRS_PREFILL_Q4K=f32 keeps Q4_K on that product too), so a batched
+    LLRS_PREFILL_CODES=f32 keeps Q4_K and Q6_K on that product too), so a batched
     prefill leaves bit-identical K/V rows and logits with either: 64- and
     128-token tiles, split K, a ragged last token tile, and the Q4_K, Q6_K,
     Q8_0 and Q5_0 stagings (hidden 384 puts the q4km recipe on its Q5_0
@@ -364,14 +364,14 @@ def test_prefill_gemm_kernels_agree(llrs, backend, tmp_path, monkeypatch, n, rec
     model = llrs.ModelLoader.load_dynamic(tmp_path / "g.gguf", backend)
     prompt = np.random.default_rng(41).integers(0, cfg.vocab_size, n).astype(np.uint32)
     kvs = []
-    monkeypatch.setenv("LLRS_PREFILL_Q4K", "f32")
+    monkeypatch.setenv("LLRS_PREFILL_CODES", "f32")
     for kernel in ("8", "4"):
         monkeypatch.setenv("LLRS_PREFILL_GEMM", kernel)
         kv = llrs.KVCache(model, 512)
         model.prefill(prompt, 0, kv)
         kvs.append(kv)
     monkeypatch.delenv("LLRS_PREFILL_GEMM")
-    monkeypatch.delenv("LLRS_PREFILL_Q4K")
+    monkeypatch.delenv("LLRS_PREFILL_CODES")
     print(f"[prefill-kernels] n={n} {recipe}: logits[:3] {kvs[0].logits()[:3]}", flush=True)
     np.testing.assert_array_equal(kvs[0].logits().view(np.uint32), kvs[1].logits().view(np.uint32))
     for layer in range(cfg.num_hidden_layers):
@@ -421,7 +421,7 @@ def test_prefill_q4k_integer_codes(llrs, backend, oracle, tmp_path, monkeypatch,
     sums) on a Q4_K model whose q, o, gate and ffn_down have blocks with d = 0,
     among them the first and the last block of a row and whole rows: within
     the logits bar of the oracle (and K/V within 1e-3), within 1e-3 of the
-    f32-weight product (LLRS_PREFILL_Q4K=f32), and bit-identical from run to
+    f32-weight product (LLRS_PREFILL_CODES=f32), and bit-identical from run to
     run.  Hidden 1,024 (4 blocks a row) and FFN 2,048 (ffn_down: 8 a row)."""
     cfg = tiny_cfg(llrs, hidden_size=1024, num_attention_heads=8, num_key_value_heads=2,
                    intermediate_size=2048, num_hidden_layers=2, seed=53,
@@ -434,11 +434,11 @@ def test_prefill_q4k_integer_codes(llrs, backend, oracle, tmp_path, monkeypatch,
     kvs = []
     for mode in ("int", "int", "f32"):
         if mode == "f32":
-            monkeypatch.setenv("LLRS_PREFILL_Q4K", "f32")
+            monkeypatch.setenv("LLRS_PREFILL_CODES", "f32")
         kv = llrs.KVCache(model, 512)
         model.prefill(prompt, 0, kv)
         kvs.append(kv)
-    monkeypatch.delenv("LLRS_PREFILL_Q4K")
+    monkeypatch.delenv("LLRS_PREFILL_CODES")
     om.prefill(prompt, 0)
     lo = om.logits()
     err = float(np.abs(kvs[0].logits() - lo).max())
