@@ -380,12 +380,13 @@ def test_prefill_gemm_kernels_agree(llrs, backend, tmp_path, monkeypatch, n, rec
                                           kvs[1].layer(layer, which, n).view(np.uint32))
 
 
-def write_q4k_zero_d(llrs, tmp_path, cfg):
-    """The synthetic model with every matrix quantized to Q4_K on the host, then
-    d (the first f16 of a 256-column block) set to 0 in chosen blocks of q, o,
-    gate and ffn_down (dmin kept): in row r the blocks b with (r + b) % 5 == 0,
-    and every block of rows 3 and 4.  value_at (src/quant.rs:349-456) then
-    gives -dmin * m for all 256 columns of such a block."""
+def write_q4k_zero_d(llrs, tmp_path, cfg, down_q6k=False):
+    """The synthetic model with every matrix quantized to Q4_K on the host (with
+    down_q6k, ffn_down to Q6_K), then d set to 0 in chosen 256-column blocks of
+    q, o, gate and ffn_down (Q4_K: the block's first f16, dmin kept; Q6_K: its
+    last f16): in row r the blocks b with (r + b) % 5 == 0, and every block of
+    rows 3 and 4.  value_at (src/quant.rs:349-456) then gives -dmin * m (Q4_K)
+    or 0 (Q6_K) for all 256 columns of such a block."""
     from gguf_write import qwen2_metadata, write_gguf
     from hf_checkpoint import gguf_names
     f32 = tmp_path / "f32.gguf"
@@ -397,15 +398,20 @@ def write_q4k_zero_d(llrs, tmp_path, cfg):
         if rows == 1 or not name.endswith(".weight"):
             tensors.append((name, 0, rows, cols, bytes(t.data)))
             continue
-        q = llrs.QuantTensor.quantize(llrs.QuantType.Q4K, np.frombuffer(t.data, np.float32), rows, cols)
+        q6 = down_q6k and name.endswith("ffn_down.weight")
+        ty = llrs.QuantType.Q6K if q6 else llrs.QuantType.Q4K
+        q = llrs.QuantTensor.quantize(ty, np.frombuffer(t.data, np.float32), rows, cols)
         data = bytearray(q.data)
         if any(name.endswith(s) for s in ("attn_q.weight", "attn_output.weight", "ffn_gate.weight",
                                           "ffn_down.weight")):
-            nb, rb = cols // 256, cols // 256 * 144
+            bb, doff = (210, 208) if q6 else (144, 0)  # block bytes, offset of d
+            nb = cols // 256
+            rb = nb * bb
             for r in range(rows):
                 for b in range(nb):
                     if (r + b) % 5 == 0 or r in (3, 4):
-                        data[r * rb + b * 144:r * rb + b * 144 + 2] = b"\x00\x00"
+                        o = r * rb + b * bb + doff
+                        data[o:o + 2] = b"\x00\x00"
                         zeroed += 1
         tensors.append((name, int(q.quant_type), rows, cols, bytes(data)))
     assert zeroed > 0
@@ -414,19 +420,22 @@ def write_q4k_zero_d(llrs, tmp_path, cfg):
     return path
 
 
-@pytest.mark.parametrize("n", [40, 300], ids=["64_token_tiles", "128_token_tiles"])
-def test_prefill_q4k_integer_codes(llrs, backend, oracle, tmp_path, monkeypatch, n):
-    """The Q4_K prefill product on the integer codes (sc * q as exact f16, d
-    applied per 256-column block, the dmin * m term from 32-column activation
-    sums) on a Q4_K model whose q, o, gate and ffn_down have blocks with d = 0,
-    among them the first and the last block of a row and whole rows: within
-    the logits bar of the oracle (and K/V within 1e-3), within 1e-3 of the
-    f32-weight product (LLRS_PREFILL_CODES=f32), and bit-identical from run to
-    run.  Hidden 1,024 (4 blocks a row) and FFN 2,048 (ffn_down: 8 a row)."""
+@pytest.mark.parametrize("n,down_q6k", [(40, False), (300, False), (300, True)],
+                         ids=["64_token_tiles", "128_token_tiles", "q6k_down"])
+def test_prefill_q4k_integer_codes(llrs, backend, oracle, tmp_path, monkeypatch, n, down_q6k):
+    """The prefill products on the integer codes -- Q4_K: sc * q as exact f16,
+    d applied per 256-column block, the dmin * m term from 32-column
+    activation sums; Q6_K (ffn_down in the q6k_down case): sc * (q - 32) as
+    f16 hi + lo, d per block -- on a model whose q, o, gate and ffn_down have
+    blocks with d = 0, among them the first and the last block of a row and
+    whole rows: within the logits bar of the oracle (and K/V within 1e-3),
+    within 1e-3 of the f32-weight products (LLRS_PREFILL_CODES=f32), and
+    bit-identical from run to run.  Hidden 1,024 (4 blocks a row) and FFN
+    2,048 (ffn_down: 8 a row)."""
     cfg = tiny_cfg(llrs, hidden_size=1024, num_attention_heads=8, num_key_value_heads=2,
                    intermediate_size=2048, num_hidden_layers=2, seed=53,
                    recipe=llrs.LoadQuantization.Q4K)
-    path = write_q4k_zero_d(llrs, tmp_path, cfg)
+    path = write_q4k_zero_d(llrs, tmp_path, cfg, down_q6k)
     model = llrs.ModelLoader.load_dynamic(path, backend)
     om = oracle.load(path)
     om.new_state(512)
