@@ -89,6 +89,45 @@ def test_head_dim_128_long_context(llrs, backend, oracle, tmp_path):
     compare_run(llrs, backend, oracle, cfg, tmp_path / "l.gguf", prompt, 32, 512)
 
 
+@pytest.mark.parametrize("hd", [32, 64, 128])
+def test_prefill_attention_f16_and_f32(llrs, backend, oracle, tmp_path, monkeypatch, hd):
+    """The batched prefill's two attention kernels -- f16 hi/lo MFMAs over the
+    blocked f16 copy of the layer's K/V rows (the default) and f32 MFMAs over
+    the cache (LLRS_PREFILL_ATTN=f32) -- on a 600-token prompt (two chunks, the
+    second attending back into the first chunk's rows; a ragged last 16-key
+    block): both within the logits bar of the oracle, K/V within 1e-3, and
+    within 1e-3 of each other."""
+    cfg = tiny_cfg(llrs, hidden_size=hd * 8, num_attention_heads=8, num_key_value_heads=2,
+                   intermediate_size=1024, num_hidden_layers=2, vocab_size=600, seed=61,
+                   max_position_embeddings=1024)
+    cfg.write_gguf(tmp_path / "a.gguf")
+    model = llrs.ModelLoader.load_dynamic(tmp_path / "a.gguf", backend)
+    om = oracle.load(tmp_path / "a.gguf")
+    om.new_state(640)
+    prompt = np.random.default_rng(61).integers(0, cfg.vocab_size, 600).astype(np.uint32)
+    om.prefill(prompt, 0)
+    kvs = []
+    for mode in ("f16", "f32"):
+        if mode == "f32":
+            monkeypatch.setenv("LLRS_PREFILL_ATTN", "f32")
+        kv = llrs.KVCache(model, 640)
+        model.prefill(prompt, 0, kv)
+        kvs.append(kv)
+    monkeypatch.delenv("LLRS_PREFILL_ATTN")
+    lo = om.logits()
+    errs = [float(np.abs(kv.logits() - lo).max()) for kv in kvs]
+    diff = float(np.abs(kvs[0].logits() - kvs[1].logits()).max())
+    print(f"[attn] hd={hd} logits err f16 {errs[0]:.3e} f32 {errs[1]:.3e}, f16 vs f32 {diff:.3e}", flush=True)
+    assert max(errs) <= LOGIT_TOL
+    assert diff <= 1e-3
+    for kv in kvs:
+        assert kv.argmax() == om.argmax()
+        for layer in range(cfg.num_hidden_layers):
+            for which in ("k", "v"):
+                a, b = kv.layer(layer, which, 600), om.kv(layer, which, 600)
+                assert float(np.abs(a - b).max()) <= 1e-3 * max(1.0, float(np.abs(b).max()))
+
+
 def test_attention_merge_in_two_levels(llrs, backend, oracle, tmp_path):
     """Past 64 chunks (2,048 positions) a head's partials merge in two levels:
     the last chunk of each group of 16 folds its group, the head's last chunk
