@@ -89,6 +89,40 @@ def test_head_dim_128_long_context(llrs, backend, oracle, tmp_path):
     compare_run(llrs, backend, oracle, cfg, tmp_path / "l.gguf", prompt, 32, 512)
 
 
+@pytest.mark.parametrize("recipe", ["Q4KM", "Q4K"])
+def test_prefill_continued_after_decode(llrs, backend, oracle, tmp_path, recipe):
+    """A conversation's second turn: a 100-token prompt is prefilled, 6 tokens
+    are decoded, then a 150-token follow-up is prefilled at position 106 (the
+    batched prefill attending back over rows written by both the first
+    prefill and the decode steps: its f16 K/V copy converts them), and 8
+    more tokens are decoded; logits after each prefill, every greedy token
+    and the K/V rows match the oracle run through the same calls
+    (CausalModel::prefill with start_pos > 0, src/architecture.rs:60-77)."""
+    cfg = tiny_cfg(llrs, hidden_size=1024, num_attention_heads=8, num_key_value_heads=2,
+                   intermediate_size=2048, num_hidden_layers=2, vocab_size=700, seed=67,
+                   recipe=getattr(llrs.LoadQuantization, recipe))
+    model, kv, om = make_pair(llrs, backend, oracle, cfg, tmp_path / "c.gguf", 320)
+    rng = np.random.default_rng(67)
+    p1 = rng.integers(0, cfg.vocab_size, 100).astype(np.uint32)
+    p2 = rng.integers(0, cfg.vocab_size, 150).astype(np.uint32)
+    model.prefill(p1, 0, kv)
+    om.prefill(p1, 0)
+    assert float(np.abs(kv.logits() - om.logits()).max()) <= LOGIT_TOL
+    got = model.decode_greedy(100, 6, kv)
+    np.testing.assert_array_equal(got, om.decode_greedy(100, 6))
+    model.prefill(p2, 106, kv)
+    om.prefill(p2, 106)
+    err = float(np.abs(kv.logits() - om.logits()).max())
+    print(f"[turn2] {recipe}: logits max-abs err after the second prefill {err:.3e}", flush=True)
+    assert err <= LOGIT_TOL
+    got = model.decode_greedy(256, 8, kv)
+    np.testing.assert_array_equal(got, om.decode_greedy(256, 8))
+    for layer in range(cfg.num_hidden_layers):
+        for which in ("k", "v"):
+            a, b = kv.layer(layer, which, 264), om.kv(layer, which, 264)
+            assert float(np.abs(a - b).max()) <= 1e-3 * max(1.0, float(np.abs(b).max()))
+
+
 @pytest.mark.parametrize("hd", [32, 64, 128])
 def test_prefill_attention_f16_and_f32(llrs, backend, oracle, tmp_path, monkeypatch, hd):
     """The batched prefill's two attention kernels -- f16 hi/lo MFMAs over the
