@@ -104,6 +104,7 @@ struct llrs_kv {
         *pf_u = nullptr;
   llrs::f16 *pf_h = nullptr, *pf_hl = nullptr;  // GEMM inputs as f16 hi + lo pairs
   llrs::f16 *pf_xs = nullptr, *pf_xsl = nullptr;  // their 32-column sums (Q4_K products), [pf_cap][pf_ldxs]
+  llrs::f16 *pf_xs2 = nullptr, *pf_xsl2 = nullptr;  // the same for ffn_down's input of the dual gate/up product
   int pf_ldxs = 0;
   llrs::PrefillKvF16 pf_kvf{};  // one layer's K/V rows as f16 hi/lo planes (prefill attention)
   float *pf_part = nullptr;                     // split-K partial tiles of the prefill GEMMs
@@ -1080,8 +1081,12 @@ static int prefill_buffers(llrs_kv *kv) {
   kv->pf_ldxs = (int)(((H > F ? H : F) / 32 + 56 + 7) / 8 * 8);
   LLRS_TRY(A((void **)&kv->pf_xs, T * kv->pf_ldxs * 2));
   LLRS_TRY(A((void **)&kv->pf_xsl, T * kv->pf_ldxs * 2));
+  LLRS_TRY(A((void **)&kv->pf_xs2, T * kv->pf_ldxs * 2));
+  LLRS_TRY(A((void **)&kv->pf_xsl2, T * kv->pf_ldxs * 2));
   LLRS_HIP(hipMemset(kv->pf_xs, 0, T * kv->pf_ldxs * 2));
   LLRS_HIP(hipMemset(kv->pf_xsl, 0, T * kv->pf_ldxs * 2));
+  LLRS_HIP(hipMemset(kv->pf_xs2, 0, T * kv->pf_ldxs * 2));
+  LLRS_HIP(hipMemset(kv->pf_xsl2, 0, T * kv->pf_ldxs * 2));
   {
     const size_t np = (kv->max_seq_len + 15) / 16 * 16, n = np * KV * 2;
     kv->pf_kvf.positions = (int)np;
@@ -1113,11 +1118,11 @@ static int prefill_xsum(llrs_kv *kv, const f16 *a, const f16 *a_lo, int k, int T
 // `xsum`: prefill_xsum has run on this input (Q4_K weights then take the integer-code product).
 static int prefill_gemm(llrs_kv *kv, const llrs_tensor *w, const f16 *a, const f16 *a_lo, int lda,
                         float *c, int ldc, const float *bias, int T, bool accumulate, bool xsum,
-                        hipStream_t s) {
+                        hipStream_t s, bool xs2 = false) {
   PrefillGemmArgs g{};
   if (xsum && w->type == LLRS_Q4_K) {
-    g.xs = kv->pf_xs;
-    g.xs_lo = kv->pf_xsl;
+    g.xs = xs2 ? kv->pf_xs2 : kv->pf_xs;
+    g.xs_lo = xs2 ? kv->pf_xsl2 : kv->pf_xsl;
     g.ldxs = kv->pf_ldxs;
   }
   g.part = kv->pf_part;
@@ -1135,6 +1140,47 @@ static int prefill_gemm(llrs_kv *kv, const llrs_tensor *w, const f16 *a, const f
   g.bias = bias;
   g.t = T;
   g.accumulate = accumulate ? 1 : 0;
+  return launch_prefill_gemm(g, s);
+}
+
+// Whether gate and up run as one dual product with SwiGLU in its epilogue:
+// both Q4_K on their codes, the FFN width a multiple of 64 (unless
+// LLRS_PREFILL_DUAL=0, read per call, for comparisons).
+static bool use_dual_gate_up(const DevLayer &L, int F) {
+  const char *e = getenv("LLRS_PREFILL_DUAL");
+  return !(e && strcmp(e, "0") == 0) && L.gate->type == LLRS_Q4_K && L.up->type == LLRS_Q4_K &&
+         L.gate->row_bytes == L.up->row_bytes && F % 64 == 0 && prefill_codes_enabled();
+}
+
+// silu(gate) * up as f16 pairs into h/hl [T][F] (and, for a Q4_K ffn_down,
+// its 32-column sums into pf_xs2) from the dual product over pf_h.
+static int prefill_gate_up_dual(llrs_kv *kv, const DevLayer &L, int H, int F, int T, f16 *h, f16 *hl,
+                                bool down_xs, hipStream_t s) {
+  PrefillGemmArgs g{};
+  g.part = kv->pf_part;
+  g.part_cap = kv->pf_part_cap;
+  g.a = kv->pf_h;
+  g.a_lo = kv->pf_hl;
+  g.lda = H;
+  g.xs = kv->pf_xs;
+  g.xs_lo = kv->pf_xsl;
+  g.ldxs = kv->pf_ldxs;
+  g.w = L.gate->dev;
+  g.w2 = L.up->dev;
+  g.type = LLRS_Q4_K;
+  g.row_bytes = (long)L.gate->row_bytes;
+  g.dual_rows = F;
+  g.n = 2 * F;
+  g.k = H;
+  g.t = T;
+  g.h = h;
+  g.hl = hl;
+  g.ldh = F;
+  if (down_xs) {
+    g.xso = kv->pf_xs2;
+    g.xso_lo = kv->pf_xsl2;
+    g.ldxso = kv->pf_ldxs;
+  }
   return launch_prefill_gemm(g, s);
 }
 
@@ -1175,12 +1221,21 @@ static int prefill_batched(llrs_model *m, llrs_kv *kv, size_t start, size_t n) {
       xs = needs_xsum({L.gate, L.up});
       LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.ffn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s,
                                        xs ? kv->pf_xs : nullptr, kv->pf_xsl, kv->pf_ldxs));
-      LLRS_TRY(prefill_gemm(kv, L.gate, kv->pf_h, kv->pf_hl, H, kv->pf_g, F, nullptr, T, false, xs, s));
-      LLRS_TRY(prefill_gemm(kv, L.up, kv->pf_h, kv->pf_hl, H, kv->pf_u, F, nullptr, T, false, xs, s));
-      xs = needs_xsum({L.down});
-      LLRS_TRY(launch_swiglu_f16(kv->pf_g, kv->pf_u, kv->pf_h, kv->pf_hl, (size_t)T * F, F, s,
-                                 xs ? kv->pf_xs : nullptr, kv->pf_xsl, kv->pf_ldxs));
-      LLRS_TRY(prefill_gemm(kv, L.down, kv->pf_h, kv->pf_hl, F, kv->pf_x, H, nullptr, T, true, xs, s));
+      if (xs && use_dual_gate_up(L, F)) {
+        // SwiGLU in the product's epilogue: its f16 pairs go to the gate/up
+        // scratch (pf_h is this product's input), the sums to pf_xs2.
+        f16 *h = reinterpret_cast<f16 *>(kv->pf_g), *hl = reinterpret_cast<f16 *>(kv->pf_u);
+        xs = needs_xsum({L.down});
+        LLRS_TRY(prefill_gate_up_dual(kv, L, H, F, T, h, hl, xs, s));
+        LLRS_TRY(prefill_gemm(kv, L.down, h, hl, F, kv->pf_x, H, nullptr, T, true, xs, s, true));
+      } else {
+        LLRS_TRY(prefill_gemm(kv, L.gate, kv->pf_h, kv->pf_hl, H, kv->pf_g, F, nullptr, T, false, xs, s));
+        LLRS_TRY(prefill_gemm(kv, L.up, kv->pf_h, kv->pf_hl, H, kv->pf_u, F, nullptr, T, false, xs, s));
+        xs = needs_xsum({L.down});
+        LLRS_TRY(launch_swiglu_f16(kv->pf_g, kv->pf_u, kv->pf_h, kv->pf_hl, (size_t)T * F, F, s,
+                                   xs ? kv->pf_xs : nullptr, kv->pf_xsl, kv->pf_ldxs));
+        LLRS_TRY(prefill_gemm(kv, L.down, kv->pf_h, kv->pf_hl, F, kv->pf_x, H, nullptr, T, true, xs, s));
+      }
     }
     last_rows = (size_t)T;
   }

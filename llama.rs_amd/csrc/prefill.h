@@ -35,6 +35,17 @@ struct PrefillGemmArgs {
   // runs on the Q4_K codes as exact integers (prefill_codes_enabled()).
   const f16 *xs, *xs_lo;
   int ldxs;
+  // Dual product (gate and up, Q4_K on its codes): w are the gate rows, w2 the
+  // up rows (same k, type and row bytes), n = 2 * dual_rows virtual rows
+  // (each 128-row tile holds 64 gate rows and the same 64 up rows), and the
+  // output is silu(gate) * up as f16 pairs h/hl [t][ldh] instead of c; with
+  // xso set, also its 32-column sums (for a Q4_K ffn_down).
+  const uint8_t *w2;
+  int dual_rows;
+  f16 *h, *hl;
+  int ldh;
+  f16 *xso, *xso_lo;
+  int ldxso;
 };
 
 // Floats of split-K scratch a prefill GEMM may need on this device: one

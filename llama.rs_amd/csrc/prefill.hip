@@ -504,6 +504,67 @@ __global__ __launch_bounds__(512) void prefill_gemm8_kernel(PrefillGemmArgs g) {
 }
 
 
+// The epilogue of a dual gate/up tile without split K: the waves of the up
+// row group (wn = 1) hand their accumulators to the waves of the gate row group
+// with the same tokens through LDS (the same lane and register layout), and
+// those write silu(g) * u as f16 pairs -- the arithmetic of swiglu_f16_kernel,
+// so the values are the same as the separate products followed by it -- and,
+// with xso, the 32-column sums of hi + lo (two 16-row blocks of a lane's
+// column group, reduced over the 16 lanes of each token quad).
+template <int MI, int NJ>
+__device__ __forceinline__ void swiglu_tile(const PrefillGemmArgs &g, const f32x4 (&acc)[MI][NJ], float *xch,
+                                            int wm, int wn, int tb, int lane) {
+#pragma clang fp contract(off)
+  __syncthreads();  // every wave is done with the LDS tiles
+  float *slot = xch + (size_t)wm * (MI * NJ * 4 * 64);
+  if (wn == 1) {
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+      for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) slot[((i * NJ + j) * 4 + e) * 64 + lane] = acc[i][j][e];
+  }
+  __syncthreads();
+  if (wn != 0) return;
+  const int f0 = blockIdx.x * 64;  // the tile's first gate/up row
+#pragma unroll
+  for (int i = 0; i < MI; i++) {
+    float xsum[NJ / 2][4];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      const int f = f0 + 16 * j + (lane & 15);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int t = tb + 16 * i + 4 * (lane >> 4) + e;
+        const float x = acc[i][j][e], u = slot[((i * NJ + j) * 4 + e) * 64 + lane];
+        f16 hi = 0, lo = 0;
+        if (f < g.dual_rows && t < g.t) {
+          split_f16((x / (1.0f + expf(-x))) * u, hi, lo);
+          g.h[(size_t)t * g.ldh + f] = hi;
+          g.hl[(size_t)t * g.ldh + f] = lo;
+        }
+        const float v = (float)hi + (float)lo;
+        if (j % 2 == 0) xsum[j / 2][e] = v;
+        else xsum[j / 2][e] += v;
+      }
+    }
+    if (g.xso) {
+#pragma unroll
+      for (int q = 0; q < NJ / 2; q++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float v = xsum[q][e];
+#pragma unroll
+          for (int m = 8; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+          const int t = tb + 16 * i + 4 * (lane >> 4) + e, f = f0 + 32 * q;
+          if ((lane & 15) == 0 && t < g.t && f < g.dual_rows)
+            split_f16(v, g.xso[(size_t)t * g.ldxso + (f >> 5)], g.xso_lo[(size_t)t * g.ldxso + (f >> 5)]);
+        }
+    }
+  }
+}
+
 // The Q4_K product with the weight codes as exact f16 integers.  A Q4_K
 // weight is d * sc * q - dmin * m (value_at, src/quant.rs:349-456): q < 16 per
 // column, sc and m < 64 per 32-column sub-block s, d and dmin per 256-column
@@ -521,8 +582,9 @@ __global__ __launch_bounds__(512) void prefill_gemm8_kernel(PrefillGemmArgs g) {
 // layout, roles and tiles are those of prefill_gemm8_kernel; K splits into
 // whole super-blocks.  Integer and f16 arithmetic on the codes is exact, so
 // the result differs from the f32 weights' only in f32 rounding.
-template <int BM, int TG>
+template <int BM, int TG, bool DUAL>
 __global__ __launch_bounds__(512) void prefill_gemm_k4_kernel(PrefillGemmArgs g) {
+  static_assert(!DUAL || TG == 4, "dual tiles pair the two row groups of waves");
   // TG token groups x 8/TG row groups of waves: a wave multiplies TW tokens x RW rows.
   constexpr int TW = BM / TG, RW = BN * TG / 8, MI = TW / 16, NJ = RW / 16;
   constexpr int APT = BM / 4, TPR = 64 / APT;
@@ -545,9 +607,11 @@ __global__ __launch_bounds__(512) void prefill_gemm_k4_kernel(PrefillGemmArgs g)
 
   const int ar = st / TPR, ac = (st % TPR) * APT;
   const int wr = st >> 1, wc = (st & 1) * 32;
-  const bool a_ok = t0 + ar < g.t, w_ok = n0 + wr < g.n;
+  // DUAL: tile rows 0-63 are gate rows blockIdx.x * 64 + wr, rows 64-127 the same up rows.
+  const int wrow_i = DUAL ? blockIdx.x * 64 + (wr & 63) : n0 + wr;
+  const bool a_ok = t0 + ar < g.t, w_ok = wrow_i < (DUAL ? g.dual_rows : g.n);
   const int arow = a_ok ? t0 + ar : 0;
-  const uint8_t *wrow = g.w + (size_t)(w_ok ? n0 + wr : 0) * g.row_bytes;
+  const uint8_t *wrow = (DUAL && wr >= 64 ? g.w2 : g.w) + (size_t)(w_ok ? wrow_i : 0) * g.row_bytes;
   union Pre {
     struct { half8 ah[APT / 8], al[APT / 8]; } a;
     struct { uint4 hdr, q0, q1; } w;  // d, dmin, 12 scale bytes; the sub-block pair's 32 code bytes
@@ -736,6 +800,12 @@ __global__ __launch_bounds__(512) void prefill_gemm_k4_kernel(PrefillGemmArgs g)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bl[j], acc[i][j], 0, 0, 0);
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
+    }
+  }
+  if constexpr (DUAL) {
+    if (g.ksplit == 1) {
+      swiglu_tile<MI, NJ>(g, acc, reinterpret_cast<float *>(lds), wm, wn, t0 + wm * TW, lane);
+      return;
     }
   }
   store_tile<MI, NJ>(g, acc, n0 + wn * RW, t0 + wm * TW, lane);
@@ -1268,6 +1338,36 @@ __global__ void split_reduce_kernel(float *__restrict__ c, int ldc, const float 
   *cp = v;
 }
 
+// split_reduce_kernel for a dual gate/up product: row f of gate is virtual
+// column (f / 64) * 128 + f % 64, of up that + 64; h + hl [t][f] = silu(g) * u
+// of the partial sums (split order), as swiglu_tile writes it, and with xso
+// the 32-column sums (half_wave_xsum).
+__global__ __launch_bounds__(256) void split_reduce_swiglu_kernel(const float *__restrict__ part, int nv, int t_rows,
+                                                                  int ksplit, int rows, f16 *__restrict__ h,
+                                                                  f16 *__restrict__ hl, int ldh,
+                                                                  f16 *__restrict__ xso, f16 *__restrict__ xso_lo,
+                                                                  int ldxso) {
+#pragma clang fp contract(off)
+  const int f = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  float v = 0.f;
+  if (f < rows) {
+    const size_t vg = (size_t)(f >> 6) * 128 + (f & 63), zs = (size_t)t_rows * nv;
+    const float *p = part + (size_t)t * nv;
+    float x = 0.f, u = 0.f;
+    for (int z = 0; z < ksplit; z++) {
+      x += p[z * zs + vg];
+      u += p[z * zs + vg + 64];
+    }
+    f16 hi, lo;
+    split_f16((x / (1.0f + expf(-x))) * u, hi, lo);
+    h[(size_t)t * ldh + f] = hi;
+    hl[(size_t)t * ldh + f] = lo;
+    v = (float)hi + (float)lo;
+  }
+  const int f32 = f & ~31;
+  if (xso && f32 < rows) half_wave_xsum(v, f32, xso + (size_t)t * ldxso, xso_lo + (size_t)t * ldxso);
+}
+
 }  // namespace
 
 namespace {
@@ -1299,10 +1399,14 @@ void launch_tiles(const PrefillGemmArgs &a, int bm, hipStream_t s) {
   const bool w8 = eight_waves();
   if (a.type == LLRS_Q4_K && a.xs) {
     const size_t lds4 = lds + 2 * BN * sizeof(float);
-    if (bm == 128)
-      hipLaunchKernelGGL((prefill_gemm_k4_kernel<128, 4>), grid, dim3(512), lds4, s, a);
+    if (a.w2 && bm == 128)
+      hipLaunchKernelGGL((prefill_gemm_k4_kernel<128, 4, true>), grid, dim3(512), lds4, s, a);
+    else if (a.w2)
+      hipLaunchKernelGGL((prefill_gemm_k4_kernel<64, 4, true>), grid, dim3(512), lds4, s, a);
+    else if (bm == 128)
+      hipLaunchKernelGGL((prefill_gemm_k4_kernel<128, 4, false>), grid, dim3(512), lds4, s, a);
     else
-      hipLaunchKernelGGL((prefill_gemm_k4_kernel<64, 4>), grid, dim3(512), lds4, s, a);
+      hipLaunchKernelGGL((prefill_gemm_k4_kernel<64, 4, false>), grid, dim3(512), lds4, s, a);
     return;
   }
 
@@ -1343,7 +1447,11 @@ int launch_split(PrefillGemmArgs a, int bm, int ksplit, hipStream_t s) {
                        a.part_cap, ksplit, a.t, a.n);
   }
   launch_tiles(a, bm, s);
-  if (ksplit > 1)
+  if (ksplit > 1 && a.w2)
+    hipLaunchKernelGGL(split_reduce_swiglu_kernel, dim3((unsigned)((a.dual_rows + 255) / 256), (unsigned)a.t),
+                       dim3(256), 0, s, a.part, a.n, a.t, ksplit, a.dual_rows, a.h, a.hl, a.ldh, a.xso, a.xso_lo,
+                       a.ldxso);
+  else if (ksplit > 1)
     hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((a.n + 255) / 256), (unsigned)a.t), dim3(256), 0,
                        s, a.c, a.ldc, a.bias, a.part, a.n, a.t, ksplit, a.accumulate);
   return LLRS_OK;
@@ -1376,6 +1484,9 @@ int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
   if (g.xs && (g.type != LLRS_Q4_K || g.k % 256 || g.ldxs % 8 || g.ldxs < g.k / 32 + 56))
     return set_error(LLRS_E_UNSUPPORTED, "prefill GEMM: activation sums (ldxs %d) for a type %u product of %d columns",
                      g.ldxs, g.type, g.k);
+  if (g.w2 && (!g.xs || g.dual_rows <= 0 || g.dual_rows % 64 || g.n != 2 * g.dual_rows || !g.h || !g.hl ||
+               (g.xso && g.ldxso < g.dual_rows / 32)))
+    return set_error(LLRS_E_UNSUPPORTED, "prefill GEMM: dual gate/up product of %d rows is not supported", g.dual_rows);
   // 128-token tiles when there are enough of them (the dequantized weight
   // tile then serves twice the tokens), else 64.  Products with fewer tiles
   // than half the slots split K over up to 8 workgroups (at least 6 K chunks
@@ -1396,12 +1507,26 @@ int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
     PrefillGemmArgs m = g;
     m.n = full * BN;
     m.ksplit = 1;
+    if (g.w2) m.dual_rows = full * BN / 2;
     launch_tiles(m, bm, s);
     PrefillGemmArgs r = g;
-    r.w = g.w + (size_t)full * BN * (size_t)g.row_bytes;
-    r.c = g.c + (size_t)full * BN;
-    r.bias = g.bias ? g.bias + (size_t)full * BN : nullptr;
     r.n = g.n - full * BN;
+    if (g.w2) {  // the remaining gate/up rows from full * 64 on
+      const size_t f = (size_t)full * BN / 2;
+      r.w = g.w + f * (size_t)g.row_bytes;
+      r.w2 = g.w2 + f * (size_t)g.row_bytes;
+      r.dual_rows = g.dual_rows - (int)f;
+      r.h = g.h + f;
+      r.hl = g.hl + f;
+      if (g.xso) {
+        r.xso = g.xso + f / 32;
+        r.xso_lo = g.xso_lo + f / 32;
+      }
+    } else {
+      r.w = g.w + (size_t)full * BN * (size_t)g.row_bytes;
+      r.c = g.c + (size_t)full * BN;
+      r.bias = g.bias ? g.bias + (size_t)full * BN : nullptr;
+    }
     LLRS_TRY(launch_split(r, bm, std::max(1, std::min({8, slots / (rem * mt), chunks / 6})), s));
   } else {
     LLRS_TRY(launch_split(g, bm, ks, s));

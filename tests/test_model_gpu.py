@@ -123,6 +123,47 @@ def test_prefill_continued_after_decode(llrs, backend, oracle, tmp_path, recipe)
             assert float(np.abs(a - b).max()) <= 1e-3 * max(1.0, float(np.abs(b).max()))
 
 
+@pytest.mark.parametrize("recipe,ffn,n", [("Q4KM", 18944, 512), ("Q4K", 18944, 512), ("Q4K", 2048, 40)],
+                         ids=["q4km_7b_width", "q4k_7b_width", "q4k_split_k"])
+def test_prefill_dual_gate_up(llrs, backend, oracle, tmp_path, monkeypatch, recipe, ffn, n):
+    """Gate and up as one dual product (each 128-row tile holds 64 gate rows and
+    the same 64 up rows) with SwiGLU in its epilogue, against the separate
+    products and SwiGLU kernel (LLRS_PREFILL_DUAL=0) and the oracle.  Hidden
+    1,536 (24 K chunks): at the 7B FFN width and 512 tokens the 296 dual
+    tiles x 4 token tiles run as two rounds of tiles plus a last launch of
+    40 with K split 3 ways (its reduction applies SwiGLU); at 40 tokens the
+    whole product splits K 4 ways.  The q4k recipe also writes ffn_down's
+    activation sums (Q4_K down) in the epilogue and in the reduction."""
+    cfg = tiny_cfg(llrs, hidden_size=1536, num_attention_heads=12, num_key_value_heads=2,
+                   intermediate_size=ffn, num_hidden_layers=2, max_position_embeddings=1024, seed=71,
+                   recipe=getattr(llrs.LoadQuantization, recipe))
+    cfg.write_gguf(tmp_path / "d.gguf")
+    model = llrs.ModelLoader.load_dynamic(tmp_path / "d.gguf", backend)
+    om = oracle.load(tmp_path / "d.gguf")
+    om.new_state(n + 16)
+    prompt = np.random.default_rng(71).integers(0, cfg.vocab_size, n).astype(np.uint32)
+    om.prefill(prompt, 0)
+    kvs = []
+    for dual in ("1", "0"):
+        monkeypatch.setenv("LLRS_PREFILL_DUAL", dual)
+        kv = llrs.KVCache(model, n + 16)
+        model.prefill(prompt, 0, kv)
+        kvs.append(kv)
+    monkeypatch.delenv("LLRS_PREFILL_DUAL")
+    lo = om.logits()
+    errs = [float(np.abs(kv.logits() - lo).max()) for kv in kvs]
+    diff = float(np.abs(kvs[0].logits() - kvs[1].logits()).max())
+    print(f"[dual] {recipe} F={ffn} n={n}: logits err dual {errs[0]:.3e} separate {errs[1]:.3e}, "
+          f"dual vs separate {diff:.3e}", flush=True)
+    assert max(errs) <= LOGIT_TOL
+    assert diff <= 1e-3
+    for kv in kvs:
+        assert kv.argmax() == om.argmax()
+        for which in ("k", "v"):  # layer 1's rows depend on layer 0's FFN
+            a, b = kv.layer(1, which, n), om.kv(1, which, n)
+            assert float(np.abs(a - b).max()) <= 1e-3 * max(1.0, float(np.abs(b).max()))
+
+
 @pytest.mark.parametrize("hd", [32, 64, 128])
 def test_prefill_attention_f16_and_f32(llrs, backend, oracle, tmp_path, monkeypatch, hd):
     """The batched prefill's two attention kernels -- f16 hi/lo MFMAs over the
