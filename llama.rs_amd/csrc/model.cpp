@@ -1184,6 +1184,54 @@ static int prefill_gate_up_dual(llrs_kv *kv, const DevLayer &L, int H, int F, in
   return launch_prefill_gemm(g, s);
 }
 
+// Q, K (and V when it is Q4_K too) of one input as one segmented Q4_K product
+// over pf_h (one launch and one split-K reduction instead of two or three):
+// when they all run on their codes and every boundary is a multiple of 128
+// rows (unless LLRS_PREFILL_QKV=0, read per call, for comparisons).  Returns
+// whether V was included; sets *done when the product ran.
+static int prefill_qkv_segmented(llrs_kv *kv, const DevLayer &L, int H, int KV, int T, bool &done,
+                                 bool &with_v, hipStream_t s) {
+  done = with_v = false;
+  const char *e = getenv("LLRS_PREFILL_QKV");
+  if ((e && strcmp(e, "0") == 0) || !prefill_codes_enabled() || L.q->type != LLRS_Q4_K ||
+      L.k->type != LLRS_Q4_K || L.k->row_bytes != L.q->row_bytes || H % 128)
+    return LLRS_OK;
+  with_v = L.v->type == LLRS_Q4_K && L.v->row_bytes == L.q->row_bytes && KV % 128 == 0;
+  PrefillGemmArgs g{};
+  g.part = kv->pf_part;
+  g.part_cap = kv->pf_part_cap;
+  g.a = kv->pf_h;
+  g.a_lo = kv->pf_hl;
+  g.lda = H;
+  g.xs = kv->pf_xs;
+  g.xs_lo = kv->pf_xsl;
+  g.ldxs = kv->pf_ldxs;
+  g.w = L.q->dev;
+  g.type = LLRS_Q4_K;
+  g.row_bytes = (long)L.q->row_bytes;
+  g.k = H;
+  g.t = T;
+  g.nseg = with_v ? 3 : 2;
+  const llrs_tensor *w[3] = {L.q, L.k, L.v};
+  float *c[3] = {kv->pf_q, kv->pf_k, kv->pf_v};
+  const float *b[3] = {L.bq, L.bk, L.bv};
+  const int rows[3] = {H, KV, KV}, ldc[3] = {H, KV, KV};
+  g.seg_base[0] = 0;
+  for (int i = 0; i < g.nseg; i++) {
+    g.seg_w[i] = w[i]->dev;
+    g.seg_c[i] = c[i];
+    g.seg_ldc[i] = ldc[i];
+    g.seg_bias[i] = b[i];
+    g.seg_base[i + 1] = g.seg_base[i] + rows[i];
+  }
+  g.n = g.seg_base[g.nseg];
+  g.c = kv->pf_q;  // unused with segments
+  g.ldc = H;
+  LLRS_TRY(launch_prefill_gemm(g, s));
+  done = true;
+  return LLRS_OK;
+}
+
 // CausalModel::prefill (src/architecture.rs:60-77) with the prompt's rows
 // batched through each layer: MFMA dequant-GEMMs for the matrices, causal
 // attention over the cache, then the decode step's fused LM head on the last
@@ -1209,9 +1257,14 @@ static int prefill_batched(llrs_model *m, llrs_kv *kv, size_t start, size_t n) {
       bool xs = needs_xsum({L.q, L.k, L.v});
       LLRS_TRY(launch_rmsnorm_rows_f16(kv->pf_x, L.attn_norm, kv->pf_h, kv->pf_hl, T, H, eps, s,
                                        xs ? kv->pf_xs : nullptr, kv->pf_xsl, kv->pf_ldxs));
-      LLRS_TRY(prefill_gemm(kv, L.q, kv->pf_h, kv->pf_hl, H, kv->pf_q, H, L.bq, T, false, xs, s));
-      LLRS_TRY(prefill_gemm(kv, L.k, kv->pf_h, kv->pf_hl, H, kv->pf_k, KV, L.bk, T, false, xs, s));
-      LLRS_TRY(prefill_gemm(kv, L.v, kv->pf_h, kv->pf_hl, H, kv->pf_v, KV, L.bv, T, false, xs, s));
+      bool qk_done = false, with_v = false;
+      if (xs) LLRS_TRY(prefill_qkv_segmented(kv, L, H, KV, T, qk_done, with_v, s));
+      if (!qk_done) {
+        LLRS_TRY(prefill_gemm(kv, L.q, kv->pf_h, kv->pf_hl, H, kv->pf_q, H, L.bq, T, false, xs, s));
+        LLRS_TRY(prefill_gemm(kv, L.k, kv->pf_h, kv->pf_hl, H, kv->pf_k, KV, L.bk, T, false, xs, s));
+      }
+      if (!with_v)
+        LLRS_TRY(prefill_gemm(kv, L.v, kv->pf_h, kv->pf_hl, H, kv->pf_v, KV, L.bv, T, false, xs, s));
       LLRS_TRY(launch_rope_append(kv->pf_q, kv->pf_k, kv->pf_v, kv->rope, T, st, nh, nkv, hd, kc, vc, s));
       LLRS_TRY(launch_attention_rows(kv->pf_q, kc, vc, T, st, nh, nkv, hd, scale, kv->pf_h, kv->pf_hl, s,
                                      &kv->pf_kvf));

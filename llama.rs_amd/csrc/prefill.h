@@ -46,6 +46,16 @@ struct PrefillGemmArgs {
   int ldh;
   f16 *xso, *xso_lo;
   int ldxso;
+  // Segmented product (Q4_K on its codes, e.g. q, k and v of one input): rows
+  // [seg_base[i], seg_base[i + 1]) of the n come from seg_w[i] and go to
+  // seg_c[i] (row stride seg_ldc[i], bias seg_bias[i] or null); every
+  // boundary but the last a multiple of 128.  nseg = 0: w, c, ldc and bias.
+  int nseg;
+  const uint8_t *seg_w[3];
+  float *seg_c[3];
+  int seg_ldc[3];
+  const float *seg_bias[3];
+  int seg_base[4];
 };
 
 // Floats of split-K scratch a prefill GEMM may need on this device: one

@@ -607,11 +607,16 @@ __global__ __launch_bounds__(512) void prefill_gemm_k4_kernel(PrefillGemmArgs g)
 
   const int ar = st / TPR, ac = (st % TPR) * APT;
   const int wr = st >> 1, wc = (st & 1) * 32;
+  // A segmented product: this tile's segment (boundaries are tile multiples).
+  const int seg = g.nseg > 1 ? (n0 >= g.seg_base[1]) + (g.nseg > 2 && n0 >= g.seg_base[2]) : 0;
+  const int sbase = g.nseg > 0 ? g.seg_base[seg] : 0;
+  const int srows = g.nseg > 0 ? g.seg_base[seg + 1] - sbase : g.n;
+  const uint8_t *wmat = g.nseg > 0 ? g.seg_w[seg] : g.w;
   // DUAL: tile rows 0-63 are gate rows blockIdx.x * 64 + wr, rows 64-127 the same up rows.
-  const int wrow_i = DUAL ? blockIdx.x * 64 + (wr & 63) : n0 + wr;
-  const bool a_ok = t0 + ar < g.t, w_ok = wrow_i < (DUAL ? g.dual_rows : g.n);
+  const int wrow_i = DUAL ? blockIdx.x * 64 + (wr & 63) : n0 - sbase + wr;
+  const bool a_ok = t0 + ar < g.t, w_ok = wrow_i < (DUAL ? g.dual_rows : srows);
   const int arow = a_ok ? t0 + ar : 0;
-  const uint8_t *wrow = (DUAL && wr >= 64 ? g.w2 : g.w) + (size_t)(w_ok ? wrow_i : 0) * g.row_bytes;
+  const uint8_t *wrow = (DUAL && wr >= 64 ? g.w2 : wmat) + (size_t)(w_ok ? wrow_i : 0) * g.row_bytes;
   union Pre {
     struct { half8 ah[APT / 8], al[APT / 8]; } a;
     struct { uint4 hdr, q0, q1; } w;  // d, dmin, 12 scale bytes; the sub-block pair's 32 code bytes
@@ -807,6 +812,15 @@ __global__ __launch_bounds__(512) void prefill_gemm_k4_kernel(PrefillGemmArgs g)
       swiglu_tile<MI, NJ>(g, acc, reinterpret_cast<float *>(lds), wm, wn, t0 + wm * TW, lane);
       return;
     }
+  }
+  if (g.nseg > 0 && g.ksplit == 1) {  // the segment's own output
+    PrefillGemmArgs gs = g;
+    gs.c = g.seg_c[seg];
+    gs.ldc = g.seg_ldc[seg];
+    gs.bias = g.seg_bias[seg];
+    gs.n = srows;
+    store_tile<MI, NJ>(gs, acc, n0 - sbase + wn * RW, t0 + wm * TW, lane);
+    return;
   }
   store_tile<MI, NJ>(g, acc, n0 + wn * RW, t0 + wm * TW, lane);
 }
@@ -1368,6 +1382,29 @@ __global__ __launch_bounds__(256) void split_reduce_swiglu_kernel(const float *_
   if (xso && f32 < rows) half_wave_xsum(v, f32, xso + (size_t)t * ldxso, xso_lo + (size_t)t * ldxso);
 }
 
+// split_reduce_kernel for a segmented product: column j of the partials
+// belongs to segment i (seg_base[i] <= j < seg_base[i + 1]) and goes to
+// seg_c[i] + r * seg_ldc[i] + (j - seg_base[i]), from its bias or 0 (or C
+// when accumulating) plus the partials in split order.
+struct SegOut {
+  float *c[3];
+  int ldc[3];
+  const float *bias[3];
+  int base[4];
+  int nseg;
+};
+__global__ void split_reduce_seg_kernel(SegOut o, const float *__restrict__ part, int n, int t, int ksplit,
+                                        int accumulate) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+  if (j >= n || r >= t) return;
+  const int s = (o.nseg > 1 && j >= o.base[1]) + (o.nseg > 2 && j >= o.base[2]);
+  const int jl = j - o.base[s];
+  float *cp = o.c[s] + (size_t)r * o.ldc[s] + jl;
+  float v = accumulate ? *cp : (o.bias[s] ? o.bias[s][jl] : 0.f);
+  for (int z = 0; z < ksplit; z++) v += part[((size_t)z * t + r) * n + j];
+  *cp = v;
+}
+
 }  // namespace
 
 namespace {
@@ -1451,7 +1488,18 @@ int launch_split(PrefillGemmArgs a, int bm, int ksplit, hipStream_t s) {
     hipLaunchKernelGGL(split_reduce_swiglu_kernel, dim3((unsigned)((a.dual_rows + 255) / 256), (unsigned)a.t),
                        dim3(256), 0, s, a.part, a.n, a.t, ksplit, a.dual_rows, a.h, a.hl, a.ldh, a.xso, a.xso_lo,
                        a.ldxso);
-  else if (ksplit > 1)
+  else if (ksplit > 1 && a.nseg > 0) {
+    SegOut o{};
+    o.nseg = a.nseg;
+    for (int i = 0; i < a.nseg; i++) {
+      o.c[i] = a.seg_c[i];
+      o.ldc[i] = a.seg_ldc[i];
+      o.bias[i] = a.seg_bias[i];
+    }
+    for (int i = 0; i <= a.nseg; i++) o.base[i] = a.seg_base[i];
+    hipLaunchKernelGGL(split_reduce_seg_kernel, dim3((unsigned)((a.n + 255) / 256), (unsigned)a.t), dim3(256), 0,
+                       s, o, a.part, a.n, a.t, ksplit, a.accumulate);
+  } else if (ksplit > 1)
     hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((a.n + 255) / 256), (unsigned)a.t), dim3(256), 0,
                        s, a.c, a.ldc, a.bias, a.part, a.n, a.t, ksplit, a.accumulate);
   return LLRS_OK;
@@ -1503,7 +1551,12 @@ int launch_prefill_gemm(const PrefillGemmArgs &g, hipStream_t s) {
   const int per_round = slots / mt;  // row tiles per round of slots
   const int full = (ks == 1 && per_round > 0) ? ntiles / per_round * per_round : 0;
   const int rem = ntiles - full;
-  if (full > 0 && rem > 0 && rem * mt * 2 <= slots) {
+  if (g.nseg > 0 && (g.type != LLRS_Q4_K || !g.xs || g.nseg > 3 || g.seg_base[0] != 0 || g.seg_base[g.nseg] != g.n))
+    return set_error(LLRS_E_UNSUPPORTED, "prefill GEMM: segmented product of %d segments is not supported", g.nseg);
+  for (int i = 1; i < g.nseg; i++)
+    if (g.seg_base[i] % BN || g.seg_base[i] <= g.seg_base[i - 1])
+      return set_error(LLRS_E_UNSUPPORTED, "prefill GEMM: segment boundary %d is not a multiple of %d", g.seg_base[i], BN);
+  if (g.nseg == 0 && full > 0 && rem > 0 && rem * mt * 2 <= slots) {
     PrefillGemmArgs m = g;
     m.n = full * BN;
     m.ksplit = 1;

@@ -164,6 +164,46 @@ def test_prefill_dual_gate_up(llrs, backend, oracle, tmp_path, monkeypatch, reci
             assert float(np.abs(a - b).max()) <= 1e-3 * max(1.0, float(np.abs(b).max()))
 
 
+@pytest.mark.parametrize("recipe,hidden,n", [("Q4KM", 1024, 40), ("Q4K", 1024, 300), ("Q4K", 256, 40)],
+                         ids=["q_k_split_k", "q_k_v_split_k", "q_k_v_direct"])
+def test_prefill_qkv_segmented(llrs, backend, oracle, tmp_path, monkeypatch, recipe, hidden, n):
+    """Q and K (q4km: V is Q8_0) or Q, K and V (q4k) as one segmented Q4_K
+    product, each 128-row tile in one segment, against the separate products
+    (LLRS_PREFILL_QKV=0) and the oracle: hidden 1,024 splits K (the reduction
+    writes each segment's columns to its own output with its bias), hidden 256
+    does not (each tile writes its segment directly).  Layer 0's K and V rows
+    come straight from the product."""
+    cfg = tiny_cfg(llrs, hidden_size=hidden, num_attention_heads=hidden // 64 if hidden < 1024 else 8,
+                   num_key_value_heads=2, intermediate_size=1024, num_hidden_layers=2, seed=73,
+                   recipe=getattr(llrs.LoadQuantization, recipe))
+    cfg.write_gguf(tmp_path / "q.gguf")
+    model = llrs.ModelLoader.load_dynamic(tmp_path / "q.gguf", backend)
+    om = oracle.load(tmp_path / "q.gguf")
+    om.new_state(n + 16)
+    prompt = np.random.default_rng(73).integers(0, cfg.vocab_size, n).astype(np.uint32)
+    om.prefill(prompt, 0)
+    kvs = []
+    for seg in ("1", "0"):
+        monkeypatch.setenv("LLRS_PREFILL_QKV", seg)
+        kv = llrs.KVCache(model, n + 16)
+        model.prefill(prompt, 0, kv)
+        kvs.append(kv)
+    monkeypatch.delenv("LLRS_PREFILL_QKV")
+    lo = om.logits()
+    errs = [float(np.abs(kv.logits() - lo).max()) for kv in kvs]
+    diff = float(np.abs(kvs[0].logits() - kvs[1].logits()).max())
+    print(f"[qkv] {recipe} H={hidden} n={n}: logits err segmented {errs[0]:.3e} separate {errs[1]:.3e}, "
+          f"segmented vs separate {diff:.3e}", flush=True)
+    assert max(errs) <= LOGIT_TOL
+    assert diff <= 1e-3
+    for kv in kvs:
+        assert kv.argmax() == om.argmax()
+        for layer in range(cfg.num_hidden_layers):
+            for which in ("k", "v"):
+                a, b = kv.layer(layer, which, n), om.kv(layer, which, n)
+                assert float(np.abs(a - b).max()) <= 1e-3 * max(1.0, float(np.abs(b).max()))
+
+
 @pytest.mark.parametrize("hd", [32, 64, 128])
 def test_prefill_attention_f16_and_f32(llrs, backend, oracle, tmp_path, monkeypatch, hd):
     """The batched prefill's two attention kernels -- f16 hi/lo MFMAs over the
