@@ -111,15 +111,21 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
   const int vd = (lane % VL) * VW, vr0 = lane / VL;
   float4 kr[NK4];
   VT vv[NVI];
-  auto load_rows = [&](int s0, int s1) {
+  auto load_k = [&](int s0, int s1) {
     const float *kp = kc + (size_t)(s0 + pl < s1 ? s0 + pl : s0) * kvw + half * KH;
 #pragma unroll
     for (int j = 0; j < NK4; j++) kr[j] = *reinterpret_cast<const float4 *>(kp + 4 * j);
+  };
+  auto load_v = [&](int s0, int s1) {
 #pragma unroll
     for (int i = 0; i < NVI; i++) {
       const int p = s0 + i * RV + vr0;
       vv[i] = *reinterpret_cast<const VT *>(vc + (size_t)(p < s1 ? p : s0) * kvw + vd);
     }
+  };
+  auto load_rows = [&](int s0, int s1) {
+    load_k(s0, s1);
+    load_v(s0, s1);
   };
   // This step's query, key and value (ordinary loads: no workgroup of the
   // launch reads them before they are written).
@@ -138,10 +144,21 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
     // The cache rows before this step's position were written by earlier
     // steps, so their loads go out before the caller waits for this step's
     // query, key and value (`wait`: the persistent kernel's barrier; the row
-    // at pos is taken from those, not from the cache).
-    load_rows(c0, min(c0 + kChunk, pos + 1));
-    wait();
-    load_new();
+    // at pos is taken from those, not from the cache).  From kSplitLoadsFrom
+    // positions only the key rows do and the value rows follow the wait:
+    // with both in flight (8 MB per layer at 4,000 positions of the 1.5B
+    // shape) the barrier's release waits behind them.
+    const int s1 = min(c0 + kChunk, pos + 1);
+    if (pos >= kSplitLoadsFrom) {
+      load_k(c0, s1);
+      wait();
+      load_new();
+      load_v(c0, s1);
+    } else {
+      load_rows(c0, s1);
+      wait();
+      load_new();
+    }
   } else {
     wait();
     load_new();

@@ -24,6 +24,10 @@ __host__ __device__ inline int attention_span(int pos, int nh) {
 // the head's last item (one round of loads per level instead of one per 16
 // partials).
 constexpr int kGroup = 16, kGroupFrom = 64;
+// From this position the persistent kernel issues an attention item's key
+// rows before the phase barrier and its value rows after it; at earlier
+// positions it issues both before the barrier.
+constexpr int kSplitLoadsFrom = 1024;
 __host__ __device__ inline int attention_groups(int max_chunks) { return (max_chunks + kGroup - 1) / kGroup; }
 
 // Fused RoPE + KV append + GQA attention of one layer.
