@@ -148,11 +148,10 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
       a.k_cache += l * p.cache_stride;
       a.v_cache += l * p.cache_stride;
       a.tag = epoch * (unsigned)p.nlayers + (unsigned)l;
-      // Every wave passes the barrier once.  In the short-context
-      // instantiation a wave waits inside its first item, after that item's
-      // cache loads are issued (rows written by earlier steps), or after the
-      // loop when it has no item; the LONG one waits first (holding the rows
-      // across the wait would spill registers there).
+      // Every wave passes the barrier once: inside its first item, after that
+      // item's cache loads are issued (rows written by earlier steps; from
+      // kSplitLoadsFrom positions only the key rows), or after the loop when
+      // it has no item.
       bool waited = false;
       auto wait = [&] {
         if (!waited) {
@@ -161,7 +160,6 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
           waited = true;
         }
       };
-      if constexpr (LONG) wait();
       const bool multi = span > 1;
       for (int it = wave * nwg + wg; it < n_items; it += nwg * nwv) {
         const int r = it >> 3, pair = (r / G) * 8 + (it & 7);
@@ -169,14 +167,14 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
         const int hh = (pair % a.nkv) * G + r % G, item = pair / a.nkv;
         if constexpr (LONG) {
           if (multi)
-            attention_item<HD, true, true>(a, hh, item, pos, aqs[wave], akn[wave]);
+            attention_item<HD, true, true, true>(a, hh, item, pos, aqs[wave], akn[wave], wait);
           else
-            attention_item<HD, true, false>(a, hh, item, pos, aqs[wave], akn[wave]);
+            attention_item<HD, true, false, true>(a, hh, item, pos, aqs[wave], akn[wave], wait);
         } else {
           attention_item<HD, true, false, true>(a, hh, item, pos, aqs[wave], akn[wave], wait);
         }
       }
-      if constexpr (!LONG) wait();
+      wait();
       bar_arrive(p.bar, wg, k);
       k++;
     }
