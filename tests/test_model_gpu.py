@@ -366,6 +366,42 @@ def test_persistent_decode_matches_per_phase(llrs, backend, tmp_path, monkeypatc
             np.testing.assert_array_equal(kv_p.layer(layer, which, n), kv_s.layer(layer, which, n))
 
 
+@pytest.mark.parametrize("case", [
+    dict(geom=dict(seed=21), prompt=1000, steps=48),
+    dict(geom=dict(hidden_size=1024, num_attention_heads=16, num_key_value_heads=2, intermediate_size=1024,
+                   num_hidden_layers=1, vocab_size=600, seed=22), prompt=4080, steps=32),
+], ids=["split_at_1024", "multi_chunk_at_4096"])
+def test_persistent_split_loads_match_per_phase(llrs, backend, tmp_path, monkeypatch, case):
+    """From 1,024 positions the persistent kernel issues an attention item's
+    key rows before the phase barrier and its value rows after it (below
+    1,024 both before); past 2,048 items (16 heads at 4,096 positions) the
+    multi-chunk instantiation does the same for its first sub-chunk.  The
+    per-phase path loads both inside its attention launch.  Decoding across
+    either position on both paths gives bit-identical tokens, logits and K/V
+    rows."""
+    cfg = tiny_cfg(llrs, max_position_embeddings=8192, **case["geom"])
+    cfg.write_gguf(tmp_path / "s.gguf")
+    model = llrs.ModelLoader.load_dynamic(tmp_path / "s.gguf", backend)
+    ctx = case["prompt"] + case["steps"] + 8
+    kv_p = llrs.KVCache(model, ctx)
+    monkeypatch.setenv("LLRS_NO_PERSISTENT", "1")
+    kv_s = llrs.KVCache(model, ctx)
+    monkeypatch.delenv("LLRS_NO_PERSISTENT")
+    assert kv_p.persistent and not kv_s.persistent
+    prompt = np.random.default_rng(case["geom"]["seed"]).integers(0, cfg.vocab_size, case["prompt"]).astype(np.uint32)
+    print(f"[split loads] prompt {len(prompt)} steps {case['steps']}", flush=True)
+    for kv in (kv_p, kv_s):
+        model.prefill(prompt, 0, kv)
+    got = model.decode_greedy(len(prompt), case["steps"], kv_p)
+    want = model.decode_greedy(len(prompt), case["steps"], kv_s)
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(kv_p.logits(), kv_s.logits())
+    n = len(prompt) + case["steps"]
+    for layer in (0, cfg.num_hidden_layers - 1):
+        for which in ("k", "v"):
+            np.testing.assert_array_equal(kv_p.layer(layer, which, n), kv_s.layer(layer, which, n))
+
+
 def test_model_error_paths(llrs, backend, tmp_path):
     cfg = tiny_cfg(llrs, seed=17)
     cfg.write_gguf(tmp_path / "e.gguf")
