@@ -60,6 +60,11 @@ typedef struct {
 } llrs_backend_config;
 
 int llrs_backend_create(const llrs_backend_config *cfg, llrs_backend **out);
+/* Drop (src/backend.rs's Arc<dyn KernelBackend> going out of scope): releases
+ * the caller's handle.  Every tensor, model and KV cache made from the
+ * backend holds a counted reference to it, as Qwen2Model holds an Arc of its
+ * backend (src/model.rs:117; src/loader.rs:99, 242), so the device state
+ * lives until the last of them is freed, in any order. */
 void llrs_backend_destroy(llrs_backend *b);
 /* KernelBackend::name (src/backend.rs:70): "hip-gfx950". */
 const char *llrs_backend_name(const llrs_backend *b);
@@ -166,6 +171,8 @@ int llrs_hf_config_read(const char *config_json_path, llrs_model_config *out);
 int llrs_safetensors_read_tensor(const char *model_dir, const char *name, uint32_t *ggml_type,
                                  size_t *shape, size_t *ndim, void *out, size_t out_capacity,
                                  size_t *nbytes);
+/* Releases the caller's handle; KV caches made from the model keep it (and
+ * its backend) alive until they are freed. */
 void llrs_model_free(llrs_model *m);
 int llrs_model_config_get(const llrs_model *m, llrs_model_config *out);
 /* Bytes of weights the decode step streams per token (all matrices incl.
@@ -198,6 +205,7 @@ int llrs_model_export_gguf(const llrs_model *m, const char *path);
  * reference's, plus device activation buffers.  Fails if max_seq_len is 0 or
  * exceeds max_position_embeddings (src/cache.rs:14-19). */
 int llrs_kv_create(llrs_model *m, size_t max_seq_len, llrs_kv **out);
+/* Frees the cache and releases its reference to the model. */
 void llrs_kv_free(llrs_kv *kv);
 /* KVCache::reset (src/cache.rs:55-57): the rows are kept (positions are
  * overwritten before they are read); the device's wait flags (below) are

@@ -292,6 +292,7 @@ class DeviceTensor:
                                         buf.size, int(tensor.quant_type), tensor.rows(),
                                         tensor.cols(), C.byref(h)))
         self.handle = h
+        self._free = lib().llrs_tensor_free  # bound now: usable at interpreter shutdown
         self.nbytes = buf.size
 
     def rows(self) -> int:
@@ -311,9 +312,11 @@ class DeviceTensor:
                                       output.size))
 
     def __del__(self):
-        h = getattr(self, "handle", None)
-        if h and _lib is not None:
-            _lib.llrs_tensor_free(h)
+        # The C side counts references (a tensor keeps its backend alive), so
+        # finalizers may run in any order, at interpreter shutdown too.
+        h, free = getattr(self, "handle", None), getattr(self, "_free", None)
+        if h and free is not None:
+            free(h)
             self.handle = None
 
 
@@ -325,6 +328,7 @@ class HipBackend(KernelBackend):
         h = P()
         _check(lib().llrs_backend_create(C.byref(cfg), C.byref(h)))
         self.handle = h
+        self._free = lib().llrs_backend_destroy
 
     def name(self) -> str:
         return lib().llrs_backend_name(self.handle).decode()
@@ -349,9 +353,11 @@ class HipBackend(KernelBackend):
         _check(lib().llrs_backend_synchronize(self.handle))
 
     def __del__(self):
-        h = getattr(self, "handle", None)
-        if h and _lib is not None:
-            _lib.llrs_backend_destroy(h)
+        # Releases this handle only: models, caches and tensors made from the
+        # backend hold their own references to it (any finalization order).
+        h, free = getattr(self, "handle", None), getattr(self, "_free", None)
+        if h and free is not None:
+            free(h)
             self.handle = None
 
 

@@ -71,6 +71,7 @@ int tensor_alloc(llrs_backend *b, uint32_t ty, size_t rows, size_t cols, llrs_te
   llrs_tensor *t = new (std::nothrow) llrs_tensor();
   if (!t) return set_error(LLRS_E_OOM, "out of host memory");
   t->b = b;
+  backend_retain(b);
   t->type = ty;
   t->rows = rows;
   t->cols = cols;
@@ -78,6 +79,7 @@ int tensor_alloc(llrs_backend *b, uint32_t ty, size_t rows, size_t cols, llrs_te
   t->nbytes = t->row_bytes * rows;
   hipError_t e = hipMalloc(&t->dev, t->nbytes + kTensorTailPad);
   if (e != hipSuccess) {
+    backend_release(b);
     delete t;
     return set_error(e == hipErrorOutOfMemory ? LLRS_E_OOM : LLRS_E_HIP,
                      "hipMalloc(%zu) failed: %s", rows * row_bytes(ty, cols) + kTensorTailPad,
@@ -86,11 +88,24 @@ int tensor_alloc(llrs_backend *b, uint32_t ty, size_t rows, size_t cols, llrs_te
   e = hipMemsetAsync(t->dev + t->nbytes, 0, kTensorTailPad, b->stream);
   if (e != hipSuccess) {
     (void)hipFree(t->dev);
+    backend_release(b);
     delete t;
     return set_error(LLRS_E_HIP, "hipMemsetAsync failed: %s", hipGetErrorString(e));
   }
   *out = t;
   return LLRS_OK;
+}
+
+void backend_retain(llrs_backend *b) { b->refs.fetch_add(1, std::memory_order_relaxed); }
+
+void backend_release(llrs_backend *b) {
+  if (b->refs.fetch_sub(1, std::memory_order_acq_rel) != 1) return;
+  (void)hipSetDevice(b->device);
+  (void)hipStreamSynchronize(b->stream);
+  if (b->x_dev) (void)hipFree(b->x_dev);
+  if (b->y_dev) (void)hipFree(b->y_dev);
+  (void)hipStreamDestroy(b->stream);
+  delete b;
 }
 
 }  // namespace llrs
@@ -130,14 +145,10 @@ int llrs_backend_create(const llrs_backend_config *cfg, llrs_backend **out) {
   return LLRS_OK;
 }
 
+// Releases the creator's handle; models, caches and tensors made from the
+// backend keep it alive until they are freed.
 void llrs_backend_destroy(llrs_backend *b) {
-  if (!b) return;
-  (void)hipSetDevice(b->device);
-  (void)hipStreamSynchronize(b->stream);
-  if (b->x_dev) (void)hipFree(b->x_dev);
-  if (b->y_dev) (void)hipFree(b->y_dev);
-  (void)hipStreamDestroy(b->stream);
-  delete b;
+  if (b) backend_release(b);
 }
 
 const char *llrs_backend_name(const llrs_backend *b) { return b ? b->name.c_str() : ""; }
@@ -179,8 +190,7 @@ int llrs_tensor_upload(llrs_backend *b, const void *bytes, size_t nbytes, uint32
     e = hipMemcpyAsync(t->dev, bytes, nbytes, hipMemcpyHostToDevice, b->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(b->stream);
   if (e != hipSuccess) {
-    (void)hipFree(t->dev);
-    delete t;
+    llrs_tensor_free(t);
     return set_error(LLRS_E_HIP, "tensor upload failed: %s", hipGetErrorString(e));
   }
   *out = t;
@@ -189,10 +199,12 @@ int llrs_tensor_upload(llrs_backend *b, const void *bytes, size_t nbytes, uint32
 
 void llrs_tensor_free(llrs_tensor *t) {
   if (!t) return;
-  (void)hipSetDevice(t->b->device);
-  (void)hipStreamSynchronize(t->b->stream);
+  llrs_backend *b = t->b;
+  (void)hipSetDevice(b->device);
+  (void)hipStreamSynchronize(b->stream);
   (void)hipFree(t->dev);
   delete t;
+  backend_release(b);
 }
 
 int llrs_tensor_info(const llrs_tensor *t, uint32_t *ty, size_t *rows, size_t *cols,

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <string>
@@ -80,7 +81,16 @@ void clear_error();
 constexpr size_t kTensorTailPad = 256;
 
 // Allocates an uninitialised device tensor of native layout (tail pad zeroed).
+// The tensor holds a counted reference to its backend.
 int tensor_alloc(llrs_backend *b, uint32_t ty, size_t rows, size_t cols, llrs_tensor **out);
+
+// Counted ownership of a backend, as the reference's Arc<dyn KernelBackend>
+// held by every model (src/model.rs:117, src/loader.rs:99, 242): the
+// creator's handle, every tensor and every model hold one reference each,
+// and the device state is released with the last of them, so destroying the
+// backend handle while a model or cache still uses it only drops the handle.
+void backend_retain(llrs_backend *b);
+void backend_release(llrs_backend *b);
 
 }  // namespace llrs
 
@@ -96,6 +106,7 @@ struct llrs_backend {
   // Scratch device buffers for the host-pointer matvec entry point.
   float *x_dev = nullptr, *y_dev = nullptr;
   size_t x_cap = 0, y_cap = 0;
+  std::atomic<int> refs{1};  // the creator's handle + one per tensor and model
 };
 
 struct llrs_tensor {

@@ -160,6 +160,48 @@ template <bool COH> __device__ __forceinline__ void st_u4(uint8_t *p, uint4 v) {
   }
 }
 
+// A value with its tag in one single-copy-atomic 64-bit word: producers and
+// consumers in one launch (the persistent decode kernel, the attention merge)
+// meet without counters.  A consumer reads the word with a device-scope load
+// until the high half is the step's tag; no value is ever seen with another
+// step's tag.
+__device__ __forceinline__ void store_tagged(unsigned long long *p, float v, unsigned tag) {
+  __hip_atomic_store(p, ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_tagged(const unsigned long long *p, unsigned tag, bool &ok) {
+  const unsigned long long w =
+      __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  ok = ok && (unsigned)(w >> 32) == tag;
+  return __uint_as_float((unsigned)w);
+}
+
+// Whether a wait for tagged words has gone on for ~20 ms (the 100 MHz wall
+// clock); then *err is set and the waiter goes on with what it read.
+__device__ __forceinline__ bool tagged_wait_over(unsigned long long &t0, unsigned *err) {
+  const unsigned long long t = wall_clock64();
+  if (!t0) t0 = t;
+  if (t - t0 < 2000000ull) return false;
+  if (err && (thread_x() & 63) == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
+// A dword read through the scalar memory path with glc (the scalar cache is
+// bypassed): a poll that does not queue behind the vector loads of the CU it
+// runs on.  Only for words in uncached device memory (no L2 keeps a copy)
+// that other workgroups change with device-scope atomics.  p is uniform.
+__device__ __forceinline__ const unsigned *uniform_ptr(const unsigned *p) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(p);
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+  return reinterpret_cast<const unsigned *>(((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ unsigned poll_scalar_u32(const unsigned *p) {
+  unsigned v;
+  asm volatile("s_load_dword %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=&s"(v) : "s"(uniform_ptr(p)) : "memory");
+  return v;
+}
+
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 // Nine dwords from the dword holding p (p 2-byte aligned): raw[0..8].

@@ -115,6 +115,7 @@ class HipQwen2Model:
     def __init__(self, backend: HipBackend, handle):
         self._backend = backend
         self.handle = handle
+        self._free = lib().llrs_model_free
         c = _ModelConfig()
         _check(lib().llrs_model_config_get(handle, C.byref(c)))
         self._config = _config_from_c(c)
@@ -178,9 +179,11 @@ class HipQwen2Model:
         return us.value, nb.value
 
     def __del__(self):
-        h = getattr(self, "handle", None)
-        if h and lib is not None:
-            lib().llrs_model_free(h)
+        # Caches hold their own reference to the model on the C side, so the
+        # finalizers may run in any order (at interpreter shutdown too).
+        h, free = getattr(self, "handle", None), getattr(self, "_free", None)
+        if h and free is not None:
+            free(h)
             self.handle = None
 
 
@@ -191,6 +194,7 @@ class KVCache:
         h = P()
         _check(lib().llrs_kv_create(model.handle, max_seq_len, C.byref(h)))
         self.handle = h
+        self._free = lib().llrs_kv_free
         self.model = model
         self.max_seq_len = max_seq_len
 
@@ -237,9 +241,9 @@ class KVCache:
         return out.reshape(n_pos, cfg.kv_width)
 
     def __del__(self):
-        h = getattr(self, "handle", None)
-        if h:
-            lib().llrs_kv_free(h)
+        h, free = getattr(self, "handle", None), getattr(self, "_free", None)
+        if h and free is not None:
+            free(h)
             self.handle = None
 
 
