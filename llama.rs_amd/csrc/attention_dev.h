@@ -57,21 +57,16 @@ __device__ __forceinline__ bool merge_wait_over(unsigned long long &t0, unsigned
 // stored at device scope.  qs and kn are the wave's own LDS (HD floats each).
 // MULTI: the instantiation for attention_span(pos, nh) > 1 (the other one
 // assumes single-chunk items and keeps their code straight-line).
-// TAGGED: this step's q|k|v arrive as tagged words (a.qkv_t, written by
-// other workgroups of the launch: the item reads them once every tag is the
-// step's, instead of after a barrier).  The head's output leaves as tagged
-// words when a.out_t is set, else as floats in a.out; with a.out_cnt set,
-// the wave that stores a head's output then adds 1 to the counter of the
-// head's group (a.out_cnt[h / a.out_group_heads]) once its stores are
-// complete, for the o_proj tiles that wait on the group.
-// The item contains no workgroup barrier (the persistent kernel's waves run
-// different numbers of items), and an EARLY item calls `wait` exactly once on
-// every path that passes the c0 > pos check.
+// EARLY (the persistent kernel): `wait` is the phase barrier, which ends in a
+// workgroup barrier.  The hardware's s_barrier counts waves, not call sites,
+// and waves run different numbers of items, so an item contains no
+// workgroup barrier of its own and calls `wait` exactly once on every path
+// past the c0 > pos check (a wave with no item waits after its item loop).
 struct NoWait {
   __device__ void operator()() const {}
 };
 
-template <int HD, bool COH, bool MULTI, bool EARLY = false, bool TAGGED = false, class Wait = NoWait>
+template <int HD, bool COH, bool MULTI, bool EARLY = false, class Wait = NoWait>
 __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, float *qs, float *kn,
                                Wait &&wait = Wait{}) {
   constexpr int KH = HD / 2;              // dimensions per score lane
@@ -101,6 +96,7 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
   //    and masked later.
   const int ri = lane & (KH - 1);
   const float *cs = a.rope + (size_t)pos * HD, *sn = cs + KH;
+  const float *qx = a.q + (size_t)h * HD, *kx = a.k + kvh * HD, *vx = a.v + kvh * HD;
   const int vd = (lane % VL) * VW, vr0 = lane / VL;
   float4 kr[NK4];
   VT vv[NVI];
@@ -121,38 +117,17 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
     load_v(s0, s1);
   };
   // This step's query, key and value (ordinary loads: no workgroup of the
-  // launch reads them before they are written), or, TAGGED, the tagged words
-  // read until every tag is this step's.
+  // launch reads them before they are written).
   float q_re, q_im, k_re, k_im, rc, rs;
   VT vnew;
   auto load_new = [&] {
+    q_re = qx[ri];
+    q_im = qx[ri + KH];
+    k_re = kx[ri];
+    k_im = kx[ri + KH];
     rc = cs[ri];
     rs = sn[ri];
-    if constexpr (TAGGED) {
-      const unsigned long long *qt = a.qkv_t + (size_t)h * HD;
-      const unsigned long long *kt = a.qkv_t + (size_t)a.nh * HD + kvh * HD;
-      const unsigned long long *vt = kt + (size_t)a.nkv * HD;
-      float *vn = reinterpret_cast<float *>(&vnew);
-      unsigned long long t0 = 0;
-      while (true) {
-        bool ok = true;
-        q_re = load_tagged(qt + ri, a.tag, ok);
-        q_im = load_tagged(qt + ri + KH, a.tag, ok);
-        k_re = load_tagged(kt + ri, a.tag, ok);
-        k_im = load_tagged(kt + ri + KH, a.tag, ok);
-#pragma unroll
-        for (int k = 0; k < VW; k++) vn[k] = load_tagged(vt + vd + k, a.tag, ok);
-        if (__all(ok) || merge_wait_over(t0, a.err)) break;
-        __builtin_amdgcn_s_sleep(1);
-      }
-    } else {
-      const float *qx = a.q + (size_t)h * HD, *kx = a.k + kvh * HD, *vx = a.v + kvh * HD;
-      q_re = qx[ri];
-      q_im = qx[ri + KH];
-      k_re = kx[ri];
-      k_im = kx[ri + KH];
-      vnew = *reinterpret_cast<const VT *>(vx + vd);
-    }
+    vnew = *reinterpret_cast<const VT *>(vx + vd);
   };
   if constexpr (EARLY) {
     // The cache rows before this step's position were written by earlier
@@ -285,28 +260,13 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
     }
   }
 
-  // The head's output: plain (device-scope with COH) floats, or tagged words;
-  // then the group counter, once the wave's stores are complete.
-  auto put = [&](int d, float v) {
-    if (a.out_t)
-      store_tagged(a.out_t + (size_t)h * HD + d, v, a.tag);
-    else
-      st_act<COH>(a.out + (size_t)h * HD + d, v);
-  };
-  auto signal = [&] {
-    if (a.out_cnt) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      if (lane == 0)
-        __hip_atomic_fetch_add(a.out_cnt + h / a.out_group_heads, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  };
+  float *out = a.out + (size_t)h * HD;
   if (n_active == 1) {  // the only chunk: finish here
     if (lane < VL) {
       const bool ok = isfinite(l) && l > 0.f;
 #pragma unroll
-      for (int k = 0; k < VW; k++) put(vd + k, ok ? O[k] / l : Vs[k] / (float)(pos + 1));
+      for (int k = 0; k < VW; k++) st_act<COH>(out + vd + k, ok ? O[k] / l : Vs[k] / (float)(pos + 1));
     }
-    signal();
     return;
   }
 
@@ -429,7 +389,7 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
   if (lane < VL) {
     if (isfinite(L) && L > 0.f) {
 #pragma unroll
-      for (int k = 0; k < VW; k++) put(vd + k, R[k] / L);
+      for (int k = 0; k < VW; k++) st_act<COH>(out + vd + k, R[k] / L);
     } else {
       float V[VW];
 #pragma unroll
@@ -447,10 +407,9 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
         for (int k = 0; k < VW; k++) V[k] += vc[k];
       }
 #pragma unroll
-      for (int k = 0; k < VW; k++) put(vd + k, V[k] / (float)(pos + 1));
+      for (int k = 0; k < VW; k++) st_act<COH>(out + vd + k, V[k] / (float)(pos + 1));
     }
   }
-  signal();
 }
 
 }  // namespace llrs

@@ -49,15 +49,6 @@ struct AttnArgs {
   int max_chunks;            // attention_chunks(max_seq)
   long part_stride;          // attention_part_stride(hd): words per (head, chunk) partial
   float scale;               // 1/sqrt(hd)
-  // Persistent decode kernel: this step's q | k | v ([nh*hd | nkv*hd |
-  // nkv*hd]) as tagged words (value | tag << 32) in place of q/k/v; the
-  // heads' outputs ([nh*hd]) as tagged words in place of out (when out_t is
-  // set); per group of out_group_heads heads, a counter of heads whose output
-  // is stored (when out_cnt is set).
-  const unsigned long long *qkv_t;
-  unsigned long long *out_t;
-  unsigned *out_cnt;
-  int out_group_heads;
 };
 
 // Also advances *epoch (the attention partials' tag) and zeroes

@@ -1,6 +1,6 @@
 // The persistent decode kernel: every layer of one token's step
 // (Qwen2Model::forward_impl, src/model.rs:173-261) in one launch of one
-// workgroup per CU, three device-wide barriers per layer.
+// workgroup per CU, the phases separated by device-wide barriers.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -11,41 +11,25 @@
 
 namespace llrs {
 
-// Column groups of o_proj: group g multiplies the columns of heads
-// [g*nh/G, (g+1)*nh/G) (whole weight blocks) into its own partial vector.
-constexpr int kMaxOGroups = 16;
-
-// One layer's GEMV phases.  Every activation a phase writes has its own
-// buffer per layer, so within one launch no buffer is read before it is
-// written and activations can be read with ordinary loads after a barrier.
-//   qkv:       RMSNorm + Q/K/V (+bias) of the layer input; outputs as tagged
-//              words (the attention items read them without a barrier);
-//   o_grp[g]:  o_proj restricted to column group g (input: the heads'
-//              tagged outputs), written as partial vector g;
-//   gate_up:   RMSNorm + gate/up + SiLU*up of input + partials 0, 1, ...;
-//   down:      ffn_down, + input + partials (the residual stream).
+// One layer's GEMV phases (those of the kernel-per-phase path).  Every
+// activation a phase writes has its own buffer per layer (the residual stream
+// included), so within one launch no buffer is read before it is written and
+// activations can be read with ordinary loads.
 struct PersistentLayer {
-  FastGemvArgs qkv, gate_up, down;
-  FastGemvArgs o_grp[kMaxOGroups];
+  FastGemvArgs qkv, o, gate_up, down;
 };
 
 struct PersistentArgs {
   const PersistentLayer *layers;  // device array, one per layer
   int nlayers;
-  int o_groups;  // column groups of o_proj (1 .. kMaxOGroups)
-  // Layer 0's attention; layer l's tagged q|k|v and head outputs lie
-  // tag_stride words further and its KV cache cache_stride floats further
-  // (kept as kernel arguments so the attention's pointers stay in scalar
-  // registers).
+  // Layer 0's attention; layer l's q/k/v/out lie act_stride floats further
+  // and its KV cache cache_stride floats further (kept as kernel arguments so
+  // the attention's pointers stay in scalar registers).
   AttnArgs attn;
-  long tag_stride, cache_stride;
-  // Per layer kMaxOGroups counters of heads whose output is stored (the
-  // o_proj tiles wait on their group's), or null when the heads' outputs
-  // are tagged words; zero at launch like the barrier counters.
-  unsigned *o_cnt;
+  long act_stride, cache_stride;
   unsigned *bar;  // kPersistentBarWords words of barrier counters, zero at launch (the embedding kernel clears them)
+  unsigned *err;  // set when a barrier wait gives up; never cleared by the kernel
   int scalar_poll;  // the counters lie in uncached memory: polled by scalar loads
-  unsigned *err;  // set when a barrier or tagged wait gives up; never cleared by the kernel
 };
 
 // Barrier counters, each on its own 128-byte line.

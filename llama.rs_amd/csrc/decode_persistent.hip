@@ -1,41 +1,29 @@
 // The persistent decode kernel: one launch runs every layer of a token's
 // step (Qwen2Model::forward_impl, src/model.rs:173-261) with one workgroup
-// per CU, all co-resident.  A layer is three intervals between device-wide
-// barriers:
-//   A. RMSNorm + Q/K/V (+bias), written as tagged words; then the attention
-//      items (RoPE, KV append, scores, softmax, V sums, merge), each reading
-//      its head's q/k/v once their tags are this step's, the heads' outputs
-//      again written as tagged words; then o_proj, split by column groups of
-//      heads: workgroup w multiplies the columns of one group (whole weight
-//      blocks) for its rows, reading that group's head outputs once tagged,
-//      into the group's partial vector.
-//   B. RMSNorm + gate/up + SiLU*up of x + partial 0 + partial 1 + ... (the
-//      residual after o_proj, summed in that fixed order by every workgroup).
-//   C. ffn_down (+ the same residual).
-// The arithmetic of each GEMV is the kernel-per-phase path's; o_proj sums
-// its column groups as separate partials, so the residual after o_proj is
-// (x + p_0) + p_1 ... where the per-phase path adds one full dot.
+// per CU, all co-resident.  Per layer the phases are those of the
+// kernel-per-phase path, with the same arithmetic: RMSNorm + Q/K/V (+bias),
+// RoPE + KV append + attention, o_proj (+residual), RMSNorm + gate/up +
+// SiLU*up, ffn_down (+residual).  A device-wide barrier separates the phases.
 //
-// Why: a barrier costs a few memory round trips under the weight traffic
-// (store drain, arrival, poll, then the activation's load).  A tagged word
-// carries its data and its readiness in one store, and a consumer that needs
-// a few KB (a head's q/k/v, a head group's outputs) reads it directly.
-// Every workgroup needs all of x before gate/up and all of SiLU*up before
-// ffn_down: those two stay barriers, and so does the layer boundary.
-//
-// Before waiting at a barrier, a workgroup issues the first weight loads of
-// its next phase (they depend on nothing the current phase writes), so the
-// wait overlaps HBM latency.
+// Why: a separate launch per phase pays the ramp-up of its first weight
+// loads and the drain of its last workgroups every time.  Here a workgroup
+// issues the first weight loads of its next phase (they depend on nothing the
+// current phase writes) before it waits at the barrier, so the wait overlaps
+// HBM latency.
 //
 // Barrier: kBarCounters device-scope counters, 128 bytes apart; workgroup w
 // increments counter w % kBarCounters (an atomic without return, so arriving
 // costs no round trip) and the first wave of every workgroup polls all of
-// them, one per lane, until their sum reaches the barrier's target.  Spread
-// over several counters, the arrivals do not queue behind each other at one
-// address (a single counter costs ~4 us per barrier at 256 workgroups, these
-// ~1.7 us).  The writer waits for its stores (device-scope stores) before
-// arriving.  Every wait is bounded in time: on expiry the kernel sets *err
-// (reported to the host as an error) and runs on rather than hang.
+// them until their sum reaches the barrier's target.  Spread over several
+// counters, the arrivals do not queue behind each other at one address (a
+// single counter costs ~4 us per barrier at 256 workgroups, these ~1.7 us).
+// The counters live in uncached memory (no L2 keeps a copy) and are polled
+// with scalar loads: a wave's vector loads complete in issue order, so a
+// vector poll would first wait for the weight loads the wave issued before
+// the barrier (+2% end to end on the 7B shape).  The writer waits for its
+// stores (device-scope stores) before arriving.  Every wait is bounded in
+// time: on expiry the kernel sets *err (reported to the host as an error)
+// and runs on rather than hang.
 #include <hip/hip_runtime.h>
 
 #include "attention_dev.h"
@@ -46,36 +34,21 @@
 namespace llrs {
 
 #ifdef LLRS_STAMPS
-// Timing build only (build.py --stamps): per barrier interval k (3 per layer)
-// and workgroup, wall-clock stamps (the 100 MHz clock): [0] released from
-// barrier k (interval 0: kernel entry), [1] activation staged, [2] weight
-// streaming done, [3] stores done and arriving at barrier k + 1; in interval
-// A also [4] Q/K/V stored, [5] attention items done, [6] o_proj's input
-// staged, [7] o_proj's streaming done.
-constexpr int kStampIntervals = 3 * 64, kStampWgs = 512, kStampSlots = 8;
-__device__ unsigned long long g_stamps[kStampIntervals * kStampWgs * kStampSlots];
-// And per layer and attention item: [0] the item's start, [1] its end (its
-// partial published, or the head's output stored).
-constexpr int kStampItems = 4096;
-__device__ unsigned long long g_item_stamps[64 * kStampItems * 2];
-#define STAMP_ITEM(l, it, i)                                                                   \
-  do {                                                                                         \
-    if ((threadIdx.x & 63) == 0 && (l) < 64 && (it) < kStampItems)                             \
-      g_item_stamps[((size_t)(l) * kStampItems + (it)) * 2 + (i)] = wall_clock64();            \
+// Timing build only (build.py --stamps): per barrier interval k (5 per layer)
+// and workgroup, wall-clock stamps (the 100 MHz clock) [0] released from
+// barrier k, [1] activation staged, [2] weight streaming done, [3] stores
+// done and arriving at barrier k + 1.  Interval 0 starts at kernel entry.
+constexpr int kStampIntervals = 5 * 64, kStampWgs = 512;
+__device__ unsigned long long g_stamps[kStampIntervals * kStampWgs * 4];
+#define STAMP(k, i)                                                                        \
+  do {                                                                                     \
+    if (threadIdx.x == 0 && (k) < kStampIntervals && wg < kStampWgs)                      \
+      g_stamps[((size_t)(k) * kStampWgs + wg) * 4 + (i)] = wall_clock64();                 \
   } while (0)
-#define STAMP(k, i)                                                                          \
-  do {                                                                                       \
-    if (threadIdx.x == 0 && (k) < kStampIntervals && wg < kStampWgs)                        \
-      g_stamps[((size_t)(k) * kStampWgs + wg) * kStampSlots + (i)] = wall_clock64();         \
-  } while (0)
-#define STAMP_PHASE(ph, k, off)                                                               \
-  ph.stamp = ((k) < kStampIntervals && wg < kStampWgs)                                        \
-                 ? g_stamps + ((size_t)(k) * kStampWgs + wg) * kStampSlots + (off)           \
-                 : nullptr
+#define STAMP_PHASE(ph, k) ph.stamp = ((k) < kStampIntervals && wg < kStampWgs) ? g_stamps + ((size_t)(k) * kStampWgs + wg) * 4 : nullptr
 #else
 #define STAMP(k, i) do {} while (0)
-#define STAMP_PHASE(ph, k, off) do {} while (0)
-#define STAMP_ITEM(l, it, i) do {} while (0)
+#define STAMP_PHASE(ph, k) do {} while (0)
 #endif
 
 namespace {
@@ -122,6 +95,8 @@ __device__ __forceinline__ unsigned bar_sum_scalar(const unsigned *bar) {
 }
 
 // Until every workgroup has arrived at barrier k (k >= 1), or ~20 ms passed.
+// scalar: the counters are in uncached memory (scalar polls); otherwise each
+// lane polls one with a device-scope vector load.
 __device__ void bar_wait(unsigned *bar, unsigned *err, int nwg, unsigned k, bool scalar) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
@@ -172,28 +147,23 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
   const int span = LONG ? attention_span(pos, p.attn.nh) : 1;
   const int n_pairs = p.attn.nkv * (pos / (span * kChunk) + 1);
   const int n_items = (n_pairs + 7) / 8 * 8 * G;
-  // o_proj column group of this workgroup: workgroups [ceil(g nwg / NG),
-  // ceil((g + 1) nwg / NG)) take group g, splitting its rows among them.
-  const int NG = p.o_groups;
-  const int og = wg * NG / nwg;
-  const int og0 = (og * nwg + NG - 1) / NG, og1 = ((og + 1) * nwg + NG - 1) / NG;
   const unsigned epoch = *p.attn.epoch;  // advanced by this step's embedding launch
   unsigned k = 0;
   for (int l = 0; l < p.nlayers; l++) {
     // Through the constant address space: the arguments are never written
     // during the launch, so they load through the scalar cache.
     const PersistentLayer &L = *(const PersistentLayer *)(ConstLayer *)((uintptr_t)(p.layers + l));
-    const unsigned tag = epoch * (unsigned)p.nlayers + (unsigned)l;
     // The phase objects are value-initialised: a member that one path leaves
     // unset would otherwise be carried in registers from the previous layer.
-    {  // A1. RMSNorm + Q/K/V (+ bias) -> tagged words
+    {  // RMSNorm + Q/K/V (+ bias)
       auto qkv = [&](auto tv) {
         GemvPhase<TQ, decltype(tv)::value, false, true> ph{};
         ph.prefetch(L.qkv, wg, nwg);
         if (k) bar_wait(p.bar, p.err, nwg, k, p.scalar_poll);
         STAMP(k, 0);
-        STAMP_PHASE(ph, k, 0);
-        ph.finish(L.qkv, smem, red, tag, p.err);
+        STAMP_PHASE(ph, k);
+        ph.finish(L.qkv, smem, red);
+        bar_arrive(p.bar, wg, k);
       };
       if constexpr (TV == kTypePerLayer) {  // V's type, read per layer (a uniform branch)
         switch (L.qkv.seg[L.qkv.nseg - 1].type) {
@@ -204,64 +174,74 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
       } else {
         qkv(TypeC<TV>{});
       }
-      STAMP(k, 4);
+      k++;
     }
-    {  // A2. RoPE, KV append, attention: one (head, chunk) item per wave
+    {  // RoPE, KV append, attention: one (head, chunk) item per wave
       AttnArgs a = p.attn;
-      a.qkv_t += l * p.tag_stride;
-      if (a.out_t) a.out_t += l * p.tag_stride;
-      if (a.out) a.out += 2 * l * p.tag_stride;
-      if (a.out_cnt) a.out_cnt += l * kMaxOGroups;
+      a.q += l * p.act_stride;
+      a.k += l * p.act_stride;
+      a.v += l * p.act_stride;
+      a.out += l * p.act_stride;
       a.k_cache += l * p.cache_stride;
       a.v_cache += l * p.cache_stride;
-      a.tag = tag;
-      // An item issues its cache loads (rows written by earlier steps; from
-      // kSplitLoadsFrom positions only the key rows) before it reads this
-      // step's tagged q/k/v.
+      a.tag = epoch * (unsigned)p.nlayers + (unsigned)l;
+      // Every wave passes the barrier once: inside its first item, after that
+      // item's cache loads are issued (rows written by earlier steps; from
+      // kSplitLoadsFrom positions only the key rows), or after the loop when
+      // it has no item.
+      bool waited = false;
+      auto wait = [&] {
+        if (!waited) {
+          bar_wait(p.bar, p.err, nwg, k, p.scalar_poll);
+          STAMP(k, 0);
+          waited = true;
+        }
+      };
       const bool multi = span > 1;
       for (int it = wave * nwg + wg; it < n_items; it += nwg * nwv) {
         const int r = it >> 3, pair = (r / G) * 8 + (it & 7);
         if (pair >= n_pairs) continue;
         const int hh = (pair % a.nkv) * G + r % G, item = pair / a.nkv;
-        STAMP_ITEM(l, it, 0);
         if constexpr (LONG) {
           if (multi)
-            attention_item<HD, true, true, true, true>(a, hh, item, pos, aqs[wave], akn[wave]);
+            attention_item<HD, true, true, true>(a, hh, item, pos, aqs[wave], akn[wave], wait);
           else
-            attention_item<HD, true, false, true, true>(a, hh, item, pos, aqs[wave], akn[wave]);
+            attention_item<HD, true, false, true>(a, hh, item, pos, aqs[wave], akn[wave], wait);
         } else {
-          attention_item<HD, true, false, true, true>(a, hh, item, pos, aqs[wave], akn[wave]);
+          attention_item<HD, true, false, true>(a, hh, item, pos, aqs[wave], akn[wave], wait);
         }
-        STAMP_ITEM(l, it, 1);
       }
-      STAMP(k, 5);
-    }
-    {  // A3. o_proj of this workgroup's column group -> partial vector og
-      const FastGemvArgs &O = L.o_grp[og];
-      GemvPhase<TO, TO, false, true> ph{};
-      ph.prefetch(O, wg - og0, og1 - og0);
-      STAMP_PHASE(ph, k, 5);
-      ph.finish(O, smem, red, tag, p.err);
+      wait();
       bar_arrive(p.bar, wg, k);
       k++;
     }
-    {  // B. RMSNorm + gate/up + SiLU*up of x + the o_proj partials
+    {  // o_proj (+ residual)
+      GemvPhase<TO, TO, false, true> ph{};
+      ph.prefetch(L.o, wg, nwg);
+      bar_wait(p.bar, p.err, nwg, k, p.scalar_poll);
+      STAMP(k, 0);
+      STAMP_PHASE(ph, k);
+      ph.finish(L.o, smem, red);
+      bar_arrive(p.bar, wg, k);
+      k++;
+    }
+    {  // RMSNorm + gate/up + SiLU*up
       GemvPhase<TGU, TGU, true, true> ph{};
       ph.prefetch(L.gate_up, wg, nwg);
       bar_wait(p.bar, p.err, nwg, k, p.scalar_poll);
       STAMP(k, 0);
-      STAMP_PHASE(ph, k, 0);
+      STAMP_PHASE(ph, k);
       ph.finish(L.gate_up, smem, red);
       bar_arrive(p.bar, wg, k);
       k++;
     }
-    {  // C. ffn_down (+ x + the o_proj partials)
+    {  // ffn_down (+ residual)
       auto down = [&](auto td) {
         GemvPhase<decltype(td)::value, decltype(td)::value, false, true> ph{};
         ph.prefetch(L.down, wg, nwg);
         bar_wait(p.bar, p.err, nwg, k, p.scalar_poll);
         STAMP(k, 0);
-        STAMP_PHASE(ph, k, 0);
+        STAMP_PHASE(ph, k);
         ph.finish(L.down, smem, red);
         bar_arrive(p.bar, wg, k);
       };
@@ -348,8 +328,6 @@ int launch_decode_persistent(const PersistentArgs &p, uint32_t t_qkv, uint32_t t
                              uint32_t t_gu, uint32_t t_down, int head_dim, int grid, size_t lds,
                              hipStream_t s, bool long_items) {
   if (grid < 1) return set_error(LLRS_E_INVALID, "persistent decode: grid %d", grid);
-  if (p.o_groups < 1 || p.o_groups > kMaxOGroups || p.o_groups > grid)
-    return set_error(LLRS_E_INVALID, "persistent decode: %d o_proj column groups", p.o_groups);
   if (lds + persistent_static_lds(head_dim) > kCuLds)
     return set_error(LLRS_E_UNSUPPORTED, "persistent decode needs %zu bytes of LDS", lds);
   if (t_qkv == LLRS_Q4_K && t_v == LLRS_Q8_0 && t_down == LLRS_Q6_K)
@@ -368,14 +346,9 @@ int launch_decode_persistent(const PersistentArgs &p, uint32_t t_qkv, uint32_t t
 
 #ifdef LLRS_STAMPS
 // Timing build only: copies the stamps of the last persistent launch
-// ([interval][512 workgroup slots][8], 64-bit ticks of the 100 MHz clock).
+// ([interval][512 workgroup slots][4], 64-bit ticks of the 100 MHz clock).
 extern "C" int llrs_debug_stamps(void *dst, size_t bytes) {
   if (bytes > sizeof(llrs::g_stamps)) bytes = sizeof(llrs::g_stamps);
   return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(llrs::g_stamps), bytes, 0, hipMemcpyDeviceToHost);
-}
-// ... and the attention items' ([layer][4096 item slots][2]).
-extern "C" int llrs_debug_item_stamps(void *dst, size_t bytes) {
-  if (bytes > sizeof(llrs::g_item_stamps)) bytes = sizeof(llrs::g_item_stamps);
-  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(llrs::g_item_stamps), bytes, 0, hipMemcpyDeviceToHost);
 }
 #endif

@@ -51,22 +51,6 @@ struct FastGemvArgs {
   uint8_t *dig_out;      // when set: the output is also written digitised here
   const uint8_t *dig_in; // when set: x arrives digitised (x and norm are unused)
   const float *res_in;   // kEpiAdd: the residual added to (null: seg[0].out itself)
-  // Persistent decode kernel only (one launch, producers on other CUs):
-  // x_add: n_add vectors, add_stride floats apart, added in order onto x (the
-  //   input is x + add[0] + add[1] + ...) and, with kEpiAdd, onto res_in;
-  // x_tagged: x arrives as 64-bit words (value | tag << 32) and is read once
-  //   every word carries the step's tag (x is unused);
-  // tag_out: kEpiStore writes each output as such a tagged word (seg[i].out
-  //   then points at 64-bit words).
-  const float *x_add;
-  int n_add, add_stride;
-  const unsigned long long *x_tagged;
-  int tag_out;
-  // x_ready: x is read once *x_ready has reached x_ready_target (a counter
-  // its producers advance after their stores; one thread polls it).
-  const unsigned *x_ready;
-  unsigned x_ready_target;
-  int x_ready_scalar;  // the counter lies in uncached memory: polled by scalar loads
 };
 
 // Rows [r0, r1) of workgroup wg of nwg: the launch's weight bytes split evenly
@@ -100,7 +84,7 @@ bool fast_gemv_supports_pair(uint32_t ta, uint32_t tb);
 // Dynamic LDS of one workgroup: the digitised activation and its rows' results.
 size_t fast_gemv_lds_bytes(const FastGemvArgs &a, int grid);
 // Bytes of a digitised activation of n elements (dig_out / dig_in).
-__host__ __device__ inline size_t fast_gemv_digits_size(size_t n) { return 2 * n + (n / 16) * 8; }
+inline size_t fast_gemv_digits_size(size_t n) { return 2 * n + (n / 16) * 8; }
 int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s);
 // Workgroups for a launch over `rows` x `cols`, never more than the
 // partition units (`part` rows each; 0 = row pairs).

@@ -54,7 +54,6 @@ __host__ __device__ constexpr size_t fast_gemv_digit_bytes(int cols) {
 }
 constexpr size_t kMaxLds = 160 * 1024;
 
-
 __device__ __forceinline__ int slot(int b, int nb4) { return (b & 3) * nb4 + (b >> 2); }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
@@ -472,12 +471,11 @@ __device__ void load_digits(const uint8_t *__restrict__ src, int cols, uint8_t *
   __syncthreads();
 }
 
-// x (times the RMSNorm gain when given) as digits in LDS, x-block b's 16
-// values coming from `block(b, v)`; returns 1/sqrt(mean(x^2) + eps) with a
-// gain, 1 without.  One pass over x.
-template <class Block>
-__device__ float digitize_from(Block &&block, const float *__restrict__ gain, float eps, int cols,
-                               uint8_t *smem, float *red) {
+// x (times the RMSNorm gain when given) as digits in LDS; returns
+// 1/sqrt(mean(x^2) + eps) with a gain, 1 without.  One pass over x.
+template <bool COH>
+__device__ float digitize(const float *__restrict__ x, const float *__restrict__ gain, float eps,
+                          int cols, uint8_t *smem, float *red) {
   const int nt = blockDim.x, tid = thread_x(), nb = cols >> 4, nb4 = nb >> 2;
   int8_t *dig = reinterpret_cast<int8_t *>(smem);
   float *xs = reinterpret_cast<float *>(smem + 2 * cols);
@@ -488,7 +486,11 @@ __device__ float digitize_from(Block &&block, const float *__restrict__ gain, fl
   // always hold the two x-blocks of a 32-column group.
   for (int b = tid; b < nb; b += nt) {
     float v[16];
-    block(b, v);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float4 a = ld_act4<COH>(x + b * 16 + q * 4);
+      v[4 * q] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w;
+    }
     if (gain) {
 #pragma unroll
       for (int j = 0; j < 16; j++) ss += v[j] * v[j];
@@ -523,67 +525,6 @@ __device__ float digitize_from(Block &&block, const float *__restrict__ gain, fl
     inv = 1.0f / sqrtf(t / (float)cols + eps);
   }
   return inv;
-}
-
-// The 16 values of x-block b of x + add[0] + add[1] + ... (n_add vectors
-// add_stride floats apart, summed in that order); the addends' loads go out
-// two vectors at a time, together with x's.
-template <bool COH>
-__device__ __forceinline__ void x_block(const float *__restrict__ x, const float *__restrict__ add,
-                                        int n_add, int add_stride, int b, float (&v)[16]) {
-#pragma unroll
-  for (int q = 0; q < 4; q++) {
-    float4 a = ld_act4<COH>(x + b * 16 + q * 4);
-    v[4 * q] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w;
-  }
-  for (int k = 0; k < n_add; k += 2) {
-    const float *p0 = add + (size_t)k * add_stride + b * 16;
-    const bool two = k + 1 < n_add;
-    const float *p1 = two ? p0 + add_stride : p0;
-    float4 a0[4], a1[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      a0[q] = ld_act4<COH>(p0 + q * 4);
-      a1[q] = ld_act4<COH>(p1 + q * 4);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const float *e0 = reinterpret_cast<const float *>(&a0[q]), *e1 = reinterpret_cast<const float *>(&a1[q]);
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        float t = v[4 * q + j] + e0[j];
-        v[4 * q + j] = two ? t + e1[j] : t;
-      }
-    }
-  }
-}
-
-template <bool COH>
-__device__ float digitize(const float *__restrict__ x, const float *__restrict__ gain, float eps,
-                          int cols, uint8_t *smem, float *red, const float *add = nullptr,
-                          int n_add = 0, int add_stride = 0) {
-  return digitize_from([&](int b, float (&v)[16]) { x_block<COH>(x, add, n_add, add_stride, b, v); },
-                       gain, eps, cols, smem, red);
-}
-
-// x as tagged words (value | tag << 32) written by other workgroups of the
-// launch: each x-block is read until all its tags are `tag` (~20 ms at most,
-// then *err is set), then digitised.
-__device__ float digitize_tagged(const unsigned long long *__restrict__ xt, unsigned tag, unsigned *err,
-                                 int cols, uint8_t *smem, float *red) {
-  unsigned long long t0 = 0;
-  return digitize_from(
-      [&](int b, float (&v)[16]) {
-        const unsigned long long *p = xt + (size_t)b * 16;
-        while (true) {
-          bool ok = true;
-#pragma unroll
-          for (int j = 0; j < 16; j++) v[j] = load_tagged(p + j, tag, ok);
-          if (__all(ok) || tagged_wait_over(t0, err)) break;
-          __builtin_amdgcn_s_sleep(1);
-        }
-      },
-      nullptr, 0.f, cols, smem, red);
 }
 
 __device__ __forceinline__ uint32_t total_order_key(float f) {
@@ -822,19 +763,6 @@ struct GemvPhase {
     hi = min(wrow1, base + a.seg[s].rows);
   }
 
-  // Row g's epilogue input: kEpiStore its bias (0 without), kEpiAdd the
-  // residual plus the addends in order (the output itself without res_in).
-  static __device__ __forceinline__ float epilogue_side(const FastGemvArgs &a, int g) {
-    int s = 0, rs = g;
-    while (s + 1 < a.nseg && rs >= a.seg[s].rows) rs -= a.seg[s++].rows;
-    const FastSeg &S = a.seg[s];
-    if (a.epi == kEpiStore) return S.bias ? S.bias[rs] : 0.f;
-    if (a.epi != kEpiAdd) return 0.f;
-    float r = a.res_in ? a.res_in[rs] : S.out[rs];
-    for (int k = 0; k < a.n_add; k++) r += a.x_add[(size_t)k * a.add_stride + rs];
-    return r;
-  }
-
   __device__ __forceinline__ void prefetch(const FastGemvArgs &a, int wg_, int nwg_) {
     wg = wg_;
     nwg = nwg_;
@@ -848,52 +776,24 @@ struct GemvPhase {
     base0 = 0;
     while (s0 + 1 < a.nseg && wrow0 >= base0 + a.seg[s0].rows) base0 += a.seg[s0++].rows;
     s0_is_ta = DUAL || TA == TB || s0 + 1 < a.nseg;
-    if (s0_is_ta) begin_first(a);
-  }
-
-  __device__ __forceinline__ void begin_first(const FastGemvArgs &a) {
-    int lo, hi;
-    seg_range(a, s0, base0, lo, hi);
-    const FastSeg Sw = shifted(a.seg[s0], lo - base0);
-    const FastSeg Uw = DUAL ? shifted(a.seg[1], lo - base0) : Sw;
-    A.begin(Sw, Uw, lo, max(lo, hi), wave, nw, a.cols, lane);
+    if (s0_is_ta) {
+      int lo, hi;
+      seg_range(a, s0, base0, lo, hi);
+      const FastSeg Sw = shifted(a.seg[s0], lo - base0);
+      const FastSeg Uw = DUAL ? shifted(a.seg[1], lo - base0) : Sw;
+      A.begin(Sw, Uw, lo, max(lo, hi), wave, nw, a.cols, lane);
+    }
   }
 
   // The activation (x or its digits) and the residual are read with ordinary
   // loads: every buffer a phase reads was written before any workgroup of the
   // launch first read it, so no cache holds a stale copy.
-  // tag / err: the step's tag of tagged inputs and outputs (x_tagged,
-  // tag_out) and the flag a wait for tagged inputs sets when it gives up.
-  __device__ void finish(const FastGemvArgs &a, uint8_t *smem, float *red, unsigned tag = 0,
-                         unsigned *err = nullptr) {
-    // The epilogue's per-row input of the thread's first row (the bias, or
-    // the residual plus its addends) is loaded now, so its latency hides
-    // under the streaming instead of lengthening the epilogue.
-    const int g_first = wrow0 + thread_x();
-    float side = 0.f;
-    if (g_first < wrow1) side = epilogue_side(a, g_first);
+  __device__ void finish(const FastGemvArgs &a, uint8_t *smem, float *red) {
     float inv = 1.0f;
-    if (a.x_ready) {  // one wave waits for the producers' counter (bounded)
-      if (thread_x() < 64) {
-        unsigned long long t0 = 0;
-        while (true) {
-          const unsigned c =
-              a.x_ready_scalar
-                  ? poll_scalar_u32(a.x_ready)
-                  : __hip_atomic_load(const_cast<unsigned *>(a.x_ready), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (__builtin_amdgcn_readfirstlane(c) >= a.x_ready_target || tagged_wait_over(t0, err)) break;
-          __builtin_amdgcn_s_sleep(1);
-        }
-      }
-      __syncthreads();
-    }
-    if (a.dig_in) {
+    if (a.dig_in)
       load_digits<false>(a.dig_in, a.cols, smem);
-    } else if (a.x_tagged) {
-      inv = digitize_tagged(a.x_tagged, tag, err, a.cols, smem, red);
-    } else {
-      inv = digitize<false>(a.x, a.norm, a.eps, a.cols, smem, red, a.x_add, a.n_add, a.add_stride);
-    }
+    else
+      inv = digitize<false>(a.x, a.norm, a.eps, a.cols, smem, red);
 #ifdef LLRS_STAMPS
     if (stamp && thread_x() == 0) stamp[1] = wall_clock64();
 #endif
@@ -954,25 +854,14 @@ struct GemvPhase {
 
     // Epilogue over the workgroup's rows, coalesced.
     unsigned long long best = 0;
-    for (int g = g_first; g < wrow1; g += blockDim.x) {
+    for (int g = wrow0 + thread_x(); g < wrow1; g += blockDim.x) {
       int s = 0, rs = g;
       while (s + 1 < a.nseg && rs >= a.seg[s].rows) rs -= a.seg[s++].rows;
       const FastSeg &S = a.seg[s];
       const float v = ybuf[g - wrow0];
       switch (a.epi) {
-        case kEpiStore: {
-          const float y = S.bias ? v + (g == g_first ? side : epilogue_side(a, g)) : v;
-          if (a.tag_out)
-            store_tagged(reinterpret_cast<unsigned long long *>(S.out) + rs, y, tag);
-          else
-            st_act<COH>(S.out + rs, y);
-          break;
-        }
-        case kEpiAdd: {
-          const float r = g == g_first ? side : epilogue_side(a, g);
-          st_act<COH>(S.out + rs, r + v);
-          break;
-        }
+        case kEpiStore: st_act<COH>(S.out + rs, S.bias ? v + S.bias[rs] : v); break;
+        case kEpiAdd: st_act<COH>(S.out + rs, (a.res_in ? a.res_in[rs] : S.out[rs]) + v); break;
         case kEpiSwiGlu: st_act<COH>(a.seg[2].out + rs, v); break;
         default: {
           st_act<COH>(S.out + rs, v);

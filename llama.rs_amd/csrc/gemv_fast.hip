@@ -2,8 +2,6 @@
 // gemv_dev.h).
 #include <hip/hip_runtime.h>
 
-#include <algorithm>
-
 #include "common.h"
 #include "gemv.h"
 #include "gemv_dev.h"

@@ -92,12 +92,9 @@ struct llrs_kv {
   // types have an instantiation: per-layer arguments, barrier words, error flag.
   llrs::PersistentLayer *p_layers = nullptr;
   unsigned *p_bar = nullptr, *p_err = nullptr;
-  llrs::AttnArgs p_attn{};  // layer 0's attention (per-layer tagged buffers p_tag_stride words apart)
-  long p_tag_stride = 0;
-  int p_o_groups = 0;       // o_proj column groups
-  unsigned *p_o_cnt = nullptr;  // per layer, the o_proj groups' head counters (inside p_bar)
-  int p_bar_words = 0;          // counters the embedding launch zeroes
-  bool p_bar_uc = false;        // p_bar is uncached memory (scalar polls), returned to the pool
+  llrs::AttnArgs p_attn{};  // layer 0's attention (per-layer buffers act_stride floats apart)
+  long p_act_stride = 0;
+  bool p_bar_uc = false;    // p_bar is uncached memory (scalar polls), returned to the pool
   int p_grid = 0;
   size_t p_lds = 0;
   uint32_t p_types[5] = {};
@@ -805,12 +802,10 @@ static int enqueue_layers(llrs_model *m, llrs_kv *kv, bool long_items) {
     p.layers = kv->p_layers;
     p.nlayers = (int)c.num_hidden_layers;
     p.attn = kv->p_attn;
-    p.o_groups = kv->p_o_groups;
-    p.tag_stride = kv->p_tag_stride;
+    p.act_stride = kv->p_act_stride;
     p.cache_stride = (long)(kv->max_seq_len * c.kv_width);
     p.bar = kv->p_bar;
     p.scalar_poll = kv->p_bar_uc ? 1 : 0;
-    p.o_cnt = kv->p_o_cnt;
     p.err = kv->p_err;
     const uint32_t *t = kv->p_types;
     return launch_decode_persistent(p, t[0], t[1], t[2], t[3], t[4], (int)c.head_dim, kv->p_grid,
@@ -830,7 +825,7 @@ static int enqueue_layers(llrs_model *m, llrs_kv *kv, bool long_items) {
 // kernel's barrier counter).
 static int enqueue_embed(llrs_model *m, llrs_kv *kv) {
   return launch_embed(m->embed, kv->tok_by_pos, kv->pos, (int)kv->max_seq_len, kv->residual,
-                      kv->epoch, m->b->stream, kv->p_bar, kv->p_bar ? kv->p_bar_words : 0);
+                      kv->epoch, m->b->stream, kv->p_bar, kv->p_bar ? kPersistentBarWords : 0);
 }
 
 static int enqueue_step(llrs_model *m, llrs_kv *kv, int mode, bool long_items) {
@@ -922,41 +917,14 @@ static int setup_persistent(llrs_model *m, llrs_kv *kv) {
     if (!decode_persistent_supports(t[0], t[1], t[2], t[3], t[4], (int)c.head_dim)) return LLRS_OK;
   }
   const int grid = m->b->cu_count;
-  const size_t H = c.hidden_size, KV = c.kv_width, F = c.intermediate_size;
-  const size_t nh = c.num_attention_heads, hd = c.head_dim;
-  // o_proj column groups: LLRS_O_GROUPS (default 1: each tile waits for
-  // every head and adds the residual itself), lowered to the largest count
-  // that splits the heads evenly into groups of whole weight blocks (and
-  // 64-column units) that the tuned GEMV takes.  Measured on the 7B shape:
-  // 1 and 2 groups ran alike, 7 and 14 slower (gate/up then reads 8 or 15
-  // vectors before its RMSNorm).
-  const llrs_tensor *o0 = m->layers[0].o;
-  int ng = 1;
-  if (const char *e = getenv("LLRS_O_GROUPS")) ng = atoi(e);
-  ng = std::max(1, std::min(ng, std::min(kMaxOGroups, grid)));
-  auto group_ok = [&](int g) {
-    if (nh % (size_t)g) return false;
-    const size_t gc = nh / g * hd;
-    return gc % 64 == 0 && gc % (size_t)block_size(o0->type) == 0 && fast_gemv_supports(o0->type, gc);
-  };
-  while (ng > 1 && !group_ok(ng)) ng--;
-  if (!group_ok(ng)) return LLRS_OK;
-  const size_t gcols = nh / ng * hd;
-  // How o_proj's tiles learn that their group's heads are done:
-  // LLRS_O_HANDOFF=tag makes the heads' outputs tagged words that the tiles
-  // read until tagged; by default each head's wave counts itself into its
-  // group's counter once its output is stored, one thread per tile polls it.
-  const char *ho = getenv("LLRS_O_HANDOFF");
-  const bool o_tagged = ho && !strcmp(ho, "tag");
   // Per-layer activation buffers (each slice 256-byte aligned, so no cache
-  // line holds two buffers): q|k|v and the heads' outputs as tagged 64-bit
-  // words, the o_proj partials, the residual after ffn_down and the SiLU*up
-  // digits.  The last layer's ffn_down writes the shared residual the LM
-  // head reads.
+  // line holds two buffers): q|k|v, attention output, residual after o_proj
+  // and after ffn_down, SiLU*up digits.  The last layer's ffn_down writes
+  // the shared residual the LM head reads.
+  const size_t H = c.hidden_size, KV = c.kv_width, F = c.intermediate_size;
   auto al = [](size_t b) { return (b + 255) / 256 * 256; };
-  const size_t sz_tag = al((H + 2 * KV) * 8) + al(nh * hd * 8), sz_h = al(H * 4);
-  const size_t sz_part = (size_t)ng * sz_h, sz_dig = al(fast_gemv_digits_size(F));
-  const size_t per_layer = sz_tag + sz_part + sz_h + sz_dig;
+  const size_t sz_qkv = al((H + 2 * KV) * 4), sz_h = al(H * 4), sz_dig = al(fast_gemv_digits_size(F));
+  const size_t per_layer = sz_qkv + 3 * sz_h + sz_dig;
   uint8_t *act = nullptr;
   LLRS_TRY(dev_alloc(kv->allocs, (void **)&act, nl * per_layer));
   std::vector<PersistentLayer> host(nl);
@@ -964,68 +932,36 @@ static int setup_persistent(llrs_model *m, llrs_kv *kv) {
   const float *x_in = kv->residual;
   for (size_t l = 0; l < nl; l++) {
     uint8_t *b = act + l * per_layer;
-    unsigned long long *qkv_t = (unsigned long long *)b;
-    unsigned long long *out_t = (unsigned long long *)(b + al((H + 2 * KV) * 8));
-    float *part = (float *)(b + sz_tag);
-    float *x_out = l + 1 == nl ? kv->residual : (float *)(b + sz_tag + sz_part);
-    uint8_t *dig = b + sz_tag + sz_part + sz_h;
+    float *q = (float *)b, *k = q + H, *v = k + KV;
+    float *attn = (float *)(b + sz_qkv), *x_mid = (float *)(b + sz_qkv + sz_h);
+    float *x_out = l + 1 == nl ? kv->residual : (float *)(b + sz_qkv + 2 * sz_h);
+    uint8_t *dig = b + sz_qkv + 3 * sz_h;
     PersistentLayer &P = host[l];
     P.qkv = projection_args(m, kv, l, P_QKV);
     P.qkv.x = x_in;
-    P.qkv.seg[0].out = (float *)qkv_t;
-    P.qkv.seg[1].out = (float *)(qkv_t + H);
-    P.qkv.seg[2].out = (float *)(qkv_t + H + KV);
-    P.qkv.tag_out = 1;
+    P.qkv.seg[0].out = q;
+    P.qkv.seg[1].out = k;
+    P.qkv.seg[2].out = v;
     if (l == 0) {
       kv->p_attn = attention_args(m, kv, 0);
-      kv->p_attn.q = kv->p_attn.k = kv->p_attn.v = nullptr;
-      kv->p_attn.out = o_tagged ? nullptr : (float *)out_t;
-      kv->p_attn.qkv_t = qkv_t;
-      kv->p_attn.out_t = o_tagged ? out_t : nullptr;
-      kv->p_attn.out_group_heads = (int)(nh / ng);
+      kv->p_attn.q = q;
+      kv->p_attn.k = k;
+      kv->p_attn.v = v;
+      kv->p_attn.out = attn;
     }
-    const llrs_tensor *o = m->layers[l].o;
-    if (o->type != o0->type) return LLRS_OK;
-    // One group: o_proj adds the residual itself (x' = x + o, as the
-    // per-phase path), and gate/up and ffn_down read x' alone.
-    const bool direct = ng == 1;
-    for (int g = 0; g < ng; g++) {
-      FastGemvArgs &a = P.o_grp[g];
-      a.seg[0] = seg_of(o, nullptr, part + g * (sz_h / 4));
-      if (direct) {
-        a.epi = kEpiAdd;
-        a.res_in = x_in;
-      }
-      a.seg[0].w = o->dev + (size_t)g * gcols / block_size(o->type) * type_size(o->type);
-      a.nseg = 1;
-      a.rows = (int)H;
-      a.cols = (int)gcols;
-      if (o_tagged) {
-        a.x_tagged = out_t + g * gcols;
-      } else {
-        a.x = (const float *)out_t + g * gcols;
-        a.x_ready = nullptr;  // filled in below, once the counters exist
-        a.x_ready_target = (unsigned)(nh / ng);
-      }
-      if (!direct) a.epi = kEpiStore;
-      const int g0 = (g * grid + ng - 1) / ng, g1 = ((g + 1) * grid + ng - 1) / ng;
-      lds = std::max(lds, fast_gemv_lds_bytes(a, g1 - g0));
-    }
+    P.o = projection_args(m, kv, l, P_O);
+    P.o.x = attn;
+    P.o.res_in = x_in;
+    P.o.seg[0].out = x_mid;
     P.gate_up = projection_args(m, kv, l, P_GATE_UP);
-    P.gate_up.x = direct ? part : x_in;
-    P.gate_up.x_add = direct ? nullptr : part;
-    P.gate_up.n_add = direct ? 0 : ng;
-    P.gate_up.add_stride = (int)(sz_h / 4);
+    P.gate_up.x = x_mid;
     P.gate_up.dig_out = dig;
     P.down = projection_args(m, kv, l, P_DOWN);
     P.down.dig_in = dig;
-    P.down.res_in = direct ? part : x_in;
-    P.down.x_add = direct ? nullptr : part;
-    P.down.n_add = direct ? 0 : ng;
-    P.down.add_stride = (int)(sz_h / 4);
+    P.down.res_in = x_mid;
     P.down.seg[0].out = x_out;
     if (!P.gate_up.dig_out || P.gate_up.part != 16) return LLRS_OK;
-    for (const FastGemvArgs *a : {&P.qkv, &P.gate_up, &P.down})
+    for (const FastGemvArgs *a : {&P.qkv, &P.o, &P.gate_up, &P.down})
       lds = std::max(lds, fast_gemv_lds_bytes(*a, grid));
     x_in = x_out;
   }
@@ -1042,41 +978,25 @@ static int setup_persistent(llrs_model *m, llrs_kv *kv) {
   }
   auto A = [&](void **p, size_t bytes) { return dev_alloc(kv->allocs, p, bytes); };
   LLRS_TRY(A((void **)&kv->p_layers, nl * sizeof(PersistentLayer)));
-  // Barrier counters, then per layer the o_proj groups' head counters: all
-  // zeroed by every step's embedding launch.
-  const size_t bar_words = kPersistentBarWords + nl * kMaxOGroups;
-  // The counters live in uncached memory and are polled by scalar loads,
-  // which do not queue behind the CU's weight loads (+1.5-2% on the 7B
+  // The barrier counters live in uncached memory and are polled by scalar
+  // loads, which do not queue behind the CU's weight loads (+2% on the 7B
   // shape); LLRS_SCALAR_POLL=0 keeps them in ordinary memory with vector
   // polls.
   const char *sp = getenv("LLRS_SCALAR_POLL");
   kv->p_bar_uc = !(sp && *sp == '0');
   if (kv->p_bar_uc) {
-    LLRS_TRY(uc_acquire(m->b->device, bar_words * 4, (void **)&kv->p_bar));
+    LLRS_TRY(uc_acquire(m->b->device, kPersistentBarWords * 4, (void **)&kv->p_bar));
   } else {
-    LLRS_TRY(A((void **)&kv->p_bar, bar_words * 4));
-  }
-  kv->p_bar_words = (int)bar_words;
-  if (!o_tagged) {
-    kv->p_o_cnt = kv->p_bar + kPersistentBarWords;
-    kv->p_attn.out_cnt = kv->p_o_cnt;
-    for (size_t l = 0; l < nl; l++)
-      for (int g = 0; g < ng; g++) {
-        host[l].o_grp[g].x_ready = kv->p_o_cnt + l * kMaxOGroups + g;
-        host[l].o_grp[g].x_ready_scalar = kv->p_bar_uc ? 1 : 0;
-      }
+    LLRS_TRY(A((void **)&kv->p_bar, kPersistentBarWords * 4));
   }
   LLRS_TRY(A((void **)&kv->p_err, 64));
   hipStream_t s = m->b->stream;
   LLRS_HIP(hipMemcpyAsync(kv->p_layers, host.data(), nl * sizeof(PersistentLayer), hipMemcpyHostToDevice, s));
-  LLRS_HIP(hipMemsetAsync(kv->p_bar, 0, bar_words * 4, s));
+  LLRS_HIP(hipMemsetAsync(kv->p_bar, 0, kPersistentBarWords * 4, s));
   LLRS_HIP(hipMemsetAsync(kv->p_err, 0, 64, s));
-  // Tag 0 is never a step's: the tagged buffers start out stale.
-  LLRS_HIP(hipMemsetAsync(act, 0, nl * per_layer, s));
   LLRS_HIP(hipStreamSynchronize(s));
   memcpy(kv->p_types, t, sizeof t);
-  kv->p_tag_stride = (long)(per_layer / 8);
-  kv->p_o_groups = ng;
+  kv->p_act_stride = (long)(per_layer / 4);
   kv->p_grid = grid;
   kv->p_lds = lds;
   return LLRS_OK;

@@ -186,21 +186,15 @@ __device__ __forceinline__ bool tagged_wait_over(unsigned long long &t0, unsigne
   return true;
 }
 
-// A dword read through the scalar memory path with glc (the scalar cache is
-// bypassed): a poll that does not queue behind the vector loads of the CU it
-// runs on.  Only for words in uncached device memory (no L2 keeps a copy)
-// that other workgroups change with device-scope atomics.  p is uniform.
+// A uniform pointer moved into scalar registers (for scalar-memory polls of
+// words in uncached device memory).
 __device__ __forceinline__ const unsigned *uniform_ptr(const unsigned *p) {
   const unsigned long long a = reinterpret_cast<unsigned long long>(p);
   const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a);
   const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
   return reinterpret_cast<const unsigned *>(((unsigned long long)hi << 32) | lo);
 }
-__device__ __forceinline__ unsigned poll_scalar_u32(const unsigned *p) {
-  unsigned v;
-  asm volatile("s_load_dword %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=&s"(v) : "s"(uniform_ptr(p)) : "memory");
-  return v;
-}
+
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 

@@ -5,13 +5,14 @@
 
 Loads libllrs_hip_stamps.so (the product library with the persistent decode
 kernel compiled with -DLLRS_STAMPS: thread 0 of every workgroup stores the
-100 MHz wall clock at fixed points of each barrier interval), builds the
-workload's synthetic model, prefills its prompt, decodes, and prints, averaged
-over the layers, then the median over the last `--steps` decode steps, in
-microseconds, for each of the three barrier intervals of a layer
-(A: Q/K/V + attention + o_proj, B: gate/up, C: down):
+100 MHz wall clock when it is released from a barrier, when its activation is
+staged in LDS, when its weight streaming ends and when it arrives at the
+next barrier), builds the workload's synthetic model, prefills its prompt,
+decodes, and prints for each of the five phases of a layer (averaged over the
+layers, then the median over the last `--steps` decode steps), in
+microseconds:
 
-    span      first release of the interval -> last arrival at its end barrier
+    span      first release of the phase -> last arrival (the phase's length)
     release   last arrival at the previous barrier -> first release (barrier latency)
     stage     median workgroup: release -> activation staged
     stream    median workgroup: staged -> streaming done
@@ -19,11 +20,9 @@ microseconds, for each of the three barrier intervals of a layer
     skew      first -> last arrival
     late-XCD  the XCD whose workgroups arrive last, on average (workgroup w runs on XCD w % 8)
 
-and for interval A the median workgroup's segments: Q/K/V stage, stream and
-epilogue, the attention items, o_proj's wait for the heads' outputs plus
-staging, its streaming and its tail; plus the kernel's total per layer.  The
-stamps are stores of one thread per workgroup at points the kernel passes
-anyway; the timing build runs the product kernel's arithmetic unchanged.
+and the kernel's total per layer.  The stamps are stores of one thread per
+workgroup at points the kernel passes anyway; the timing build runs the
+product kernel's arithmetic unchanged.
 """
 from __future__ import annotations
 
@@ -37,10 +36,8 @@ import sys
 import numpy as np
 
 PKG = pathlib.Path(__file__).resolve().parent
-PHASES = ("A_qkv_attn_o", "gate_up", "down")
-SEGMENTS = ("qkv_stage", "qkv_stream", "qkv_epilogue", "attention", "o_wait_stage", "o_stream", "o_tail")
-K_INTERVALS, K_WGS, K_SLOTS = 3 * 64, 512, 8
-PER_LAYER = len(PHASES)
+PHASES = ("qkv", "attention", "o_proj", "gate_up", "down")
+K_INTERVALS, K_WGS = 5 * 64, 512
 
 WORKLOADS = {
     "cfg5": dict(hidden_size=3584, intermediate_size=18944, num_attention_heads=28,
@@ -68,68 +65,33 @@ def load_stamps_package(lib=None):
 
 
 def read_stamps(llrs, nwg: int, nlayers: int) -> np.ndarray:
-    buf = np.zeros(K_INTERVALS * K_WGS * K_SLOTS, np.uint64)
+    buf = np.zeros(K_INTERVALS * K_WGS * 4, np.uint64)
     f = llrs.lib().llrs_debug_stamps
     f.restype, f.argtypes = C.c_int, [C.c_void_p, C.c_size_t]
     if f(buf.ctypes.data, buf.nbytes) != 0:
         raise RuntimeError("reading the stamps failed")
-    return buf.reshape(K_INTERVALS, K_WGS, K_SLOTS)[:PER_LAYER * nlayers, :nwg, :].astype(np.int64)
-
-
-K_ITEMS = 4096
-
-
-def read_item_stamps(llrs, nlayers: int) -> np.ndarray:
-    buf = np.zeros(64 * K_ITEMS * 2, np.uint64)
-    f = llrs.lib().llrs_debug_item_stamps
-    f.restype, f.argtypes = C.c_int, [C.c_void_p, C.c_size_t]
-    if f(buf.ctypes.data, buf.nbytes) != 0:
-        raise RuntimeError("reading the item stamps failed")
-    return buf.reshape(64, K_ITEMS, 2)[:nlayers].astype(np.int64)
-
-
-def analyse_items(ts: np.ndarray, its: np.ndarray, nlayers: int, pos: int, nh: int, nkv: int) -> dict:
-    """Interval A's attention items relative to the interval's first release:
-    the median and last item start, the last end of non-merging items, and
-    the median and last end of the merging (last-chunk) items (us)."""
-    G, span = nh // nkv, 1
-    n_pairs = nkv * (pos // 32 + 1)
-    n_items = (n_pairs + 7) // 8 * 8 * G
-    it = np.arange(n_items)
-    r = it >> 3
-    pair = (r // G) * 8 + (it & 7)
-    live = pair < n_pairs
-    chunk = pair // nkv
-    last = chunk == pos // 32
-    rows = []
-    for l in range(nlayers):
-        t0 = ts[PER_LAYER * l, :, 0].min()
-        st, en = its[l, :n_items, 0], its[l, :n_items, 1]
-        ok = live & (st > 0)
-        if not ok.any():
-            continue
-        rows.append((np.median(st[ok] - t0), (st[ok] - t0).max(), (en[ok & ~last] - t0).max() if (ok & ~last).any() else 0,
-                     np.median(en[ok & last] - t0), (en[ok & last] - t0).max()))
-    a = np.array(rows, np.float64) * 10.0 / 1e3
-    return dict(item_start_med=a[:, 0].mean(), item_start_max=a[:, 1].mean(), partial_end_max=a[:, 2].mean(),
-                merge_end_med=a[:, 3].mean(), merge_end_max=a[:, 4].mean())
+    return buf.reshape(K_INTERVALS, K_WGS, 4)[:5 * nlayers, :nwg, :].astype(np.int64)
 
 
 def analyse(ts: np.ndarray, nlayers: int) -> dict:
-    """Per interval, averaged over the layers: microseconds (ticks are 10 ns)."""
+    """Per phase, averaged over the layers: microseconds (ticks are 10 ns)."""
     out = {}
     ns = 10.0
     for ph, name in enumerate(PHASES):
         rows = []
         for l in range(nlayers):
-            k = PER_LAYER * l + ph
+            k = 5 * l + ph
             rel, arr = ts[k, :, 0], ts[k, :, 3]
             span = (arr.max() - rel.min()) * ns
             release = (rel.min() - ts[k - 1, :, 3].max()) * ns if k > 0 else 0.0
             skew = (arr.max() - arr.min()) * ns
-            stage = np.median(ts[k, :, 1] - rel) * ns
-            stream = np.median(ts[k, :, 2] - ts[k, :, 1]) * ns
-            tail = np.median(arr - (ts[k, :, 7] if ph == 0 else ts[k, :, 2])) * ns
+            if ph == 1:
+                stage = stream = 0.0
+                tail = np.median(arr - rel) * ns
+            else:
+                stage = np.median(ts[k, :, 1] - rel) * ns
+                stream = np.median(ts[k, :, 2] - ts[k, :, 1]) * ns
+                tail = np.median(arr - ts[k, :, 2]) * ns
             xcd = [np.mean(arr[x::8]) for x in range(8)]
             rows.append((span, release, stage, stream, tail, skew, int(np.argmax(xcd))))
         a = np.array(rows, np.float64)
@@ -137,26 +99,7 @@ def analyse(ts: np.ndarray, nlayers: int) -> dict:
                          stage=a[:, 2].mean() / 1e3, stream=a[:, 3].mean() / 1e3,
                          tail=a[:, 4].mean() / 1e3, skew=a[:, 5].mean() / 1e3,
                          late_xcd=int(np.bincount(a[:, 6].astype(int), minlength=8).argmax()))
-    # Interval A's landmarks relative to its first release (us), mean over
-    # layers: the last Q/K/V store, the median and last o_proj staging.
-    lm = []
-    for l in range(nlayers):
-        t = ts[PER_LAYER * l]
-        t0 = t[:, 0].min()
-        lm.append(((t[:, 4] - t0).max(), np.median(t[:, 6] - t0), (t[:, 6] - t0).max(), (t[:, 3] - t0).max()))
-    lm = np.array(lm, np.float64) * ns / 1e3
-    out["landmarks_A"] = dict(qkv_stored_max=lm[:, 0].mean(), o_staged_med=lm[:, 1].mean(),
-                              o_staged_max=lm[:, 2].mean(), arrival_max=lm[:, 3].mean())
-    # Interval A's segments, median workgroup: slots 0 released, 1 staged, 2
-    # streamed, 4 Q/K/V stored, 5 attention done, 6 o_proj staged, 7 o_proj
-    # streamed, 3 arrival.
-    seg = {n: [] for n in SEGMENTS}
-    for l in range(nlayers):
-        t = ts[PER_LAYER * l]
-        for n, (a, b) in zip(SEGMENTS, ((0, 1), (1, 2), (2, 4), (4, 5), (5, 6), (6, 7), (7, 3))):
-            seg[n].append(np.median(t[:, b] - t[:, a]) * ns)
-    out["segments_A"] = {n: float(np.mean(v)) / 1e3 for n, v in seg.items()}
-    total = (ts[PER_LAYER * nlayers - 1, :, 3].max() - ts[0, :, 0].min()) * ns / 1e3
+    total = (ts[5 * nlayers - 1, :, 3].max() - ts[0, :, 0].min()) * ns / 1e3
     out["kernel_us_per_layer"] = total / nlayers
     return out
 
@@ -189,18 +132,12 @@ def main():
         pos += 1
         ts = read_stamps(llrs, be.threads(), cfg.num_hidden_layers)
         raw.append(ts)
-        a = analyse(ts, cfg.num_hidden_layers)
-        a["items_A"] = analyse_items(ts, read_item_stamps(llrs, cfg.num_hidden_layers), cfg.num_hidden_layers,
-                                     pos - 1, cfg.num_attention_heads, cfg.num_key_value_heads)
-        per_step.append(a)
+        per_step.append(analyse(ts, cfg.num_hidden_layers))
     if args.dump:
         np.save(args.dump, np.stack(raw))
     res = {}
     for name in PHASES:
         res[name] = {k: float(np.median([s[name][k] for s in per_step])) for k in per_step[0][name]}
-    res["segments_A"] = {n: float(np.median([s["segments_A"][n] for s in per_step])) for n in SEGMENTS}
-    for key in ("landmarks_A", "items_A"):
-        res[key] = {n: float(np.median([s[key][n] for s in per_step])) for n in per_step[0][key]}
     res["kernel_us_per_layer"] = float(np.median([s["kernel_us_per_layer"] for s in per_step]))
     if args.json:
         print(json.dumps(res))
@@ -217,10 +154,6 @@ def main():
         print(f"| {name} | {r['span']:.2f} | {r['release']:.2f} | {r['stage']:.2f} | {r['stream']:.2f} | "
               f"{r['tail']:.2f} | {r['skew']:.2f} | {r['late_xcd']} |")
     print(f"\nsum of spans + releases {tot:.2f} us per layer; kernel {res['kernel_us_per_layer']:.2f} us per layer")
-    print("\ninterval A, median workgroup (us): " +
-          ", ".join(f"{n} {res['segments_A'][n]:.2f}" for n in SEGMENTS))
-    print("interval A, from its first release (us): " +
-          ", ".join(f"{n} {v:.2f}" for n, v in {**res["landmarks_A"], **res["items_A"]}.items()))
 
 
 if __name__ == "__main__":
