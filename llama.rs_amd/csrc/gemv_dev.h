@@ -473,18 +473,23 @@ __device__ void load_digits(const uint8_t *__restrict__ src, int cols, uint8_t *
 
 // x (times the RMSNorm gain when given) as digits in LDS; returns
 // 1/sqrt(mean(x^2) + eps) with a gain, 1 without.  One pass over x.
-template <bool COH>
+// REV: the blocks go to the highest threads first.  The waves without rows
+// in a small phase are the highest ones (rows go to waves in order), and they
+// have no weight loads in flight: a wave's loads complete in issue order, so
+// x loads issued behind prefetched weights would wait for them.
+template <bool COH, bool REV = false>
 __device__ float digitize(const float *__restrict__ x, const float *__restrict__ gain, float eps,
                           int cols, uint8_t *smem, float *red) {
   const int nt = blockDim.x, tid = thread_x(), nb = cols >> 4, nb4 = nb >> 2;
+  const int t0 = REV ? nt - 1 - tid : tid;
   int8_t *dig = reinterpret_cast<int8_t *>(smem);
   float *xs = reinterpret_cast<float *>(smem + 2 * cols);
   int *sx = reinterpret_cast<int *>(xs + nb);
   float *xsum32 = reinterpret_cast<float *>(sx + nb);
   float ss = 0.f;
   // nb is a multiple of 4 and nt of 64, so the lanes b and b^1 of one wave
-  // always hold the two x-blocks of a 32-column group.
-  for (int b = tid; b < nb; b += nt) {
+  // always hold the two x-blocks of a 32-column group (nt - 1 is odd).
+  for (int b = t0; b < nb; b += nt) {
     float v[16];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -793,7 +798,7 @@ struct GemvPhase {
     if (a.dig_in)
       load_digits<false>(a.dig_in, a.cols, smem);
     else
-      inv = digitize<false>(a.x, a.norm, a.eps, a.cols, smem, red);
+      inv = digitize<false, COH>(a.x, a.norm, a.eps, a.cols, smem, red);
 #ifdef LLRS_STAMPS
     if (stamp && thread_x() == 0) stamp[1] = wall_clock64();
 #endif
