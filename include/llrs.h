@@ -259,8 +259,10 @@ typedef struct llrs_sampling {
 int llrs_sample(llrs_kv *kv, const llrs_sampling *opts, const uint32_t *recent, size_t n_recent,
                 float uniform, uint32_t *out_token);
 /* llrs_sample without any allocation, on any call: no counterpart in the
- * reference.  For callers that cannot allocate device memory (code under
- * graph capture, serving loops, harnesses that forbid hipMalloc).  Its
+ * reference.  For callers that cannot allocate device memory (tight serving
+ * loops, harnesses that forbid hipMalloc).  It is not for code under stream
+ * capture: like llrs_sample it copies the window from host memory,
+ * synchronises the stream and reads the token back.  Its
  * scratch (sort keys and indices, the repeat window, the radix sort's
  * temporary storage: 8.3 MB) is one file-scope device array per GPU, held
  * until the process ends, so the vocabulary is limited to 262,144 tokens and

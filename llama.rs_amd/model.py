@@ -347,7 +347,9 @@ class InferenceEngine:
         takes them from rand::thread_rng); None draws them with numpy."""
         prompt = np.ascontiguousarray(prompt_tokens, dtype=np.uint32)
         if uniforms is None:
-            uniforms = np.random.default_rng().random(max(max_new_tokens, 1))
+            # float32 draws in [0, 1): a float64 draw above 1 - 2^-25 would
+            # round to 1.0f, which the sampler rejects.
+            uniforms = np.random.default_rng().random(max(max_new_tokens, 1), dtype=np.float32)
         u = np.ascontiguousarray(uniforms, dtype=np.float32)
         if u.size < max_new_tokens:
             raise LlrsError(-1, "one uniform draw per generated token is needed")

@@ -441,17 +441,21 @@ def test_config3_qwen05b_shape_greedy_parity(llrs, backend, oracle, tmp_path):
         assert llrs.gguf_read_tensor(tmp_path / "c3.gguf", name)[1].quant_type == qt, name
 
 
+@pytest.mark.parametrize("n_prompt", [70, 2100], ids=["one_level", "two_level"])
 @pytest.mark.parametrize("decode_path", ["persistent", "per_phase"])
-def test_softmax_uniform_fallback_on_gpu(llrs, backend, oracle, tmp_path, monkeypatch, decode_path):
+def test_softmax_uniform_fallback_on_gpu(llrs, backend, oracle, tmp_path, monkeypatch, decode_path, n_prompt):
     """A NaN query bias in layer 0 makes every score NaN: the GPU attention must
     fall back to the plain V mean as softmax_inplace does (src/model.rs:305-312).
     Covered: one position (single chunk); a 70-token prompt fed token by token
     through the decode step (from position 64 on, three 32-position chunks are
     merged, each chunk's partial non-finite); the batched prefill's attention
     tiles; then 8 decode steps from position 70, every step's logits against
-    the oracle's.  Once on the persistent decode kernel, once on the
+    the oracle's.  A 2,100-token prompt then decodes past 2,100 positions
+    (66 chunks per head, more than 64: the merge runs in two levels, group
+    leaders publishing non-finite group partials and the last item summing
+    every chunk's V sums).  Once on the persistent decode kernel, once on the
     launch-per-phase path."""
-    cfg = tiny_cfg(llrs, seed=29, num_hidden_layers=2)
+    cfg = tiny_cfg(llrs, seed=29, num_hidden_layers=2, max_position_embeddings=4096)
     path = tmp_path / "n.gguf"
     cfg.write_gguf(path)
     _, bias = oracle.gguf_read_f32(path, "blk.0.attn_q.bias")
@@ -461,11 +465,12 @@ def test_softmax_uniform_fallback_on_gpu(llrs, backend, oracle, tmp_path, monkey
     assert at > 0 and raw.find(old, at + 1) < 0
     raw[at:at + len(old)] = np.full(bias.size, np.nan, np.float32).tobytes()
     path.write_bytes(bytes(raw))
-    prompt = np.random.default_rng(29).integers(0, cfg.vocab_size, 70).astype(np.uint32)
+    prompt = np.random.default_rng(29).integers(0, cfg.vocab_size, n_prompt).astype(np.uint32)
+    ctx = n_prompt + 58
     if decode_path == "per_phase":
         monkeypatch.setenv("LLRS_NO_PERSISTENT", "1")
     model = llrs.ModelLoader.load_dynamic(path, backend)  # the patched file, not a rewrite
-    kv, om = llrs.KVCache(model, 128), oracle.load(path)
+    kv, om = llrs.KVCache(model, ctx), oracle.load(path)
     assert kv.persistent == (decode_path == "persistent")
 
     def check(what):
@@ -476,12 +481,13 @@ def test_softmax_uniform_fallback_on_gpu(llrs, backend, oracle, tmp_path, monkey
         assert err <= LOGIT_TOL
         assert kv.argmax() == om.argmax()
 
-    for n, tokenwise in ((1, False), (len(prompt), True), (len(prompt), False)):
+    runs = ((1, False), (len(prompt), True), (len(prompt), False)) if n_prompt < 128 else ((len(prompt), False),)
+    for n, tokenwise in runs:
         if tokenwise:
             monkeypatch.setenv("LLRS_PREFILL_TOKENWISE", "1")
         model.prefill(prompt[:n], 0, kv)
         monkeypatch.delenv("LLRS_PREFILL_TOKENWISE", raising=False)
-        om.new_state(128)
+        om.new_state(ctx)
         om.prefill(prompt[:n], 0)
         check(f"prompt {n} ({'token by token' if tokenwise else 'batched'})")
     for step in range(8):

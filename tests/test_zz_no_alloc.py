@@ -6,6 +6,10 @@ Two calls in a row on the same GPU share that array: a 152,064-token
 vocabulary first, then a 1,000-token one (a smaller input, whose call must
 not see anything the larger one left).  Each call's token must equal
 llrs_sample's for the same options, window and uniform draw.
+
+The property itself is probed with hipMemGetInfo: on a fresh cache the
+device's free bytes are unchanged by the first llrs_sample_noalloc calls,
+and the same probe sees llrs_sample's first call allocate its scratch.
 """
 from __future__ import annotations
 
@@ -56,6 +60,35 @@ def test_sample_noalloc_matches_sample(llrs, backend):
                 assert a == b
         # The window alone changes: the penalty must see the new one.
         assert noalloc(llrs, kv, cases[2], [], 0.5) == kv.sample(cases[2], 0.5, [])
+
+
+def free_device_bytes() -> int:
+    """hipMemGetInfo's free bytes of the current device (the HIP runtime the
+    library already initialised)."""
+    hip = C.CDLL("libamdhip64.so")
+    free, total = C.c_size_t(), C.c_size_t()
+    assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return free.value
+
+
+def test_sample_noalloc_allocates_nothing(llrs, backend):
+    opts = llrs.SamplingOptions(temperature=0.8, top_p=0.9, top_k=40, repetition_penalty=1.1)
+    recent = np.arange(64, dtype=np.uint32)
+    _, warm = model_kv(llrs, backend, 1000, 7)
+    noalloc(llrs, warm, opts, recent, 0.5)  # the sampler's code is resident before the probe
+    _, kv = model_kv(llrs, backend, 152064, 6)  # a fresh cache: no sampler scratch yet
+    backend.synchronize()
+    before = free_device_bytes()
+    for u in (0.1, 0.5, 0.9):
+        noalloc(llrs, kv, opts, recent, u)
+    after = free_device_bytes()
+    print(f"[noalloc] free bytes {before} -> {after}", flush=True)
+    assert after == before
+    # The probe sees an allocation: llrs_sample's first call allocates its scratch.
+    kv.sample(opts, 0.5, recent)
+    allocated = free_device_bytes()
+    print(f"[noalloc] llrs_sample's first call: free bytes {after} -> {allocated}", flush=True)
+    assert allocated < after
 
 
 def test_sample_noalloc_rejects_oversized_window(llrs, backend):
