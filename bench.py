@@ -173,17 +173,49 @@ TUNED_TYPES = ("Q4K", "Q5K", "Q6K", "Q8_0", "Q5_0", "Q4_0", "Q4_1", "Q5_1")
 FLOAT_TYPES = ("F32", "F16", "BF16")
 
 
-def gemv_sweep(llrs, be) -> int:
+def gemv_cpu(oracle, kernel, threads: int, data: bytes, ty: int, rows: int, cols: int,
+             x: np.ndarray, reps: int) -> float:
+    """Median seconds of `reps` oracle matvecs (CpuBackend::matvec with the
+    reference's row-parallel policy, src/backend.rs:143-162), after one
+    untimed call."""
+    buf = np.frombuffer(data, dtype=np.uint8)
+    y = np.empty(rows, np.float32)
+    import ctypes as C
+    F32P = C.POINTER(C.c_float)
+    call = lambda: oracle.lib.oq_matvec(buf.ctypes.data, ty, rows, cols, x.ctypes.data_as(F32P),
+                                        y.ctypes.data_as(F32P), kernel, threads, 128 * 1024)
+    assert call() == 0
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        call()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def gemv_sweep(llrs, be, cpu_reps: int) -> int:
     """Configs 1 and 2: single batch-1 GEMVs through KernelBackend::matvec
     (llrs_matvec_dev on device buffers).  Config 1: Q4_K 8960 x 1536 (seed 1);
     config 2: every type at 18944 x 3584 and 3584 x 18944 (seed 2).  Each
     tensor is uploaded as many times as makes >= 1.2 GB, and the launches
     rotate over the copies, so the 256 MB MALL cannot serve a repeat; the
     timed loop is one synchronisation around n launches.  Algorithmic bytes
-    = weights + x + y."""
+    = weights + x + y.
+
+    With cpu_reps > 0 every case is also timed on the host through the
+    oracle's restatement of CpuBackend::matvec (the reference cannot be built
+    here): its AVX2 dots (src/simd.rs; types without one use the scalar dot,
+    as the reference does) on all host threads and on one, and its scalar
+    dots on all threads, each the median of cpu_reps calls."""
     import ctypes as C
     QT = llrs.QuantType
     lib = llrs.lib()
+    oracle = None
+    if cpu_reps > 0:
+        sys.path.insert(0, str(ROOT / "tests"))
+        from oracle_ffi import AVX2, SCALAR, Oracle
+        oracle = Oracle()
+        threads = host_threads()
     cases = [("cfg1", QT.Q4K, 8960, 1536, 1)]
     for name in ("Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q4K", "Q5K", "Q6K", "F16", "BF16"):
         cases += [("cfg2", QT[name], 18944, 3584, 2), ("cfg2", QT[name], 3584, 18944, 2)]
@@ -220,6 +252,16 @@ def gemv_sweep(llrs, be) -> int:
                "frac": round(alg / dt / 1e9 / PEAK_HBM_GBS, 4)}
         log(f"{cfg} {ty.name:5s} {rows:6d} x {cols:5d} {nbytes / 1e6:8.2f} MB {rec['kernel']:7s} "
             f"{rec['us']:9.2f} us {rec['gbs']:7.1f} GB/s ({100 * rec['frac']:.1f}% of peak)")
+        if oracle is not None:
+            cpu = {"kind": "port", "reps": cpu_reps, "statistic": "median"}
+            for name, kernel, th in (("avx2_all", AVX2, threads), ("avx2_one", AVX2, 1),
+                                     ("scalar_all", SCALAR, threads)):
+                dt_c = gemv_cpu(oracle, kernel, th, data, int(ty), rows, cols, xs, cpu_reps)
+                cpu[name] = {"us": round(dt_c * 1e6, 1), "gbs": round(alg / dt_c / 1e9, 2), "threads": th}
+            rec["cpu_baseline"] = cpu
+            log(f"  cpu: AVX2 {cpu['avx2_all']['gbs']} GB/s on {threads} threads, "
+                f"{cpu['avx2_one']['gbs']} on 1; scalar {cpu['scalar_all']['gbs']} on {threads}; "
+                f"GPU / AVX2-all {rec['gbs'] / cpu['avx2_all']['gbs']:.0f}x")
         out.append(rec)
     print(json.dumps({"gemv": out}), flush=True)
     return 0
@@ -227,15 +269,19 @@ def gemv_sweep(llrs, be) -> int:
 
 def profiled_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration copy), or None."""
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration copy) and the
+    commit its runs measured, or (None, None)."""
     f = ROOT / "profiles" / "pmc_traffic_7b_q4km.md"
     if not f.exists():
-        return None
+        return None, None
+    nbytes = commit = None
     for line in f.read_text().splitlines():
         parts = line.strip().strip("`").split()
         if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
-            return int(parts[2])
-    return None
+            nbytes = int(parts[2])
+        if len(parts) == 3 and parts[0] == "traffic_commit" and parts[1] == kernel:
+            commit = parts[2]
+    return nbytes, commit
 
 
 # The end-to-end benchmark configs: synthetic models (random-init
@@ -391,6 +437,8 @@ def main() -> int:
                          "calibration copy (the workload of the rocprofv3 --pmc traffic runs)")
     ap.add_argument("--gemv", action="store_true",
                     help="configs 1 and 2 instead: single GEMVs per type over rotating weight copies")
+    ap.add_argument("--gemv-cpu-reps", type=int, default=20,
+                    help="--gemv: host oracle calls per case and path (median; 0 = no CPU timing)")
     ap.add_argument("--load", action="store_true",
                     help="instead: load a BF16 safetensors checkpoint of the workload's shape with "
                          "load-time q4km quantization")
@@ -413,7 +461,7 @@ def main() -> int:
     be = llrs.HipBackend(0)
     log(f"backend {be.name()} with {be.threads()} CUs")
     if args.gemv:
-        return gemv_sweep(llrs, be)
+        return gemv_sweep(llrs, be, 0 if args.no_cpu_baseline else args.gemv_cpu_reps)
     if args.load:
         return load_bench(llrs, be, args.workload, args.cpu_seconds, args.keep_checkpoint)
     cfg = llrs.SynthConfig(max_position_embeddings=32768, rope_theta=1e6, rms_norm_eps=1e-6,
@@ -498,18 +546,24 @@ def main() -> int:
         log(f"  layers   {us:8.2f} us/launch  {(wb + kvb) / 1e6:8.2f} MB  {(wb + kvb) / us / 1e3:7.1f} GB/s "
             f"(persistent kernel, position {pos_now})")
         achieved = (wb + kvb) / us / 1e3
+        traffic, commit = profiled_traffic("decode_persistent_kernel") if args.workload == "cfg5" else (None, None)
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                    "traffic": profiled_traffic("decode_persistent_kernel") if args.workload == "cfg5" else None,
+                    "traffic": traffic,
+                    "traffic_source": (f"profiles/pmc_traffic_7b_q4km.md: rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE "
+                                       f"at commit {commit}") if traffic else None,
                     "kernel": f"decode_persistent_kernel: all {mc.num_hidden_layers} layers in one "
                               f"launch ({wb} weight bytes + {kvb} KV bytes at position {pos_now})"}
     else:
         dom = max(per, key=lambda k: per[k]["us_per_token"])
         d = per[dom]
         achieved = d["bytes"] / d["avg_us"] / 1e3
+        traffic, commit = profiled_traffic(dom) if args.workload == "cfg5" else (None, None)
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                    "traffic": profiled_traffic(dom) if args.workload == "cfg5" else None,
+                    "traffic": traffic,
+                    "traffic_source": (f"profiles/pmc_traffic_7b_q4km.md: rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE "
+                                       f"at commit {commit}") if traffic else None,
                     "kernel": f"{dom} projection GEMV ({d['bytes']} algorithmic weight bytes/launch)"}
 
     cpu = None

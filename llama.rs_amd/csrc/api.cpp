@@ -54,6 +54,10 @@ static int launch_matvec(llrs_backend *b, const llrs_tensor *w, const float *x, 
   a.cols = (int)w->cols;
   a.x = x;
   a.epi = kEpiStore;
+  {  // the balanced split (LLRS_BAL=0 turns it off)
+    const char *eb = getenv("LLRS_BAL");
+    a.bal = !(eb && *eb == '0');
+  }
   return launch_gemv_fast(a, fast_gemv_grid(b->cu_count, a.rows, a.cols, false, 0), b->stream);
 }
 

@@ -8,7 +8,7 @@
 namespace llrs {
 
 // Decode attention items.
-constexpr int kChunk = 32;  // positions per wave: lane = (half of the head, position)
+constexpr int kChunk = 32;  // positions per attention sub-chunk (one wave)
 // Sub-chunks per attention item at position pos for nh query heads: one
 // while the items of all heads fit kItemSlots (the persistent kernel's 256
 // workgroups x 8 waves on this part, so every wave takes at most one item),
@@ -19,16 +19,28 @@ __host__ __device__ inline int attention_span(int pos, int nh) {
   const long n = (long)(pos / kChunk + 1) * (nh > 0 ? nh : 1);
   return (int)((n + kItemSlots - 1) / kItemSlots);
 }
-// A head of more than kGroupFrom items merges in two levels: groups of
-// kGroup items are folded by their last item, then the group partials by
-// the head's last item (one round of loads per level instead of one per 16
-// partials).
-constexpr int kGroup = 16, kGroupFrom = 64;
+// Attention tasks: T consecutive items of one head, one per wave of a
+// workgroup of kTaskItems waves, whose partials meet in LDS; the head's tasks
+// then meet through the scratch partials, folded by the head's last task in
+// loads of 32 / VW partials (VW = 2 V floats per lane at head_dim 128, else
+// 1).  T (1, 2, 4 or 8): kTaskItems while a head has at most that many items
+// (its task alone writes the output), else the smallest that lets the fold
+// take one load: larger tasks gather more items on one CU, whose loads then
+// queue behind each other.
+constexpr int kTaskItems = 8;
+__host__ __device__ inline int attention_task_items(int n_items, int hd) {
+  if (n_items <= kTaskItems) return kTaskItems;
+  const int fold = hd >= 128 ? 16 : 32;
+  int t = 1;
+  while (t < kTaskItems && (n_items + t - 1) / t - 1 > fold) t *= 2;
+  return t;
+}
+// Workgroups per head of the attention kernel: kTaskItems items each.
+__host__ __device__ inline int attention_blocks(int max_chunks) { return (max_chunks + kTaskItems - 1) / kTaskItems; }
 // From this position the persistent kernel issues an attention item's key
 // rows before the phase barrier and its value rows after it; at earlier
 // positions it issues both before the barrier.
 constexpr int kSplitLoadsFrom = 1024;
-__host__ __device__ inline int attention_groups(int max_chunks) { return (max_chunks + kGroup - 1) / kGroup; }
 
 // Fused RoPE + KV append + GQA attention of one layer.
 struct AttnArgs {
@@ -37,9 +49,9 @@ struct AttnArgs {
   const int *pos;
   float *k_cache, *v_cache;  // this layer's [max_seq][kv_width]
   float *out;                // [nh * hd]
-  // Chunk partials then group partials per head, attention_scratch_words(nh,
-  // hd, max_seq) words: each value with the tag of the (step, layer) that
-  // wrote it in the high half.
+  // Task partials per head, attention_scratch_words(nh, hd, max_seq) words:
+  // each value with the tag of the (step, layer) that wrote it in the high
+  // half.
   unsigned long long *scratch;
   const unsigned *epoch;     // step counter, advanced by the embedding kernel
   unsigned *err;             // set when a merge gave up waiting for a partial
@@ -47,7 +59,7 @@ struct AttnArgs {
   unsigned tag;              // filled in on the device
   int nh, nkv, hd, max_seq;
   int max_chunks;            // attention_chunks(max_seq)
-  long part_stride;          // attention_part_stride(hd): words per (head, chunk) partial
+  long part_stride;          // attention_part_stride(hd): words per (head, task) partial
   float scale;               // 1/sqrt(hd)
 };
 

@@ -72,17 +72,26 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *__restrict__
 }
 
 template <int HD>
-__global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
-  __shared__ __align__(16) float qs[HD], kn[HD];
+__global__ __launch_bounds__(64 * kTaskItems) void attention_kernel(AttnArgs a) {
+  __shared__ __align__(16) float qs[kTaskItems][HD], kn[kTaskItems][HD];
+  __shared__ __align__(16) float part[kTaskItems * AttnGeom<HD>::kPart];
   a.tag = *a.epoch * (unsigned)a.nlayers + (unsigned)a.layer;
-  // Grid (head, chunk): the low chunks, the ones that run, are dispatched
-  // first, so the chunk that merges a head always starts after the chunks it
-  // waits for.
+  // Grid (head, block of kTaskItems items): the low blocks, the ones that
+  // run, are dispatched first, so the task that merges a head always starts
+  // with or after the tasks it waits for.
   const int pos = bounded_pos(a.pos, a.max_seq);
-  if (attention_span(pos, a.nh) > 1)
-    attention_item<HD, false, true>(a, blockIdx.x, blockIdx.y, pos, qs, kn);
+  const int S = attention_span(pos, a.nh);
+  if ((int)blockIdx.y * kTaskItems * S * kChunk > pos) return;
+  const int wave = threadIdx.x >> 6;
+  auto slot = [&](int s, int T, int n_tasks, int &h, int &task) {
+    h = blockIdx.x;
+    task = blockIdx.y * (kTaskItems / T) + s;  // T divides kTaskItems
+    return task < n_tasks;
+  };
+  if (S > 1)
+    attention_round<HD, false, true>(a, pos, slot, qs[wave], kn[wave], part);
   else
-    attention_item<HD, false, false>(a, blockIdx.x, blockIdx.y, pos, qs, kn);
+    attention_round<HD, false, false>(a, pos, slot, qs[wave], kn[wave], part);
 }
 
 // silu(gate) * up (src/model.rs:251-254).
@@ -172,7 +181,7 @@ long attention_part_stride(int hd) { return 2L * hd + 2; }
 
 size_t attention_scratch_words(int nh, int hd, int max_seq) {
   const int chunks = attention_chunks(max_seq);
-  return (size_t)nh * (size_t)(chunks + attention_groups(chunks)) * (size_t)attention_part_stride(hd);
+  return (size_t)nh * (size_t)chunks * (size_t)attention_part_stride(hd);
 }
 
 int attention_chunks(int max_seq) { return (max_seq + kChunk - 1) / kChunk; }
@@ -185,12 +194,12 @@ int launch_attention(const AttnArgs &args, hipStream_t s) {
   if (args.part_stride != attention_part_stride(hd) || args.max_chunks != attention_chunks(args.max_seq))
     return set_error(LLRS_E_INVALID, "attention scratch geometry does not match head_dim %d, context %d",
                      hd, args.max_seq);
-  const dim3 grid((unsigned)args.nh, (unsigned)args.max_chunks);
+  const dim3 grid((unsigned)args.nh, (unsigned)attention_blocks(args.max_chunks)), block(64 * kTaskItems);
   switch (hd) {
-    case 16: hipLaunchKernelGGL(attention_kernel<16>, grid, dim3(64), 0, s, args); break;
-    case 32: hipLaunchKernelGGL(attention_kernel<32>, grid, dim3(64), 0, s, args); break;
-    case 64: hipLaunchKernelGGL(attention_kernel<64>, grid, dim3(64), 0, s, args); break;
-    default: hipLaunchKernelGGL(attention_kernel<128>, grid, dim3(64), 0, s, args); break;
+    case 16: hipLaunchKernelGGL(attention_kernel<16>, grid, block, 0, s, args); break;
+    case 32: hipLaunchKernelGGL(attention_kernel<32>, grid, block, 0, s, args); break;
+    case 64: hipLaunchKernelGGL(attention_kernel<64>, grid, block, 0, s, args); break;
+    default: hipLaunchKernelGGL(attention_kernel<128>, grid, block, 0, s, args); break;
   }
   LLRS_HIP(hipGetLastError());
   return LLRS_OK;

@@ -136,17 +136,26 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
   __shared__ float red[16];
   __shared__ __align__(16) float aqs[kPersistentThreads / 64][HD], akn[kPersistentThreads / 64][HD];
   const int wg = blockIdx.x, nwg = gridDim.x;
-  const int wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  const int wave = threadIdx.x >> 6;
+  static_assert(kPersistentThreads == 64 * kTaskItems, "an attention task is one item per wave");
   const int pos = bounded_pos(p.attn.pos, p.attn.max_seq);
-  // Attention items: the G query heads that share a (KV head, chunk) run on
-  // workgroups of one XCD (workgroup w sits on XCD w % 8), so the chunk's keys
-  // and values come from HBM once and from that XCD's L2 for the other heads.
-  // Item i: XCD x = i % 8, r = i / 8, head j = r % G of pair q * 8 + x with
-  // q = r / G; pair = chunk * nkv + kv head.
+  // Attention tasks (T items of one head, attention_task_items): the G query
+  // heads that share a (KV head, task index) run on workgroups of one XCD
+  // (workgroup w sits on XCD w % 8), so the items' keys and values come from
+  // HBM once and from that XCD's L2 for the other heads.  Task t: XCD x =
+  // t % 8, r = t / 8, head j = r % G of pair q * 8 + x with q = r / G; pair =
+  // task index * nkv + kv head.  Workgroup w runs tasks w + j nwg in rounds
+  // of kTaskItems / T, in increasing pair order (nwg >= 8 G, checked by the
+  // host), and a head's last task waits only for tasks of lower pairs (or of
+  // its own round, folded by other waves), so every wait ends.
   const int G = p.attn.nh / p.attn.nkv;
   const int span = LONG ? attention_span(pos, p.attn.nh) : 1;
-  const int n_pairs = p.attn.nkv * (pos / (span * kChunk) + 1);
-  const int n_items = (n_pairs + 7) / 8 * 8 * G;
+  const int n_items_h = pos / (span * kChunk) + 1;
+  const int task_items = attention_task_items(n_items_h, HD);
+  const int n_task_h = (n_items_h + task_items - 1) / task_items;
+  const int per_round = kTaskItems / task_items;
+  const int n_pairs = p.attn.nkv * n_task_h;
+  const int n_tasks = (n_pairs + 7) / 8 * 8 * G;
   const unsigned epoch = *p.attn.epoch;  // advanced by this step's embedding launch
   unsigned k = 0;
   for (int l = 0; l < p.nlayers; l++) {
@@ -158,7 +167,7 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
     {  // RMSNorm + Q/K/V (+ bias)
       auto qkv = [&](auto tv) {
         GemvPhase<TQ, decltype(tv)::value, false, true> ph{};
-        ph.prefetch(L.qkv, wg, nwg);
+        ph.prefetch(L.qkv, wg, nwg, smem);
         if (k) bar_wait(p.bar, p.err, nwg, k, p.scalar_poll);
         STAMP(k, 0);
         STAMP_PHASE(ph, k);
@@ -176,7 +185,7 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
       }
       k++;
     }
-    {  // RoPE, KV append, attention: one (head, chunk) item per wave
+    {  // RoPE, KV append, attention: one item per wave, kTaskItems per task
       AttnArgs a = p.attn;
       a.q += l * p.act_stride;
       a.k += l * p.act_stride;
@@ -187,8 +196,9 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
       a.tag = epoch * (unsigned)p.nlayers + (unsigned)l;
       // Every wave passes the barrier once: inside its first item, after that
       // item's cache loads are issued (rows written by earlier steps; from
-      // kSplitLoadsFrom positions only the key rows), or after the loop when
-      // it has no item.
+      // kSplitLoadsFrom positions only the key rows), or in its first task
+      // when it has no item there, or after the loop when the workgroup has
+      // no task.
       bool waited = false;
       auto wait = [&] {
         if (!waited) {
@@ -198,17 +208,29 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
         }
       };
       const bool multi = span > 1;
-      for (int it = wave * nwg + wg; it < n_items; it += nwg * nwv) {
-        const int r = it >> 3, pair = (r / G) * 8 + (it & 7);
-        if (pair >= n_pairs) continue;
-        const int hh = (pair % a.nkv) * G + r % G, item = pair / a.nkv;
+      // The items' partials meet in LDS, two buffers alternating by task: a
+      // buffer is written again only after the next task's workgroup barrier,
+      // which wave 0 reaches after folding it.
+      float *part = reinterpret_cast<float *>(smem);
+      int nt = 0;
+      for (int t0 = wg; t0 < n_tasks; t0 += per_round * nwg) {
+        auto slot = [&](int s, int, int, int &h, int &task) {
+          const int t = t0 + s * nwg;
+          if (t >= n_tasks) return false;
+          const int r = t >> 3, pair = (r / G) * 8 + (t & 7);
+          if (pair >= n_pairs) return false;
+          h = (pair % a.nkv) * G + r % G;
+          task = pair / a.nkv;
+          return true;
+        };
+        float *pb = part + (nt++ & 1) * kTaskItems * AttnGeom<HD>::kPart;
         if constexpr (LONG) {
           if (multi)
-            attention_item<HD, true, true, true>(a, hh, item, pos, aqs[wave], akn[wave], wait);
+            attention_round<HD, true, true, true>(a, pos, slot, aqs[wave], akn[wave], pb, wait);
           else
-            attention_item<HD, true, false, true>(a, hh, item, pos, aqs[wave], akn[wave], wait);
+            attention_round<HD, true, false, true>(a, pos, slot, aqs[wave], akn[wave], pb, wait);
         } else {
-          attention_item<HD, true, false, true>(a, hh, item, pos, aqs[wave], akn[wave], wait);
+          attention_round<HD, true, false, true>(a, pos, slot, aqs[wave], akn[wave], pb, wait);
         }
       }
       wait();
@@ -217,7 +239,7 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
     }
     {  // o_proj (+ residual)
       GemvPhase<TO, TO, false, true> ph{};
-      ph.prefetch(L.o, wg, nwg);
+      ph.prefetch(L.o, wg, nwg, smem);
       bar_wait(p.bar, p.err, nwg, k, p.scalar_poll);
       STAMP(k, 0);
       STAMP_PHASE(ph, k);
@@ -227,7 +249,7 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
     }
     {  // RMSNorm + gate/up + SiLU*up
       GemvPhase<TGU, TGU, true, true> ph{};
-      ph.prefetch(L.gate_up, wg, nwg);
+      ph.prefetch(L.gate_up, wg, nwg, smem);
       bar_wait(p.bar, p.err, nwg, k, p.scalar_poll);
       STAMP(k, 0);
       STAMP_PHASE(ph, k);
@@ -238,7 +260,7 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
     {  // ffn_down (+ residual)
       auto down = [&](auto td) {
         GemvPhase<decltype(td)::value, decltype(td)::value, false, true> ph{};
-        ph.prefetch(L.down, wg, nwg);
+        ph.prefetch(L.down, wg, nwg, smem);
         bar_wait(p.bar, p.err, nwg, k, p.scalar_poll);
         STAMP(k, 0);
         STAMP_PHASE(ph, k);

@@ -51,6 +51,12 @@ struct FastGemvArgs {
   uint8_t *dig_out;      // when set: the output is also written digitised here
   const uint8_t *dig_in; // when set: x arrives digitised (x and norm are unused)
   const float *res_in;   // kEpiAdd: the residual added to (null: seg[0].out itself)
+  // Balanced split: a workgroup whose rows lie in one segment and form fewer
+  // row groups than twice its waves (and not a multiple of them) spreads the
+  // (row group, unit iteration) steps evenly over all waves and sums each
+  // row's per-wave partials in wave order.  The sums then depend on the grid
+  // and the block size in their last bits.
+  int bal;
 };
 
 // Rows [r0, r1) of workgroup wg of nwg: the launch's weight bytes split evenly
@@ -82,7 +88,8 @@ bool fast_gemv_supports(uint32_t type, size_t cols);
 // has a tuned instantiation.
 bool fast_gemv_supports_pair(uint32_t ta, uint32_t tb);
 // Dynamic LDS of one workgroup: the digitised activation and its rows' results.
-size_t fast_gemv_lds_bytes(const FastGemvArgs &a, int grid);
+// `threads`: the block size (the balanced split keeps partials per wave).
+size_t fast_gemv_lds_bytes(const FastGemvArgs &a, int grid, int threads = 256);
 // Bytes of a digitised activation of n elements (dig_out / dig_in).
 inline size_t fast_gemv_digits_size(size_t n) { return 2 * n + (n / 16) * 8; }
 int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s);

@@ -571,6 +571,16 @@ __device__ __forceinline__ float half_sum2(float v0, float v1, int lane) {
   return k;
 }
 
+// The balanced split runs while a segment has fewer than this many row groups
+// per wave; its LDS holds kBalMaxGroupsPerWave * nw groups x nw waves x R
+// (at most 4) partials.
+constexpr int kBalMaxGroupsPerWave = 2;
+__host__ __device__ constexpr size_t bal_slot_bytes(int nw) {
+  return (size_t)kBalMaxGroupsPerWave * nw * nw * 4 * sizeof(float);
+}
+// The row results' LDS (after the digits), rounded to 16 bytes.
+__host__ __device__ constexpr size_t fast_gemv_ybuf_bytes(int rows) { return ((size_t)rows * 4 + 15) & ~(size_t)15; }
+
 // Rows per wave step for a type (kept small enough to double-buffer the raw
 // loads in registers); dual gate/up steps hold two rows of each matrix.
 template <uint32_t TY, bool DUAL> struct RowsPerStep { static constexpr int value = DUAL ? 2 : 4; };
@@ -588,13 +598,27 @@ template <> struct RowsPerStep<LLRS_Q5_K, false> { static constexpr int value = 
 // 24 units), a group is 2R rows and each 32-lane half of the wave takes R of
 // them, lane & 31 being the unit: twice the rows per step, at the same
 // registers, where otherwise most lanes would idle.
-template <uint32_t TY, bool DUAL>
+// BAL: the balanced split may run (the standalone GEMV only: in the decode
+// step its partial-sum pass cost more than the idle waves it fills, and its
+// state costs the persistent kernel registers).
+template <uint32_t TY, bool DUAL, bool BAL = false>
 struct SegStream {
   using T = Traits<TY>;
   static constexpr int R = RowsPerStep<TY, DUAL>::value;
+  static_assert(R <= 4, "bal_slot_bytes holds 4 partials per (group, wave)");
   FastSeg S, U;
   int row_lo, row_hi, first, stride, units, iters, steps, lane, gsz;
   bool packed;
+  // Balanced split (single-matrix streams): when the row groups do not
+  // divide among the waves and a row takes several unit iterations (long
+  // rows over few rows, e.g. a 3,584 x 18,944 GEMV), the wave takes the
+  // contiguous range of the (group, iteration) steps starting at group g0,
+  // iteration it0, and leaves its per-group partial sums in
+  // slots[(group * nw + wave) * R + row]; the caller sums them over the
+  // waves, in wave order, after the streaming.
+  bool bal;
+  int g0, it0, wave, nw;
+  float *slots;
   typename T::Raw cur[R], nxt[R], cu[DUAL ? R : 1], nu[DUAL ? R : 1];
 
   // First row of this wave's g-th row group (of gsz rows: R, or 2R packed).
@@ -616,8 +640,11 @@ struct SegStream {
       if constexpr (DUAL) T::load(U.w + (size_t)r * U.row_bytes, u, dstu[i]);
     }
   }
+  // first_ / stride_: this wave and the wave count.  slots_: LDS for the
+  // balanced split's partial sums (null: whole row groups per wave).
   __device__ __forceinline__ void begin(const FastSeg &S_, const FastSeg &U_, int lo, int hi,
-                                        int first_, int stride_, int cols, int lane_) {
+                                        int first_, int stride_, int cols, int lane_,
+                                        float *slots_ = nullptr) {
     S = S_;
     U = U_;
     row_lo = lo;
@@ -625,28 +652,52 @@ struct SegStream {
     first = first_;
     stride = stride_;
     lane = lane_;
+    wave = first_;
+    nw = stride_;
+    slots = slots_;
     units = cols / T::kColsPerUnit;
     packed = units <= 32;
     iters = packed ? 1 : (units + 63) / 64;
     gsz = packed ? 2 * R : R;
     const int ngroups = (row_hi - row_lo + gsz - 1) / gsz;
-    int nmine = first < ngroups ? (ngroups - first + stride - 1) / stride : 0;
-    steps = __builtin_amdgcn_readfirstlane(nmine) * iters;
-    if (steps > 0) load(0, 0, cur, cu);
+    bal = BAL && !DUAL && slots_ && iters > 1 && ngroups % nw != 0 && ngroups < kBalMaxGroupsPerWave * nw;
+    g0 = it0 = 0;
+    if (bal) {
+      const int T_ = ngroups * iters, sb = wave * T_ / nw, se = (wave + 1) * T_ / nw;
+      steps = se - sb;
+      g0 = sb / iters;
+      it0 = sb % iters;
+      first = 0;
+      stride = 1;
+    } else {
+      int nmine = first < ngroups ? (ngroups - first + stride - 1) / stride : 0;
+      steps = __builtin_amdgcn_readfirstlane(nmine) * iters;
+    }
+    if (steps > 0) load(g0, it0, cur, cu);
   }
   template <class Emit>
   __device__ __forceinline__ void run(const Lds &L, Emit &&emit);
 };
 
-template <uint32_t TY, bool DUAL>
+template <uint32_t TY, bool DUAL, bool BAL>
 template <class Emit>
-__device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&emit) {
+__device__ __forceinline__ void SegStream<TY, DUAL, BAL>::run(const Lds &L, Emit &&emit) {
   using Raw = typename T::Raw;
   constexpr int RU = DUAL ? R : 1;
   float acc[R], acc2[R];
 #pragma unroll
   for (int i = 0; i < R; i++) acc[i] = acc2[i] = 0.f;
-  int g = 0, it = 0;  // the current step's row group and unit iteration
+  int g = g0, it = it0;  // the current step's row group and unit iteration
+  // A complete row's sum goes to emit; in the balanced split every partial
+  // goes to the wave's slot of its group.
+  auto out = [&](int r, float t, float up) {
+    if (BAL && !DUAL && bal) {
+      const int gg = (r - row_lo) / gsz, i = (r - row_lo) % gsz;
+      slots[(gg * nw + wave) * R + i] = t;
+    } else {
+      emit(r - row_lo, t, up);
+    }
+  };
   // One step on buffers (c, cu_); when `more` (a compile-time flag, so the
   // loads stay branch-free and their waits exact) the next step's loads go
   // to (n, nu_) first.
@@ -672,7 +723,9 @@ __device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&em
         acc2[i] += live ? d2 : 0.f;
       }
     }
-    if (itn == 0 && packed) {  // the row group is complete: per-half sums
+    // The row group is complete, or (balanced split) the wave's range ends.
+    const bool flush = itn == 0 || (BAL && bal && !decltype(more)::value);
+    if (flush && packed) {  // per-half sums
       if constexpr (DUAL) {
         // gate rows 0, 1 in lane groups 0/8, up rows in 16/24 of each half.
         float v[4] = {acc[0], acc[1], acc2[0], acc2[1]};
@@ -680,24 +733,24 @@ __device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&em
         float up = __shfl_xor(t, 16, 64);
         if ((lane & 23) == 0) {  // lanes 0, 8, 32, 40
           int r = r0 + ((lane >> 3) & 1);
-          if (r < row_hi) emit(r - row_lo, t, up);
+          if (r < row_hi) out(r, t, up);
         }
       } else if constexpr (R == 4) {
         float t = half_sum4(acc, lane);
         if ((lane & 7) == 0) {
           int r = r0 + ((lane >> 3) & 3);
-          if (r < row_hi) emit(r - row_lo, t, 0.f);
+          if (r < row_hi) out(r, t, 0.f);
         }
       } else {
         float t = half_sum2(acc[0], acc[1], lane);
         if ((lane & 15) == 0) {
           int r = r0 + ((lane >> 4) & 1);
-          if (r < row_hi) emit(r - row_lo, t, 0.f);
+          if (r < row_hi) out(r, t, 0.f);
         }
       }
 #pragma unroll
       for (int i = 0; i < R; i++) acc[i] = acc2[i] = 0.f;
-    } else if (itn == 0) {  // the row group is complete
+    } else if (flush) {
       if constexpr (DUAL) {
         // rows 0, 1 of gate and of up: gate sums land in lanes 0/16, up in 32/48.
         float v[4] = {acc[0], acc[1], acc2[0], acc2[1]};
@@ -705,19 +758,19 @@ __device__ __forceinline__ void SegStream<TY, DUAL>::run(const Lds &L, Emit &&em
         float up = __shfl_xor(t, 32, 64);
         if ((lane & 47) == 0) {  // lanes 0 and 16
           int r = r0 + ((lane >> 4) & 1);
-          if (r < row_hi) emit(r - row_lo, t, up);
+          if (r < row_hi) out(r, t, up);
         }
       } else if constexpr (R == 4) {
         float t = wave_sum4(acc, lane);
         if ((lane & 15) == 0) {
           int r = r0 + (((lane >> 5) << 1) | ((lane >> 4) & 1));
-          if (r < row_hi) emit(r - row_lo, t, 0.f);
+          if (r < row_hi) out(r, t, 0.f);
         }
       } else {
         float t = wave_sum2(acc[0], acc[1], lane);
         if ((lane & 31) == 0) {
           int r = r0 + (lane >> 5);
-          if (r < row_hi) emit(r - row_lo, t, 0.f);
+          if (r < row_hi) out(r, t, 0.f);
         }
       }
 #pragma unroll
@@ -752,7 +805,12 @@ template <uint32_t TA, uint32_t TB, bool DUAL, bool COH>
 struct GemvPhase {
   int lane, wave, nw, wg, nwg, wrow0, wrow1, s0, base0;
   bool s0_is_ta;
-  SegStream<TA, DUAL> A;
+  // The balanced split's partials (set when a.bal and the workgroup's rows
+  // lie in one segment).
+  float *slots;
+  // The balanced split in the standalone GEMV only (COH: the persistent kernel).
+  static constexpr bool BAL = !COH && !DUAL;
+  SegStream<TA, DUAL, BAL> A;
 #ifdef LLRS_STAMPS
   // Timing build only: wall-clock stamps of this workgroup's phase, [1] when
   // the activation is staged, [2] when the weight streaming ends.
@@ -768,7 +826,8 @@ struct GemvPhase {
     hi = min(wrow1, base + a.seg[s].rows);
   }
 
-  __device__ __forceinline__ void prefetch(const FastGemvArgs &a, int wg_, int nwg_) {
+  // smem: the launch's dynamic LDS (only its address is taken here).
+  __device__ __forceinline__ void prefetch(const FastGemvArgs &a, int wg_, int nwg_, uint8_t *smem) {
     wg = wg_;
     nwg = nwg_;
     lane = thread_x() & 63;
@@ -781,12 +840,28 @@ struct GemvPhase {
     base0 = 0;
     while (s0 + 1 < a.nseg && wrow0 >= base0 + a.seg[s0].rows) base0 += a.seg[s0++].rows;
     s0_is_ta = DUAL || TA == TB || s0 + 1 < a.nseg;
+    const bool one_seg = wrow1 <= base0 + a.seg[s0].rows;
+    slots = BAL && a.bal && one_seg
+                ? reinterpret_cast<float *>(smem + fast_gemv_digit_bytes(a.cols) + fast_gemv_ybuf_bytes(wrow1 - wrow0))
+                : nullptr;
     if (s0_is_ta) {
       int lo, hi;
       seg_range(a, s0, base0, lo, hi);
       const FastSeg Sw = shifted(a.seg[s0], lo - base0);
       const FastSeg Uw = DUAL ? shifted(a.seg[1], lo - base0) : Sw;
-      A.begin(Sw, Uw, lo, max(lo, hi), wave, nw, a.cols, lane);
+      A.begin(Sw, Uw, lo, max(lo, hi), wave, nw, a.cols, lane, slots);
+    }
+  }
+
+  // Row results of a balanced stream: the partials of row i's group summed
+  // over the waves in order (slots the waves did not write are zero).
+  template <class SS, class Emit>
+  __device__ __forceinline__ void bal_reduce(Emit &&emit) const {
+    for (int i = thread_x(); i < wrow1 - wrow0; i += blockDim.x) {
+      const float *sl = slots + (i / SS::R) * nw * SS::R + i % SS::R;
+      float t = 0.f;
+      for (int w = 0; w < nw; w++) t += sl[w * SS::R];
+      emit(i, t, 0.f);
     }
   }
 
@@ -794,6 +869,10 @@ struct GemvPhase {
   // loads: every buffer a phase reads was written before any workgroup of the
   // launch first read it, so no cache holds a stale copy.
   __device__ void finish(const FastGemvArgs &a, uint8_t *smem, float *red) {
+    // The balanced split's partials start at zero (ordered before the
+    // streaming by the staging's workgroup barrier).
+    if (BAL && slots)
+      for (int i = thread_x(); i < (int)(bal_slot_bytes(nw) / 4); i += blockDim.x) slots[i] = 0.f;
     float inv = 1.0f;
     if (a.dig_in)
       load_digits<false>(a.dig_in, a.cols, smem);
@@ -825,6 +904,7 @@ struct GemvPhase {
     // first one's loads are already in flight.  Dual launches have one segment.
     const int nseg_a = (DUAL || TA == TB) ? a.nseg : a.nseg - 1;
     int base = base0;
+    bool bal_a = false, bal_b = false;
     for (int s = s0; s < nseg_a; s++) {
       const FastSeg &S = a.seg[s];
       int lo, hi;
@@ -832,9 +912,10 @@ struct GemvPhase {
       if (lo < hi) {
         if (!DUAL && s != s0) {
           const FastSeg Sw = shifted(S, lo - base);
-          A.begin(Sw, Sw, lo, hi, wave, nw, a.cols, lane);
+          A.begin(Sw, Sw, lo, hi, wave, nw, a.cols, lane, slots);
         }
         A.run(L, emitter(lo));
+        bal_a = A.bal;
       }
       base += S.rows;
     }
@@ -846,13 +927,25 @@ struct GemvPhase {
         seg_range(a, s, base, lo, hi);
         if (lo < hi) {
           const FastSeg Sw = shifted(S, lo - base);
-          SegStream<TB, false> B;
-          B.begin(Sw, Sw, lo, hi, wave, nw, a.cols, lane);
+          SegStream<TB, false, BAL> B;
+          B.begin(Sw, Sw, lo, hi, wave, nw, a.cols, lane, slots);
           B.run(L, emitter(lo));
+          bal_b = B.bal;
         }
       }
     }
     __syncthreads();
+    // bal_a / bal_b are the same in every wave (they depend on the
+    // workgroup's rows only), so the barrier below is uniform.
+    if constexpr (BAL) {
+      if (bal_a || bal_b) {
+        if (bal_a)
+          bal_reduce<SegStream<TA, false, true>>(emitter(wrow0));
+        else
+          bal_reduce<SegStream<TB, false, true>>(emitter(wrow0));
+        __syncthreads();
+      }
+    }
 #ifdef LLRS_STAMPS
     if (stamp && thread_x() == 0) stamp[2] = wall_clock64();
 #endif

@@ -15,20 +15,21 @@ __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[16];
   GemvPhase<TA, TB, DUAL, false> ph;
-  ph.prefetch(a, blockIdx.x, gridDim.x);
+  ph.prefetch(a, blockIdx.x, gridDim.x, smem);
   ph.finish(a, smem, red);
 }
 
 }  // namespace
 
-size_t fast_gemv_lds_bytes(const FastGemvArgs &a, int grid) {
+size_t fast_gemv_lds_bytes(const FastGemvArgs &a, int grid, int threads) {
   int most = 0;
   for (int w = 0; w < grid; w++) {
     int r0, r1;
     fast_gemv_rows(a, w, grid, r0, r1);
     most = r1 - r0 > most ? r1 - r0 : most;
   }
-  return fast_gemv_digit_bytes(a.cols) + (size_t)most * sizeof(float);
+  return fast_gemv_digit_bytes(a.cols) + fast_gemv_ybuf_bytes(most) +
+         (a.bal ? bal_slot_bytes(threads >> 6) : 0);
 }
 
 bool fast_gemv_supports(uint32_t type, size_t cols) {

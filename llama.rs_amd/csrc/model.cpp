@@ -654,6 +654,8 @@ static FastGemvArgs projection_args(llrs_model *m, llrs_kv *kv, size_t l, int wh
   a.eps = c.rms_norm_eps;
   a.cols = H;
   a.x = kv->residual;
+  // No balanced split (bal = 0): in the decode step its partial-sum pass cost
+  // more than the idle waves it fills.
   if (which == P_LM_HEAD) {
     a.seg[0] = seg_of(m->lm_head, nullptr, kv->logits);
     a.nseg = 1;
@@ -917,6 +919,10 @@ static int setup_persistent(llrs_model *m, llrs_kv *kv) {
     if (!decode_persistent_supports(t[0], t[1], t[2], t[3], t[4], (int)c.head_dim)) return LLRS_OK;
   }
   const int grid = m->b->cu_count;
+  // The attention tasks' wait order needs at least 8 G workgroups, and the
+  // task partials two LDS buffers.
+  if (grid < 8 * (int)(c.num_attention_heads / c.num_key_value_heads)) return LLRS_OK;
+  static_assert(2 * kTaskItems * (2 * 128 + 2) * 4 <= kPersistentMinLds, "attention partials fit the LDS");
   // Per-layer activation buffers (each slice 256-byte aligned, so no cache
   // line holds two buffers): q|k|v, attention output, residual after o_proj
   // and after ffn_down, SiLU*up digits.  The last layer's ffn_down writes
@@ -962,7 +968,7 @@ static int setup_persistent(llrs_model *m, llrs_kv *kv) {
     P.down.seg[0].out = x_out;
     if (!P.gate_up.dig_out || P.gate_up.part != 16) return LLRS_OK;
     for (const FastGemvArgs *a : {&P.qkv, &P.o, &P.gate_up, &P.down})
-      lds = std::max(lds, fast_gemv_lds_bytes(*a, grid));
+      lds = std::max(lds, fast_gemv_lds_bytes(*a, grid, kPersistentThreads));
     x_in = x_out;
   }
   // More than half a CU's LDS per workgroup: exactly one workgroup per CU.

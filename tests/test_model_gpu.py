@@ -243,11 +243,11 @@ def test_prefill_attention_f16_and_f32(llrs, backend, oracle, tmp_path, monkeypa
                 assert float(np.abs(a - b).max()) <= 1e-3 * max(1.0, float(np.abs(b).max()))
 
 
-def test_attention_merge_in_two_levels(llrs, backend, oracle, tmp_path):
-    """Past 64 chunks (2,048 positions) a head's partials merge in two levels:
-    the last chunk of each group of 16 folds its group, the head's last chunk
-    its own group and then the group partials.  The decode runs from position
-    2,030 across 2,048: one-level merges first, two-level after.  (Seed 43:
+def test_attention_task_sizes_across_2048(llrs, backend, oracle, tmp_path):
+    """Attention items merge in tasks of T items (in LDS), then across a
+    head's tasks (through the scratch partials).  At head_dim 128 a head of
+    64 chunks (up to position 2,047) runs tasks of 4 items, from 65 chunks
+    tasks of 8.  The decode runs from position 2,030 across 2,048.  (Seed 43:
     the oracle's top-2 logit gap stays above 4.5e-3 on every step.)"""
     cfg = tiny_cfg(llrs, hidden_size=1024, num_attention_heads=8, num_key_value_heads=2,
                    intermediate_size=1024, num_hidden_layers=1, vocab_size=600,
@@ -441,7 +441,7 @@ def test_config3_qwen05b_shape_greedy_parity(llrs, backend, oracle, tmp_path):
         assert llrs.gguf_read_tensor(tmp_path / "c3.gguf", name)[1].quant_type == qt, name
 
 
-@pytest.mark.parametrize("n_prompt", [70, 2100], ids=["one_level", "two_level"])
+@pytest.mark.parametrize("n_prompt", [70, 2100], ids=["one_task", "many_tasks"])
 @pytest.mark.parametrize("decode_path", ["persistent", "per_phase"])
 def test_softmax_uniform_fallback_on_gpu(llrs, backend, oracle, tmp_path, monkeypatch, decode_path, n_prompt):
     """A NaN query bias in layer 0 makes every score NaN: the GPU attention must
@@ -451,10 +451,10 @@ def test_softmax_uniform_fallback_on_gpu(llrs, backend, oracle, tmp_path, monkey
     merged, each chunk's partial non-finite); the batched prefill's attention
     tiles; then 8 decode steps from position 70, every step's logits against
     the oracle's.  A 2,100-token prompt then decodes past 2,100 positions
-    (66 chunks per head, more than 64: the merge runs in two levels, group
-    leaders publishing non-finite group partials and the last item summing
-    every chunk's V sums).  Once on the persistent decode kernel, once on the
-    launch-per-phase path."""
+    (66 chunks per head at head_dim 64: 33 tasks of 2 items, whose LDS
+    merges and the head's fold see non-finite partials, and the last task
+    sums every task's V sums; the 70-token run has one task per head).  Once on the persistent decode kernel, once on the launch-per-phase
+    path."""
     cfg = tiny_cfg(llrs, seed=29, num_hidden_layers=2, max_position_embeddings=4096)
     path = tmp_path / "n.gguf"
     cfg.write_gguf(path)
