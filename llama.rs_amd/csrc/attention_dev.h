@@ -403,7 +403,7 @@ __device__ void attention_round(const AttnArgs &a, int pos, Slot &&slot, float *
 #pragma clang fp contract(off)
   using Gm = AttnGeom<HD>;
   constexpr int VW = Gm::VW, VL = Gm::VL, PF = Gm::kPart;
-  const int wave = __builtin_amdgcn_readfirstlane(thread_x() >> 6), lane = thread_x() & 63;
+  const int wave = thread_x() >> 6, lane = thread_x() & 63;
   const int vd = (lane % VL) * VW;
   const int S = MULTI ? attention_span(pos, a.nh) : 1;
   const int n_items = pos / (S * kChunk) + 1;

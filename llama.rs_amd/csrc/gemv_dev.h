@@ -801,15 +801,16 @@ __device__ __forceinline__ void SegStream<TY, DUAL, BAL>::run(const Lds &L, Emit
 // prefetch() picks the workgroup's rows and issues its first weight loads
 // (they depend on nothing the previous phase writes); finish() stages the
 // activation, streams the rest and runs the epilogue.
-template <uint32_t TA, uint32_t TB, bool DUAL, bool COH>
+template <uint32_t TA, uint32_t TB, bool DUAL, bool COH, bool BALANCED = false>
 struct GemvPhase {
   int lane, wave, nw, wg, nwg, wrow0, wrow1, s0, base0;
   bool s0_is_ta;
   // The balanced split's partials (set when a.bal and the workgroup's rows
   // lie in one segment).
   float *slots;
-  // The balanced split in the standalone GEMV only (COH: the persistent kernel).
-  static constexpr bool BAL = !COH && !DUAL;
+  // The balanced split: its own instantiation of the standalone GEMV, for
+  // launches that ask for it (its code costs the others registers).
+  static constexpr bool BAL = BALANCED && !COH && !DUAL;
   SegStream<TA, DUAL, BAL> A;
 #ifdef LLRS_STAMPS
   // Timing build only: wall-clock stamps of this workgroup's phase, [1] when

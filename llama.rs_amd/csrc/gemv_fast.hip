@@ -10,11 +10,11 @@ namespace llrs {
 
 namespace {
 
-template <uint32_t TA, uint32_t TB, bool DUAL>
+template <uint32_t TA, uint32_t TB, bool DUAL, bool BAL>
 __global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[16];
-  GemvPhase<TA, TB, DUAL, false> ph;
+  GemvPhase<TA, TB, DUAL, false, BAL> ph;
   ph.prefetch(a, blockIdx.x, gridDim.x, smem);
   ph.finish(a, smem, red);
 }
@@ -41,9 +41,9 @@ bool fast_gemv_supports(uint32_t type, size_t cols) {
   }
 }
 
-template <uint32_t TA, uint32_t TB, bool DUAL>
+template <uint32_t TA, uint32_t TB, bool DUAL, bool BAL = false>
 static void launch_one(const FastGemvArgs &args, int grid, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((gemv_fast_kernel<TA, TB, DUAL>), dim3(grid), dim3(256), lds, s, args);
+  hipLaunchKernelGGL((gemv_fast_kernel<TA, TB, DUAL, BAL>), dim3(grid), dim3(256), lds, s, args);
 }
 
 int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
@@ -76,11 +76,21 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
     LLRS_HIP(hipGetLastError());                   \
     return LLRS_OK;                                \
   }
-  PAIR(LLRS_Q4_K, LLRS_Q4_K) PAIR(LLRS_Q6_K, LLRS_Q6_K) PAIR(LLRS_Q8_0, LLRS_Q8_0)
-  PAIR(LLRS_Q5_0, LLRS_Q5_0) PAIR(LLRS_Q4_K, LLRS_Q8_0) PAIR(LLRS_Q5_0, LLRS_Q8_0)
+  // One type: the balanced split when asked for.
+#define SAME(A)                                          \
+  if (ta == A && tb == A) {                              \
+    if (args.bal)                                        \
+      launch_one<A, A, false, true>(args, grid, lds, s); \
+    else                                                 \
+      launch_one<A, A, false>(args, grid, lds, s);       \
+    LLRS_HIP(hipGetLastError());                         \
+    return LLRS_OK;                                      \
+  }
+  SAME(LLRS_Q4_K) SAME(LLRS_Q6_K) SAME(LLRS_Q8_0) SAME(LLRS_Q5_0)
+  PAIR(LLRS_Q4_K, LLRS_Q8_0) PAIR(LLRS_Q5_0, LLRS_Q8_0)
   PAIR(LLRS_Q4_K, LLRS_Q6_K) PAIR(LLRS_Q4_K, LLRS_Q5_0)
-  PAIR(LLRS_Q4_0, LLRS_Q4_0) PAIR(LLRS_Q4_1, LLRS_Q4_1) PAIR(LLRS_Q5_1, LLRS_Q5_1)
-  PAIR(LLRS_Q5_K, LLRS_Q5_K)
+  SAME(LLRS_Q4_0) SAME(LLRS_Q4_1) SAME(LLRS_Q5_1) SAME(LLRS_Q5_K)
+#undef SAME
 #undef PAIR
   return set_error(LLRS_E_UNSUPPORTED, "no tuned GEMV for %s + %s", type_name(ta), type_name(tb));
 }
