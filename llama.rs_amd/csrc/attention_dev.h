@@ -407,7 +407,7 @@ __device__ void attention_round(const AttnArgs &a, int pos, Slot &&slot, float *
   const int vd = (lane % VL) * VW;
   const int S = MULTI ? attention_span(pos, a.nh) : 1;
   const int n_items = pos / (S * kChunk) + 1;
-  const int T = attention_task_items(n_items, HD), lt = __builtin_ctz(T);  // T is a power of two
+  const int T = attention_task_items(n_items, a.fold_max), lt = __builtin_ctz(T);  // T is a power of two
   const int n_tasks = (n_items + T - 1) >> lt;
   const int sl = wave >> lt, wi = wave & (T - 1);
   int h = 0, task = 0;

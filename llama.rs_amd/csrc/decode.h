@@ -21,20 +21,21 @@ __host__ __device__ inline int attention_span(int pos, int nh) {
 }
 // Attention tasks: T consecutive items of one head, one per wave of a
 // workgroup of kTaskItems waves, whose partials meet in LDS; the head's tasks
-// then meet through the scratch partials, folded by the head's last task in
-// loads of 32 / VW partials (VW = 2 V floats per lane at head_dim 128, else
-// 1).  T (1, 2, 4 or 8): kTaskItems while a head has at most that many items
-// (its task alone writes the output), else the smallest that lets the fold
-// take one load: larger tasks gather more items on one CU, whose loads then
-// queue behind each other.
+// then meet through the scratch partials, folded by the head's last task.  T
+// (1, 2, 4 or 8): kTaskItems while a head has at most that many items (its
+// task alone writes the output), else the smallest that leaves the fold at
+// most `fold` partials (AttnArgs::fold_max): larger tasks gather more items
+// on one CU, whose loads then queue behind each other.
 constexpr int kTaskItems = 8;
-__host__ __device__ inline int attention_task_items(int n_items, int hd) {
+__host__ __device__ inline int attention_task_items(int n_items, int fold) {
   if (n_items <= kTaskItems) return kTaskItems;
-  const int fold = hd >= 128 ? 16 : 32;
   int t = 1;
   while (t < kTaskItems && (n_items + t - 1) / t - 1 > fold) t *= 2;
   return t;
 }
+// The default fold bound: the partials one load round of the fold reads
+// (32 / VW, VW = 2 V floats per lane at head_dim 128, else 1).
+inline int attention_fold_default(int hd) { return hd >= 128 ? 16 : 32; }
 // Workgroups per head of the attention kernel: kTaskItems items each.
 __host__ __device__ inline int attention_blocks(int max_chunks) { return (max_chunks + kTaskItems - 1) / kTaskItems; }
 // From this position the persistent kernel issues an attention item's key
@@ -60,6 +61,7 @@ struct AttnArgs {
   int nh, nkv, hd, max_seq;
   int max_chunks;            // attention_chunks(max_seq)
   long part_stride;          // attention_part_stride(hd): words per (head, task) partial
+  int fold_max;              // attention_task_items' fold bound
   float scale;               // 1/sqrt(hd)
 };
 

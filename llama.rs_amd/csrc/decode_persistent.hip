@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
   const int G = p.attn.nh / p.attn.nkv;
   const int span = LONG ? attention_span(pos, p.attn.nh) : 1;
   const int n_items_h = pos / (span * kChunk) + 1;
-  const int task_items = attention_task_items(n_items_h, HD);
+  const int task_items = attention_task_items(n_items_h, p.attn.fold_max);
   const int n_task_h = (n_items_h + task_items - 1) / task_items;
   const int per_round = kTaskItems / task_items;
   const int n_pairs = p.attn.nkv * n_task_h;

@@ -791,6 +791,11 @@ static AttnArgs attention_args(llrs_model *m, llrs_kv *kv, size_t l) {
   at.max_seq = (int)kv->max_seq_len;
   at.max_chunks = attention_chunks(at.max_seq);
   at.part_stride = attention_part_stride(at.hd);
+  at.fold_max = attention_fold_default(at.hd);
+  if (const char *e = getenv("LLRS_ATTN_FOLD")) {  // tuning: another fold bound
+    const int f = atoi(e);
+    if (f > 0) at.fold_max = f;
+  }
   at.scale = 1.0f / sqrtf((float)c.head_dim);
   return at;
 }
