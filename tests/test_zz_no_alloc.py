@@ -62,12 +62,15 @@ def test_sample_noalloc_matches_sample(llrs, backend):
         assert noalloc(llrs, kv, cases[2], [], 0.5) == kv.sample(cases[2], 0.5, [])
 
 
-def free_device_bytes() -> int:
-    """hipMemGetInfo's free bytes of the current device (the HIP runtime the
-    library already initialised)."""
-    hip = C.CDLL("libamdhip64.so")
+def free_device_bytes(llrs) -> int:
+    """hipMemGetInfo's free bytes of the current device, looked up through the
+    library's own handle: the HIP runtime it links and has initialised (a
+    separate dlopen of libamdhip64.so may load another copy that sees no
+    device)."""
+    f = llrs.lib().hipMemGetInfo
+    f.restype, f.argtypes = C.c_int, [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
     free, total = C.c_size_t(), C.c_size_t()
-    assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    assert f(C.byref(free), C.byref(total)) == 0
     return free.value
 
 
@@ -78,15 +81,15 @@ def test_sample_noalloc_allocates_nothing(llrs, backend):
     noalloc(llrs, warm, opts, recent, 0.5)  # the sampler's code is resident before the probe
     _, kv = model_kv(llrs, backend, 152064, 6)  # a fresh cache: no sampler scratch yet
     backend.synchronize()
-    before = free_device_bytes()
+    before = free_device_bytes(llrs)
     for u in (0.1, 0.5, 0.9):
         noalloc(llrs, kv, opts, recent, u)
-    after = free_device_bytes()
+    after = free_device_bytes(llrs)
     print(f"[noalloc] free bytes {before} -> {after}", flush=True)
     assert after == before
     # The probe sees an allocation: llrs_sample's first call allocates its scratch.
     kv.sample(opts, 0.5, recent)
-    allocated = free_device_bytes()
+    allocated = free_device_bytes(llrs)
     print(f"[noalloc] llrs_sample's first call: free bytes {after} -> {allocated}", flush=True)
     assert allocated < after
 
