@@ -76,16 +76,19 @@ __global__ __launch_bounds__(64 * kTaskItems) void attention_kernel(AttnArgs a) 
   __shared__ __align__(16) float qs[kTaskItems][HD], kn[kTaskItems][HD];
   __shared__ __align__(16) float part[kTaskItems * AttnGeom<HD>::kPart];
   a.tag = *a.epoch * (unsigned)a.nlayers + (unsigned)a.layer;
-  // Grid (head, block of kTaskItems items): the low blocks, the ones that
-  // run, are dispatched first, so the task that merges a head always starts
-  // with or after the tasks it waits for.
+  // Grid (head, y): block y runs tasks y, y + Y, y + 2Y, .. (Y = gridDim.y,
+  // up to kTaskItems / T of them), so the tasks spread over the blocks as
+  // the persistent kernel spreads them over its workgroups.  Blocks past the
+  // head's tasks exit at once.  A head's last task waits only for tasks
+  // that never wait (one waiting block per head), so every wait ends.
   const int pos = bounded_pos(a.pos, a.max_seq);
   const int S = attention_span(pos, a.nh);
-  if ((int)blockIdx.y * kTaskItems * S * kChunk > pos) return;
+  const int n_items = pos / (S * kChunk) + 1, T = attention_task_items(n_items, a.fold_max);
+  if ((int)blockIdx.y >= (n_items + T - 1) / T) return;
   const int wave = threadIdx.x >> 6;
-  auto slot = [&](int s, int T, int n_tasks, int &h, int &task) {
+  auto slot = [&](int s, int, int n_tasks, int &h, int &task) {
     h = blockIdx.x;
-    task = blockIdx.y * (kTaskItems / T) + s;  // T divides kTaskItems
+    task = blockIdx.y + s * gridDim.y;
     return task < n_tasks;
   };
   if (S > 1)
