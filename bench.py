@@ -173,6 +173,27 @@ TUNED_TYPES = ("Q4K", "Q5K", "Q6K", "Q8_0", "Q5_0", "Q4_0", "Q4_1", "Q5_1")
 FLOAT_TYPES = ("F32", "F16", "BF16")
 
 
+LDS_PROBE_MODES = ("read32 conflict-free", "read64 conflict-free", "read128 conflict-free",
+                   "read32 one bank", "write128 conflict-free")
+
+
+def lds_probe(llrs, be, iters: int) -> int:
+    """The LDS access-pattern probe (llrs_debug_lds_probe): each mode once,
+    512 workgroups of 256 threads, `iters` LDS accesses per thread; run under
+    rocprofv3 --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE to read what the
+    counters report for known bank patterns."""
+    lib = llrs.lib()
+    out = []
+    for mode, name in enumerate(LDS_PROBE_MODES):
+        t0 = time.perf_counter()
+        llrs._check(lib.llrs_debug_lds_probe(be.handle, mode, 512, iters))
+        dt = time.perf_counter() - t0
+        out.append({"mode": mode, "pattern": name, "blocks": 512, "iters": iters, "ms": round(dt * 1e3, 3)})
+        log(f"lds probe mode {mode} ({name}): {dt * 1e3:.2f} ms")
+    print(json.dumps({"lds_probe": out}), flush=True)
+    return 0
+
+
 def gemv_cpu(oracle, kernel, threads: int, data: bytes, ty: int, rows: int, cols: int,
              x: np.ndarray, reps: int) -> float:
     """Median seconds of `reps` oracle matvecs (CpuBackend::matvec with the
@@ -437,6 +458,8 @@ def main() -> int:
                          "calibration copy (the workload of the rocprofv3 --pmc traffic runs)")
     ap.add_argument("--gemv", action="store_true",
                     help="configs 1 and 2 instead: single GEMVs per type over rotating weight copies")
+    ap.add_argument("--lds-probe", type=int, default=0, metavar="ITERS",
+                    help="instead: the LDS bank-pattern probe kernels, ITERS accesses per thread")
     ap.add_argument("--gemv-cpu-reps", type=int, default=20,
                     help="--gemv: host oracle calls per case and path (median; 0 = no CPU timing)")
     ap.add_argument("--load", action="store_true",
@@ -460,6 +483,8 @@ def main() -> int:
     llrs = package()
     be = llrs.HipBackend(0)
     log(f"backend {be.name()} with {be.threads()} CUs")
+    if args.lds_probe:
+        return lds_probe(llrs, be, args.lds_probe)
     if args.gemv:
         return gemv_sweep(llrs, be, 0 if args.no_cpu_baseline else args.gemv_cpu_reps)
     if args.load:

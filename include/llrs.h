@@ -221,6 +221,13 @@ int llrs_kv_reset(llrs_kv *kv);
  * merge) so that tests can exercise the reporting path; no counterpart in
  * the reference. */
 int llrs_kv_debug_set_wait_flag(llrs_kv *kv, int which);
+/* Measurement only, no counterpart in the reference: runs `blocks`
+ * workgroups of an LDS access-pattern probe for `iters` iterations and
+ * waits for them (mode 0: conflict-free 32-bit reads, 1: 64-bit reads, 2:
+ * 128-bit reads, 3: 32-bit reads with every lane in one bank, 4:
+ * conflict-free 128-bit writes), so that the LDS counters can be read
+ * against a known bank pattern (bench.py --lds-probe). */
+int llrs_debug_lds_probe(llrs_backend *b, int mode, int blocks, int iters);
 /* Which implementation runs this state's decode steps: 1 = one persistent
  * launch for all layers (chosen at llrs_kv_create when the model's weight
  * types and head_dim have an instantiation and LLRS_NO_PERSISTENT is unset),

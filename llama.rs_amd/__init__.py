@@ -131,6 +131,7 @@ SIGNATURES = [
     ("llrs_kv_reset", C.c_int, [P]),
     ("llrs_kv_decode_path", C.c_int, [P]),
     ("llrs_kv_debug_set_wait_flag", C.c_int, [P, C.c_int]),
+    ("llrs_debug_lds_probe", C.c_int, [P, C.c_int, C.c_int, C.c_int]),
     ("llrs_forward_token", C.c_int, [P, P, C.c_uint32, SZ, C.c_int]),
     ("llrs_prefill", C.c_int, [P, P, U32P, SZ, SZ]),
     ("llrs_decode_greedy", C.c_int, [P, P, SZ, SZ, U32P]),
