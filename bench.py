@@ -174,7 +174,10 @@ FLOAT_TYPES = ("F32", "F16", "BF16")
 
 
 LDS_PROBE_MODES = ("read32 conflict-free", "read64 conflict-free", "read128 conflict-free",
-                   "read32 one bank", "write128 conflict-free")
+                   "read32 one bank", "write128 conflict-free", "read128 MFMA fragment, 144-byte rows",
+                   "read128 MFMA fragment, 176-byte rows", "write128 staging, 144-byte rows",
+                   "read128 256 B runs, unaligned", "read128 256 B runs, aligned",
+                   "write128 chunk-major staging, swizzled", "write128 chunk-major staging, plain")
 
 
 def lds_probe(llrs, be, iters: int) -> int:

@@ -225,8 +225,12 @@ int llrs_kv_debug_set_wait_flag(llrs_kv *kv, int which);
  * workgroups of an LDS access-pattern probe for `iters` iterations and
  * waits for them (mode 0: conflict-free 32-bit reads, 1: 64-bit reads, 2:
  * 128-bit reads, 3: 32-bit reads with every lane in one bank, 4:
- * conflict-free 128-bit writes), so that the LDS counters can be read
- * against a known bank pattern (bench.py --lds-probe). */
+ * conflict-free 128-bit writes, 5 and 6: 128-bit MFMA operand reads from
+ * rows 144 and 176 bytes apart, 7: 128-bit staging writes to rows 144 bytes
+ * apart, 8 and 9: 128-bit reads of 256-byte runs at unaligned and aligned
+ * offsets, 10 and 11: chunk-major staging writes with and without a row
+ * swizzle), so that the LDS counters can be read against a known bank
+ * pattern (bench.py --lds-probe). */
 int llrs_debug_lds_probe(llrs_backend *b, int mode, int blocks, int iters);
 /* Which implementation runs this state's decode steps: 1 = one persistent
  * launch for all layers (chosen at llrs_kv_create when the model's weight

@@ -22,6 +22,20 @@ constexpr int kProbeFloats = 8192;  // 32 KB of LDS per workgroup
 // MODE 2: ds_read_b128, lane l reads dwords 4l .. 4l + 3 (conflict-free).
 // MODE 3: ds_read_b32, lane l reads dword 64 l (every lane in bank 0).
 // MODE 4: ds_write_b128, lane l writes dwords 4l .. 4l + 3 (conflict-free).
+// MODE 5: ds_read_b128 of an MFMA 16x16x32 operand fragment from a tile with
+//         rows 144 bytes apart (the prefill GEMMs' LDS row stride): lane l
+//         reads row l % 16 at byte 16 (l / 16).
+// MODE 6: as 5 with rows 176 bytes apart.
+// MODE 7: ds_write_b128 of the prefill GEMMs' staging pattern: lane l writes
+//         16 bytes at row l / 2, byte 64 (l % 2) (+16 per iteration's row),
+//         rows 144 bytes apart.
+// MODE 8: ds_read_b128, lanes 16g .. 16g + 15 read 256 contiguous bytes at
+//         byte 2064 g + 16 (not 256-byte aligned).
+// MODE 9: as 8 at byte 2048 g (256-byte aligned).
+// MODE 10: ds_write_b128, lane l writes row l / 2 of chunk c = 4 (l % 2) +
+//         (iteration % 4), chunks 2048 bytes apart, the row's 16-byte slot
+//         XOR-swizzled by 2 (c / 2).
+// MODE 11: as 10 without the swizzle.
 // Each iteration moves to another row; the sums go to `out` so nothing is
 // eliminated.
 template <int MODE>
@@ -43,6 +57,23 @@ __global__ __launch_bounds__(kProbeThreads) void lds_probe_kernel(float *out, in
       acc += v.x + v.y + v.z + v.w;
     } else if constexpr (MODE == 3) {
       acc += buf[(row * 8 + lane * 64) & (kProbeFloats - 1)];
+    } else if constexpr (MODE == 5 || MODE == 6) {
+      constexpr int RS = MODE == 5 ? 36 : 44;  // row stride in dwords
+      const float4 v = *reinterpret_cast<const float4 *>(&buf[(row & 7) * 1024 + (lane & 15) * RS + 4 * (lane >> 4)]);
+      acc += v.x + v.y + v.z + v.w;
+    } else if constexpr (MODE == 8 || MODE == 9) {
+      const int o = (MODE == 8 ? 516 * (lane >> 4) + 4 : 512 * (lane >> 4)) + 4 * (lane & 15);
+      const float4 v = *reinterpret_cast<const float4 *>(&buf[o + (row & 3) * 64]);
+      acc += v.x + v.y + v.z + v.w;
+    } else if constexpr (MODE == 10 || MODE == 11) {
+      const int c = 4 * (lane & 1) + (it & 3), r = lane >> 1;
+      const int slot = MODE == 10 ? ((r & ~15) | ((r ^ (2 * (c >> 1))) & 15)) : r;
+      *reinterpret_cast<float4 *>(&buf[c * 512 + slot * 4]) = make_float4(acc, acc, acc, acc);
+      acc += 1.f;
+    } else if constexpr (MODE == 7) {
+      *reinterpret_cast<float4 *>(&buf[(lane >> 1) * 36 + 16 * (lane & 1) + 4 * (it & 3)]) =
+          make_float4(acc, acc, acc, acc);
+      acc += 1.f;
     } else {
       *reinterpret_cast<float4 *>(&buf[row * 512 + 4 * lane]) = make_float4(acc, acc, acc, acc);
       acc += 1.f;
@@ -51,7 +82,7 @@ __global__ __launch_bounds__(kProbeThreads) void lds_probe_kernel(float *out, in
     // repeat every four iterations, and LDS does not change in between).
     asm volatile("" ::: "memory");
   }
-  if constexpr (MODE == 4) {  // the written rows are read back, so the stores are live
+  if constexpr (MODE == 4 || MODE == 7 || MODE == 10 || MODE == 11) {  // the written rows are read back, so the stores are live
     __syncthreads();
     acc += buf[(tid * 17) & (kProbeFloats - 1)];
   }
@@ -71,8 +102,8 @@ using namespace llrs;
 
 extern "C" int llrs_debug_lds_probe(llrs_backend *b, int mode, int blocks, int iters) {
   if (!b) return set_error(LLRS_E_INVALID, "null backend");
-  if (mode < 0 || mode > 4 || blocks <= 0 || blocks > 65536 || iters <= 0)
-    return set_error(LLRS_E_INVALID, "LDS probe: mode 0..4, 1..65536 blocks, iters > 0");
+  if (mode < 0 || mode > 11 || blocks <= 0 || blocks > 65536 || iters <= 0)
+    return set_error(LLRS_E_INVALID, "LDS probe: mode 0..11, 1..65536 blocks, iters > 0");
   float *out = nullptr;
   LLRS_HIP(hipMalloc((void **)&out, (size_t)blocks * kProbeThreads * sizeof(float)));
   switch (mode) {
@@ -80,7 +111,14 @@ extern "C" int llrs_debug_lds_probe(llrs_backend *b, int mode, int blocks, int i
     case 1: launch_probe<1>(out, blocks, iters, b->stream); break;
     case 2: launch_probe<2>(out, blocks, iters, b->stream); break;
     case 3: launch_probe<3>(out, blocks, iters, b->stream); break;
-    default: launch_probe<4>(out, blocks, iters, b->stream); break;
+    case 4: launch_probe<4>(out, blocks, iters, b->stream); break;
+    case 5: launch_probe<5>(out, blocks, iters, b->stream); break;
+    case 6: launch_probe<6>(out, blocks, iters, b->stream); break;
+    case 7: launch_probe<7>(out, blocks, iters, b->stream); break;
+    case 8: launch_probe<8>(out, blocks, iters, b->stream); break;
+    case 9: launch_probe<9>(out, blocks, iters, b->stream); break;
+    case 10: launch_probe<10>(out, blocks, iters, b->stream); break;
+    default: launch_probe<11>(out, blocks, iters, b->stream); break;
   }
   const hipError_t e = hipGetLastError();
   const hipError_t e2 = hipStreamSynchronize(b->stream);
