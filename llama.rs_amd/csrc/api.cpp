@@ -5,6 +5,7 @@
 // uploaded once in their native GGUF block layout (src/quant.rs:86-157).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -58,7 +59,11 @@ static int launch_matvec(llrs_backend *b, const llrs_tensor *w, const float *x, 
     const char *eb = getenv("LLRS_BAL");
     a.bal = !(eb && *eb == '0');
   }
-  return launch_gemv_fast(a, fast_gemv_grid(b->cu_count, a.rows, a.cols, false, 0), b->stream);
+  // One 512-thread workgroup per CU (two waves per SIMD, one digitised x per
+  // CU): measured faster than 256-thread blocks at one to three per CU on
+  // every tuned type at 18944 x 3584 and 3584 x 18944.
+  const int grid = std::min(b->cu_count, fast_gemv_grid(b->cu_count, a.rows, a.cols, false, 0));
+  return launch_gemv_fast(a, grid, b->stream, 512);
 }
 
 // validate_matvec (src/quant.rs:303-318).

@@ -92,7 +92,9 @@ bool fast_gemv_supports_pair(uint32_t ta, uint32_t tb);
 size_t fast_gemv_lds_bytes(const FastGemvArgs &a, int grid, int threads = 256);
 // Bytes of a digitised activation of n elements (dig_out / dig_in).
 inline size_t fast_gemv_digits_size(size_t n) { return 2 * n + (n / 16) * 8; }
-int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s);
+// `threads`: 256 or 512 per workgroup (the digitised activation is built
+// once per workgroup and shared by its waves).
+int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s, int threads = 256);
 // Workgroups for a launch over `rows` x `cols`, never more than the
 // partition units (`part` rows each; 0 = row pairs).
 int fast_gemv_grid(int cu_count, int rows, int cols, bool dual, int part);

@@ -453,13 +453,31 @@ __device__ __forceinline__ void digit_block(const float (&v)[16], uint4 &d1, uin
 
 // An activation digitised by the kernel that produced it (layout of the LDS
 // image below: [2][cols] digit planes, xs[nb], sx[nb], all in slot order),
-// copied to LDS; the per-32 sums follow from xs and sx.
+// copied to LDS; the per-32 sums follow from xs and sx.  With more than two
+// 16-byte chunks per thread, a thread issues up to kDigitLoads loads before
+// its first LDS store, so the copy takes one memory round trip where a
+// load-store loop takes one per chunk (2,960 chunks at 18,944 columns: six
+// per thread of 512); at one or two chunks per thread the plain loop
+// measured faster.
+constexpr int kDigitLoads = 6;
 template <bool COH>
 __device__ void load_digits(const uint8_t *__restrict__ src, int cols, uint8_t *smem) {
-  const int nb = cols >> 4, nb4 = nb >> 2;
+  const int nb = cols >> 4, nb4 = nb >> 2, nt = blockDim.x;
   const int n16 = (2 * cols + 8 * nb) >> 4;  // 16-byte chunks (cols is a multiple of 64)
-  for (int i = thread_x(); i < n16; i += blockDim.x)
-    reinterpret_cast<uint4 *>(smem)[i] = ld_u4<COH>(src + 16 * (size_t)i);
+  if (n16 > 2 * nt) {
+    for (int i0 = thread_x(); i0 < n16; i0 += kDigitLoads * nt) {
+      uint4 r[kDigitLoads];
+#pragma unroll
+      for (int k = 0; k < kDigitLoads; k++)
+        if (i0 + k * nt < n16) r[k] = ld_u4<COH>(src + 16 * (size_t)(i0 + k * nt));
+#pragma unroll
+      for (int k = 0; k < kDigitLoads; k++)
+        if (i0 + k * nt < n16) reinterpret_cast<uint4 *>(smem)[i0 + k * nt] = r[k];
+    }
+  } else {
+    for (int i = thread_x(); i < n16; i += nt)
+      reinterpret_cast<uint4 *>(smem)[i] = ld_u4<COH>(src + 16 * (size_t)i);
+  }
   __syncthreads();
   const float *xs = reinterpret_cast<const float *>(smem + 2 * cols);
   const int *sx = reinterpret_cast<const int *>(xs + nb);

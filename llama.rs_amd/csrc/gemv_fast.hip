@@ -10,8 +10,8 @@ namespace llrs {
 
 namespace {
 
-template <uint32_t TA, uint32_t TB, bool DUAL, bool BAL>
-__global__ __launch_bounds__(256) void gemv_fast_kernel(FastGemvArgs a) {
+template <uint32_t TA, uint32_t TB, bool DUAL, bool BAL, int NT>
+__global__ __launch_bounds__(NT) void gemv_fast_kernel(FastGemvArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[16];
   GemvPhase<TA, TB, DUAL, false, BAL> ph;
@@ -42,17 +42,21 @@ bool fast_gemv_supports(uint32_t type, size_t cols) {
 }
 
 template <uint32_t TA, uint32_t TB, bool DUAL, bool BAL = false>
-static void launch_one(const FastGemvArgs &args, int grid, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((gemv_fast_kernel<TA, TB, DUAL, BAL>), dim3(grid), dim3(256), lds, s, args);
+static void launch_one(const FastGemvArgs &args, int grid, int threads, size_t lds, hipStream_t s) {
+  if (threads == 512)
+    hipLaunchKernelGGL((gemv_fast_kernel<TA, TB, DUAL, BAL, 512>), dim3(grid), dim3(512), lds, s, args);
+  else
+    hipLaunchKernelGGL((gemv_fast_kernel<TA, TB, DUAL, BAL, 256>), dim3(grid), dim3(256), lds, s, args);
 }
 
-int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
+int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s, int threads) {
   if (grid <= 0) return set_error(LLRS_E_INVALID, "GEMV grid must be positive");
+  if (threads != 256 && threads != 512) return set_error(LLRS_E_INVALID, "GEMV blocks are 256 or 512 threads");
   if (args.dig_out && (args.part != 16 || args.rows % 64))
     return set_error(LLRS_E_INVALID, "a digitised output needs 16-row partitions of a multiple of 64 rows");
   if (args.part && args.part != 2 && args.part != 16)
     return set_error(LLRS_E_INVALID, "GEMV partition of %d rows is not supported", args.part);
-  size_t lds = fast_gemv_lds_bytes(args, grid);
+  size_t lds = fast_gemv_lds_bytes(args, grid, threads);
   if (lds > kMaxLds) return set_error(LLRS_E_UNSUPPORTED, "GEMV needs %zu bytes of LDS (cols %d, rows %d, grid %d)", lds, args.cols, args.rows, grid);
   uint32_t ta = args.seg[0].type, tb = args.seg[args.nseg - 1].type;
   for (int i = 0; i + 1 < args.nseg; i++)
@@ -62,7 +66,7 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
       return set_error(LLRS_E_UNSUPPORTED, "gate and up must share a type");
 #define DUAL1(A)                                  \
   if (ta == A) {                                  \
-    launch_one<A, A, true>(args, grid, lds, s);   \
+    launch_one<A, A, true>(args, grid, threads, lds, s);   \
     LLRS_HIP(hipGetLastError());                  \
     return LLRS_OK;                               \
   }
@@ -72,7 +76,7 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
   }
 #define PAIR(A, B)                                 \
   if (ta == A && tb == B) {                        \
-    launch_one<A, B, false>(args, grid, lds, s);   \
+    launch_one<A, B, false>(args, grid, threads, lds, s);   \
     LLRS_HIP(hipGetLastError());                   \
     return LLRS_OK;                                \
   }
@@ -80,9 +84,9 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s) {
 #define SAME(A)                                          \
   if (ta == A && tb == A) {                              \
     if (args.bal)                                        \
-      launch_one<A, A, false, true>(args, grid, lds, s); \
+      launch_one<A, A, false, true>(args, grid, threads, lds, s); \
     else                                                 \
-      launch_one<A, A, false>(args, grid, lds, s);       \
+      launch_one<A, A, false>(args, grid, threads, lds, s);       \
     LLRS_HIP(hipGetLastError());                         \
     return LLRS_OK;                                      \
   }
