@@ -249,12 +249,6 @@ __global__ __launch_bounds__(kPersistentThreads) void decode_persistent_kernel(P
     }
     {  // RMSNorm + gate/up + SiLU*up
       GemvPhase<TGU, TGU, true, true> ph{};
-      // The first gate/up loads (two streams per wave) are issued after the
-      // activation is staged, not before the barrier: in flight, they delay
-      // the barrier's release by more than their latency saves (0.5-1% per
-      // token at the 7B and 1.5B shapes; the same for the other phases'
-      // smaller first loads costs 1-4%).
-      ph.defer = true;
       ph.prefetch(L.gate_up, wg, nwg, smem);
       bar_wait(p.bar, p.err, nwg, k, p.scalar_poll);
       STAMP(k, 0);

@@ -823,9 +823,6 @@ template <uint32_t TA, uint32_t TB, bool DUAL, bool COH, bool BALANCED = false>
 struct GemvPhase {
   int lane, wave, nw, wg, nwg, wrow0, wrow1, s0, base0;
   bool s0_is_ta;
-  // defer: prefetch() only picks the rows; the first weight loads are issued
-  // after the activation is staged.
-  bool defer = false;
   // The balanced split's partials (set when a.bal and the workgroup's rows
   // lie in one segment).
   float *slots;
@@ -866,14 +863,13 @@ struct GemvPhase {
     slots = BAL && a.bal && one_seg
                 ? reinterpret_cast<float *>(smem + fast_gemv_digit_bytes(a.cols) + fast_gemv_ybuf_bytes(wrow1 - wrow0))
                 : nullptr;
-    if (s0_is_ta && !defer) begin_first(a);
-  }
-  __device__ __forceinline__ void begin_first(const FastGemvArgs &a) {
-    int lo, hi;
-    seg_range(a, s0, base0, lo, hi);
-    const FastSeg Sw = shifted(a.seg[s0], lo - base0);
-    const FastSeg Uw = DUAL ? shifted(a.seg[1], lo - base0) : Sw;
-    A.begin(Sw, Uw, lo, max(lo, hi), wave, nw, a.cols, lane, slots);
+    if (s0_is_ta) {
+      int lo, hi;
+      seg_range(a, s0, base0, lo, hi);
+      const FastSeg Sw = shifted(a.seg[s0], lo - base0);
+      const FastSeg Uw = DUAL ? shifted(a.seg[1], lo - base0) : Sw;
+      A.begin(Sw, Uw, lo, max(lo, hi), wave, nw, a.cols, lane, slots);
+    }
   }
 
   // Row results of a balanced stream: the partials of row i's group summed
@@ -904,7 +900,6 @@ struct GemvPhase {
 #ifdef LLRS_STAMPS
     if (stamp && thread_x() == 0) stamp[1] = wall_clock64();
 #endif
-    if (defer && s0_is_ta) begin_first(a);
     Lds L;
     L.cols = a.cols;
     L.nb4 = a.cols >> 6;
