@@ -180,18 +180,22 @@ LDS_PROBE_MODES = ("read32 conflict-free", "read64 conflict-free", "read128 conf
                    "write128 chunk-major staging, swizzled", "write128 chunk-major staging, plain")
 
 
-def lds_probe(llrs, be, iters: int) -> int:
-    """The LDS access-pattern probe (llrs_debug_lds_probe): each mode once,
-    512 workgroups of 256 threads, `iters` LDS accesses per thread; run under
-    rocprofv3 --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE to read what the
-    counters report for known bank patterns."""
+def lds_probe(llrs, be, iters: int, reps: int = 1) -> int:
+    """The LDS access-pattern probe (llrs_debug_lds_probe): each mode `reps`
+    times, 512 workgroups of 256 threads, `iters` LDS accesses per thread; run
+    under rocprofv3 --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE to read what
+    the counters report for known bank patterns.  With iters 1 the kernels do
+    almost nothing: under rocprofv3 --kernel-trace their durations are the
+    floor of a launch."""
     lib = llrs.lib()
     out = []
     for mode, name in enumerate(LDS_PROBE_MODES):
         t0 = time.perf_counter()
-        llrs._check(lib.llrs_debug_lds_probe(be.handle, mode, 512, iters))
-        dt = time.perf_counter() - t0
-        out.append({"mode": mode, "pattern": name, "blocks": 512, "iters": iters, "ms": round(dt * 1e3, 3)})
+        for _ in range(reps):
+            llrs._check(lib.llrs_debug_lds_probe(be.handle, mode, 512, iters))
+        dt = (time.perf_counter() - t0) / reps
+        out.append({"mode": mode, "pattern": name, "blocks": 512, "iters": iters, "reps": reps,
+                    "ms": round(dt * 1e3, 3)})
         log(f"lds probe mode {mode} ({name}): {dt * 1e3:.2f} ms")
     print(json.dumps({"lds_probe": out}), flush=True)
     return 0
@@ -241,13 +245,16 @@ def gemv_sweep(llrs, be, cpu_reps: int) -> int:
         oracle = Oracle()
         threads = host_threads()
     cases = [("cfg1", QT.Q4K, 8960, 1536, 1)]
+    # The fixed cost of a launch: 64 rows (32 workgroups), a few hundred KB.
+    cases += [("floor", QT.Q4K, 64, 3584, 2), ("floor", QT.Q4K, 64, 18944, 2)]
     for name in ("Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q4K", "Q5K", "Q6K", "F16", "BF16"):
         cases += [("cfg2", QT[name], 18944, 3584, 2), ("cfg2", QT[name], 3584, 18944, 2)]
     out = []
     for cfg, ty, rows, cols, seed in cases:
         data = llrs.blocks.random_tensor_bytes(ty, rows, cols, seed=seed)
         nbytes = len(data)
-        copies = max(2, int(1.2e9 // nbytes) + 1)
+        # Enough copies that the MALL cannot serve a repeat (the floor cases: two).
+        copies = 2 if cfg == "floor" else max(2, int(1.2e9 // nbytes) + 1)
         qt = llrs.QuantTensor(data, (rows, cols), ty)
         ts = [be.upload(qt) for _ in range(copies)]
         x, y = C.c_void_p(), C.c_void_p()
@@ -463,6 +470,8 @@ def main() -> int:
                     help="configs 1 and 2 instead: single GEMVs per type over rotating weight copies")
     ap.add_argument("--lds-probe", type=int, default=0, metavar="ITERS",
                     help="instead: the LDS bank-pattern probe kernels, ITERS accesses per thread")
+    ap.add_argument("--lds-probe-reps", type=int, default=1,
+                    help="--lds-probe: launches of each probe kernel")
     ap.add_argument("--gemv-cpu-reps", type=int, default=20,
                     help="--gemv: host oracle calls per case and path (median; 0 = no CPU timing)")
     ap.add_argument("--load", action="store_true",
@@ -487,7 +496,7 @@ def main() -> int:
     be = llrs.HipBackend(0)
     log(f"backend {be.name()} with {be.threads()} CUs")
     if args.lds_probe:
-        return lds_probe(llrs, be, args.lds_probe)
+        return lds_probe(llrs, be, args.lds_probe, args.lds_probe_reps)
     if args.gemv:
         return gemv_sweep(llrs, be, 0 if args.no_cpu_baseline else args.gemv_cpu_reps)
     if args.load:
