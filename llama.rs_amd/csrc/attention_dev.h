@@ -77,7 +77,11 @@ template <int HD> struct AttnPart {
 // single-chunk items and keeps their code straight-line).
 // EARLY (the persistent kernel): `wait` is the phase barrier, issued after the
 // item's cache loads (rows written by earlier steps); the caller makes sure
-// every wave passes it exactly once.
+// every wave passes it exactly once.  The phase barrier ends in a workgroup
+// barrier that waves reach from different call sites (here, or after their
+// task loop), which pairs up because s_barrier counts waves: so this
+// function contains no workgroup barrier of its own and calls `wait` on
+// every path, before any return.
 struct NoWait {
   __device__ void operator()() const {}
 };
