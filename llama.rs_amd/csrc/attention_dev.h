@@ -10,6 +10,7 @@
 #include "common.h"
 #include "decode.h"
 #include "quant_dev.h"
+#include "wave_dev.h"
 
 namespace llrs {
 
@@ -236,19 +237,17 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
 #pragma unroll
       for (int j = 0; j < n / 2; j++) {
         const float keep = hi ? d[j + n / 2] : d[j], give = hi ? d[j] : d[j + n / 2];
-        d[j] = keep + __shfl_xor(give, n, 64);
+        d[j] = keep + lane_partner(give, n);
       }
     }
-    float sc = d[0] + __shfl_xor(d[0], 1, 64);
+    float sc = d[0] + lane_partner(d[0], 1);
     const bool valid = s0 + srow < s1;
     sc = valid ? sc * a.scale : -INFINITY;
     float ms = sc;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ms = fmaxf(ms, __shfl_xor(ms, o, 64));
+    ms = wave_max(ms);
     const float x = valid ? expf(sc - ms) : 0.f;
     float ls = (lane & 1) ? 0.f : x;  // every row is held by two lanes
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ls += __shfl_xor(ls, o, 64);
+    ls = wave_total(ls);
     float Os[VW], Vss[VW];
 #pragma unroll
     for (int k = 0; k < VW; k++) Os[k] = Vss[k] = 0.f;
@@ -272,8 +271,8 @@ __device__ void attention_item(const AttnArgs &a, int h, int chunk, int pos, flo
     for (int o = VL; o < 64; o <<= 1) {
 #pragma unroll
       for (int k = 0; k < VW; k++) {
-        Os[k] += __shfl_xor(Os[k], o, 64);
-        Vss[k] += __shfl_xor(Vss[k], o, 64);
+        Os[k] += lane_partner(Os[k], o);
+        Vss[k] += lane_partner(Vss[k], o);
       }
     }
     if (sub == 0) {  // one sub-chunk: exactly its own partial
@@ -343,12 +342,10 @@ __device__ void fold_scratch(const AttnArgs &a, const unsigned long long *slots,
     }
     const bool in = lane < nc && mm != -INFINITY;
     float Mr = in ? mm : -INFINITY;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) Mr = fmaxf(Mr, __shfl_xor(Mr, o, 64));
+    Mr = wave_max(Mr);
     const float w = in ? expf(mm - Mr) : 0.f;
     float Lr = w * ll;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) Lr += __shfl_xor(Lr, o, 64);
+    Lr = wave_total(Lr);
     float Rr[VW];
 #pragma unroll
     for (int k = 0; k < VW; k++) Rr[k] = 0.f;

@@ -33,6 +33,7 @@
 #include "common.h"
 #include "gemv.h"
 #include "quant_dev.h"
+#include "wave_dev.h"
 
 namespace llrs {
 
@@ -402,11 +403,7 @@ template <> struct Traits<LLRS_Q5_K> {
   }
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave_total(v); }
 
 // Sum of each of four per-lane values over the wave: returns the total of
 // row ((lane >> 5) << 1 | (lane >> 4) & 1) in lanes 0, 16, 32, 48.
@@ -414,12 +411,12 @@ __device__ __forceinline__ float wave_sum4(const float (&v)[4], int lane) {
   bool hi = lane & 32;
   float s0 = hi ? v[0] : v[2], s1 = hi ? v[1] : v[3];
   float k0 = hi ? v[2] : v[0], k1 = hi ? v[3] : v[1];
-  k0 += __shfl_xor(s0, 32, 64);
-  k1 += __shfl_xor(s1, 32, 64);
+  k0 += lane_partner(s0, 32);
+  k1 += lane_partner(s1, 32);
   bool hb = lane & 16;
-  float k = (hb ? k1 : k0) + __shfl_xor(hb ? k0 : k1, 16, 64);
+  float k = (hb ? k1 : k0) + lane_partner(hb ? k0 : k1, 16);
 #pragma unroll
-  for (int o = 8; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
+  for (int b = 8; b > 0; b >>= 1) k += lane_partner(k, b);
   return k;
 }
 
@@ -533,7 +530,7 @@ __device__ float digitize(const float *__restrict__ x, const float *__restrict__
     xs[s] = scale;
     sx[s] = sum;
     float part = scale * (float)sum;
-    float pair = __shfl_xor(part, 1, 64);
+    float pair = lane_partner(part, 1);
     if ((b & 1) == 0) xsum32[b >> 1] = part + pair;
   }
   if (gain) {
@@ -560,9 +557,9 @@ __device__ __forceinline__ uint32_t total_order_key(float f) {
 // (lane >> 5) ends up in lanes 0 and 32.
 __device__ __forceinline__ float wave_sum2(float v0, float v1, int lane) {
   bool hi = lane & 32;
-  float k = (hi ? v1 : v0) + __shfl_xor(hi ? v0 : v1, 32, 64);
+  float k = (hi ? v1 : v0) + lane_partner(hi ? v0 : v1, 32);
 #pragma unroll
-  for (int o = 16; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
+  for (int b = 16; b > 0; b >>= 1) k += lane_partner(k, b);
   return k;
 }
 
@@ -573,19 +570,19 @@ __device__ __forceinline__ float half_sum4(const float (&v)[4], int lane) {
   bool a = lane & 16;
   float s0 = a ? v[0] : v[2], s1 = a ? v[1] : v[3];
   float k0 = a ? v[2] : v[0], k1 = a ? v[3] : v[1];
-  k0 += __shfl_xor(s0, 16, 64);
-  k1 += __shfl_xor(s1, 16, 64);
+  k0 += lane_partner(s0, 16);
+  k1 += lane_partner(s1, 16);
   bool b = lane & 8;
-  float k = (b ? k1 : k0) + __shfl_xor(b ? k0 : k1, 8, 64);
+  float k = (b ? k1 : k0) + lane_partner(b ? k0 : k1, 8);
 #pragma unroll
-  for (int o = 4; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
+  for (int o = 4; o > 0; o >>= 1) k += lane_partner(k, o);
   return k;
 }
 __device__ __forceinline__ float half_sum2(float v0, float v1, int lane) {
   bool a = lane & 16;
-  float k = (a ? v1 : v0) + __shfl_xor(a ? v0 : v1, 16, 64);
+  float k = (a ? v1 : v0) + lane_partner(a ? v0 : v1, 16);
 #pragma unroll
-  for (int o = 8; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
+  for (int o = 8; o > 0; o >>= 1) k += lane_partner(k, o);
   return k;
 }
 
@@ -748,7 +745,7 @@ __device__ __forceinline__ void SegStream<TY, DUAL, BAL>::run(const Lds &L, Emit
         // gate rows 0, 1 in lane groups 0/8, up rows in 16/24 of each half.
         float v[4] = {acc[0], acc[1], acc2[0], acc2[1]};
         float t = half_sum4(v, lane);
-        float up = __shfl_xor(t, 16, 64);
+        float up = lane_swap16(t);
         if ((lane & 23) == 0) {  // lanes 0, 8, 32, 40
           int r = r0 + ((lane >> 3) & 1);
           if (r < row_hi) out(r, t, up);
@@ -773,7 +770,7 @@ __device__ __forceinline__ void SegStream<TY, DUAL, BAL>::run(const Lds &L, Emit
         // rows 0, 1 of gate and of up: gate sums land in lanes 0/16, up in 32/48.
         float v[4] = {acc[0], acc[1], acc2[0], acc2[1]};
         float t = wave_sum4(v, lane);
-        float up = __shfl_xor(t, 32, 64);
+        float up = lane_swap32(t);
         if ((lane & 47) == 0) {  // lanes 0 and 16
           int r = r0 + ((lane >> 4) & 1);
           if (r < row_hi) out(r, t, up);
