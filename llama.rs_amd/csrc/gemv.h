@@ -93,8 +93,12 @@ size_t fast_gemv_lds_bytes(const FastGemvArgs &a, int grid, int threads = 256);
 // Bytes of a digitised activation of n elements (dig_out / dig_in).
 inline size_t fast_gemv_digits_size(size_t n) { return 2 * n + (n / 16) * 8; }
 // `threads`: 256 or 512 per workgroup (the digitised activation is built
-// once per workgroup and shared by its waves).
-int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s, int threads = 256);
+// once per workgroup and shared by its waves).  `lds_exchange`: row sums
+// through ds_bpermute rather than DPP / permlane swaps, for launches whose
+// waves stream many row steps (the LM head); 256 threads, one weight type,
+// no SwiGLU, no balanced split.
+int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s, int threads = 256,
+                     bool lds_exchange = false);
 // Workgroups for a launch over `rows` x `cols`, never more than the
 // partition units (`part` rows each; 0 = row pairs).
 int fast_gemv_grid(int cu_count, int rows, int cols, bool dual, int part);

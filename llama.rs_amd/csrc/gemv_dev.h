@@ -405,18 +405,34 @@ template <> struct Traits<LLRS_Q5_K> {
 
 __device__ __forceinline__ float wave_sum(float v) { return wave_total(v); }
 
+// The flush's lane exchange: lane_partner's DPP moves and permlane swaps,
+// or, with LDSX, ds_bpermute to the same partner lane (same bits either
+// way).  ds_bpermute goes through the LDS unit and waits on its round trip,
+// but leaves the VALU free: a GEMV whose waves stream many steps (the LM
+// head: ~37 four-row steps per wave) keeps its VALU busy with the next
+// step's dot products meanwhile, where one or two steps per wave wait on
+// the exchange's latency.
+template <bool LDSX>
+__device__ __forceinline__ float flush_partner(float v, int b) {
+  if constexpr (LDSX)
+    return __shfl_xor(v, b == 4 ? 7 : b == 8 ? 15 : b);
+  else
+    return lane_partner(v, b);
+}
+
 // Sum of each of four per-lane values over the wave: returns the total of
 // row ((lane >> 5) << 1 | (lane >> 4) & 1) in lanes 0, 16, 32, 48.
+template <bool LDSX = false>
 __device__ __forceinline__ float wave_sum4(const float (&v)[4], int lane) {
   bool hi = lane & 32;
   float s0 = hi ? v[0] : v[2], s1 = hi ? v[1] : v[3];
   float k0 = hi ? v[2] : v[0], k1 = hi ? v[3] : v[1];
-  k0 += lane_partner(s0, 32);
-  k1 += lane_partner(s1, 32);
+  k0 += flush_partner<LDSX>(s0, 32);
+  k1 += flush_partner<LDSX>(s1, 32);
   bool hb = lane & 16;
-  float k = (hb ? k1 : k0) + lane_partner(hb ? k0 : k1, 16);
+  float k = (hb ? k1 : k0) + flush_partner<LDSX>(hb ? k0 : k1, 16);
 #pragma unroll
-  for (int b = 8; b > 0; b >>= 1) k += lane_partner(k, b);
+  for (int b = 8; b > 0; b >>= 1) k += flush_partner<LDSX>(k, b);
   return k;
 }
 
@@ -555,11 +571,12 @@ __device__ __forceinline__ uint32_t total_order_key(float f) {
 
 // Sum of each of two per-lane values over the wave: the total of row
 // (lane >> 5) ends up in lanes 0 and 32.
+template <bool LDSX = false>
 __device__ __forceinline__ float wave_sum2(float v0, float v1, int lane) {
   bool hi = lane & 32;
-  float k = (hi ? v1 : v0) + lane_partner(hi ? v0 : v1, 32);
+  float k = (hi ? v1 : v0) + flush_partner<LDSX>(hi ? v0 : v1, 32);
 #pragma unroll
-  for (int b = 16; b > 0; b >>= 1) k += lane_partner(k, b);
+  for (int b = 16; b > 0; b >>= 1) k += flush_partner<LDSX>(k, b);
   return k;
 }
 
@@ -616,7 +633,8 @@ template <> struct RowsPerStep<LLRS_Q5_K, false> { static constexpr int value = 
 // BAL: the balanced split may run (the standalone GEMV only: in the decode
 // step its partial-sum pass cost more than the idle waves it fills, and its
 // state costs the persistent kernel registers).
-template <uint32_t TY, bool DUAL, bool BAL = false>
+// LDSX: whole-wave row sums exchange through ds_bpermute (flush_partner).
+template <uint32_t TY, bool DUAL, bool BAL = false, bool LDSX = false>
 struct SegStream {
   using T = Traits<TY>;
   static constexpr int R = RowsPerStep<TY, DUAL>::value;
@@ -694,9 +712,9 @@ struct SegStream {
   __device__ __forceinline__ void run(const Lds &L, Emit &&emit);
 };
 
-template <uint32_t TY, bool DUAL, bool BAL>
+template <uint32_t TY, bool DUAL, bool BAL, bool LDSX>
 template <class Emit>
-__device__ __forceinline__ void SegStream<TY, DUAL, BAL>::run(const Lds &L, Emit &&emit) {
+__device__ __forceinline__ void SegStream<TY, DUAL, BAL, LDSX>::run(const Lds &L, Emit &&emit) {
   using Raw = typename T::Raw;
   constexpr int RU = DUAL ? R : 1;
   float acc[R], acc2[R];
@@ -745,7 +763,7 @@ __device__ __forceinline__ void SegStream<TY, DUAL, BAL>::run(const Lds &L, Emit
         // gate rows 0, 1 in lane groups 0/8, up rows in 16/24 of each half.
         float v[4] = {acc[0], acc[1], acc2[0], acc2[1]};
         float t = half_sum4(v, lane);
-        float up = lane_swap16(t);
+        float up = lane_partner(t, 16);
         if ((lane & 23) == 0) {  // lanes 0, 8, 32, 40
           int r = r0 + ((lane >> 3) & 1);
           if (r < row_hi) out(r, t, up);
@@ -769,20 +787,20 @@ __device__ __forceinline__ void SegStream<TY, DUAL, BAL>::run(const Lds &L, Emit
       if constexpr (DUAL) {
         // rows 0, 1 of gate and of up: gate sums land in lanes 0/16, up in 32/48.
         float v[4] = {acc[0], acc[1], acc2[0], acc2[1]};
-        float t = wave_sum4(v, lane);
-        float up = lane_swap32(t);
+        float t = wave_sum4<LDSX>(v, lane);
+        float up = flush_partner<LDSX>(t, 32);
         if ((lane & 47) == 0) {  // lanes 0 and 16
           int r = r0 + ((lane >> 4) & 1);
           if (r < row_hi) out(r, t, up);
         }
       } else if constexpr (R == 4) {
-        float t = wave_sum4(acc, lane);
+        float t = wave_sum4<LDSX>(acc, lane);
         if ((lane & 15) == 0) {
           int r = r0 + (((lane >> 5) << 1) | ((lane >> 4) & 1));
           if (r < row_hi) out(r, t, 0.f);
         }
       } else {
-        float t = wave_sum2(acc[0], acc[1], lane);
+        float t = wave_sum2<LDSX>(acc[0], acc[1], lane);
         if ((lane & 31) == 0) {
           int r = r0 + (lane >> 5);
           if (r < row_hi) out(r, t, 0.f);
@@ -816,7 +834,7 @@ __device__ __forceinline__ void SegStream<TY, DUAL, BAL>::run(const Lds &L, Emit
 // prefetch() picks the workgroup's rows and issues its first weight loads
 // (they depend on nothing the previous phase writes); finish() stages the
 // activation, streams the rest and runs the epilogue.
-template <uint32_t TA, uint32_t TB, bool DUAL, bool COH, bool BALANCED = false>
+template <uint32_t TA, uint32_t TB, bool DUAL, bool COH, bool BALANCED = false, bool LDSX = false>
 struct GemvPhase {
   int lane, wave, nw, wg, nwg, wrow0, wrow1, s0, base0;
   bool s0_is_ta;
@@ -826,7 +844,7 @@ struct GemvPhase {
   // The balanced split: its own instantiation of the standalone GEMV, for
   // launches that ask for it (its code costs the others registers).
   static constexpr bool BAL = BALANCED && !COH && !DUAL;
-  SegStream<TA, DUAL, BAL> A;
+  SegStream<TA, DUAL, BAL, LDSX> A;
 #ifdef LLRS_STAMPS
   // Timing build only: wall-clock stamps of this workgroup's phase, [1] when
   // the activation is staged, [2] when the weight streaming ends.
@@ -943,7 +961,7 @@ struct GemvPhase {
         seg_range(a, s, base, lo, hi);
         if (lo < hi) {
           const FastSeg Sw = shifted(S, lo - base);
-          SegStream<TB, false, BAL> B;
+          SegStream<TB, false, BAL, LDSX> B;
           B.begin(Sw, Sw, lo, hi, wave, nw, a.cols, lane, slots);
           B.run(L, emitter(lo));
           bal_b = B.bal;

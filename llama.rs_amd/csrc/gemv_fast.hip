@@ -10,11 +10,13 @@ namespace llrs {
 
 namespace {
 
-template <uint32_t TA, uint32_t TB, bool DUAL, bool BAL, int NT>
+// LDSX: row sums through ds_bpermute (the LM head, whose waves stream ~37
+// row steps each); otherwise through DPP and permlane swaps.
+template <uint32_t TA, uint32_t TB, bool DUAL, bool BAL, int NT, bool LDSX = false>
 __global__ __launch_bounds__(NT) void gemv_fast_kernel(FastGemvArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[16];
-  GemvPhase<TA, TB, DUAL, false, BAL> ph;
+  GemvPhase<TA, TB, DUAL, false, BAL, LDSX> ph;
   ph.prefetch(a, blockIdx.x, gridDim.x, smem);
   ph.finish(a, smem, red);
 }
@@ -41,17 +43,28 @@ bool fast_gemv_supports(uint32_t type, size_t cols) {
   }
 }
 
+// The ds_bpermute variant is built for single-type, single-matrix launches
+// in 256-thread workgroups (the LM head's shape) only.
 template <uint32_t TA, uint32_t TB, bool DUAL, bool BAL = false>
-static void launch_one(const FastGemvArgs &args, int grid, int threads, size_t lds, hipStream_t s) {
-  if (threads == 512)
+static void launch_one(const FastGemvArgs &args, int grid, int threads, bool ldsx, size_t lds, hipStream_t s) {
+  if (threads == 512) {
     hipLaunchKernelGGL((gemv_fast_kernel<TA, TB, DUAL, BAL, 512>), dim3(grid), dim3(512), lds, s, args);
-  else
+  } else if constexpr (TA == TB && !DUAL && !BAL) {
+    if (ldsx)
+      hipLaunchKernelGGL((gemv_fast_kernel<TA, TB, DUAL, BAL, 256, true>), dim3(grid), dim3(256), lds, s, args);
+    else
+      hipLaunchKernelGGL((gemv_fast_kernel<TA, TB, DUAL, BAL, 256>), dim3(grid), dim3(256), lds, s, args);
+  } else {
     hipLaunchKernelGGL((gemv_fast_kernel<TA, TB, DUAL, BAL, 256>), dim3(grid), dim3(256), lds, s, args);
+  }
 }
 
-int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s, int threads) {
+int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s, int threads, bool lds_exchange) {
   if (grid <= 0) return set_error(LLRS_E_INVALID, "GEMV grid must be positive");
   if (threads != 256 && threads != 512) return set_error(LLRS_E_INVALID, "GEMV blocks are 256 or 512 threads");
+  if (lds_exchange && (threads != 256 || args.epi == kEpiSwiGlu || args.bal ||
+                       args.seg[0].type != args.seg[args.nseg - 1].type))
+    return set_error(LLRS_E_UNSUPPORTED, "ds_bpermute row sums are built for 256-thread single-type launches");
   if (args.dig_out && (args.part != 16 || args.rows % 64))
     return set_error(LLRS_E_INVALID, "a digitised output needs 16-row partitions of a multiple of 64 rows");
   if (args.part && args.part != 2 && args.part != 16)
@@ -66,7 +79,7 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s, int thre
       return set_error(LLRS_E_UNSUPPORTED, "gate and up must share a type");
 #define DUAL1(A)                                  \
   if (ta == A) {                                  \
-    launch_one<A, A, true>(args, grid, threads, lds, s);   \
+    launch_one<A, A, true>(args, grid, threads, lds_exchange, lds, s);   \
     LLRS_HIP(hipGetLastError());                  \
     return LLRS_OK;                               \
   }
@@ -76,7 +89,7 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s, int thre
   }
 #define PAIR(A, B)                                 \
   if (ta == A && tb == B) {                        \
-    launch_one<A, B, false>(args, grid, threads, lds, s);   \
+    launch_one<A, B, false>(args, grid, threads, lds_exchange, lds, s);   \
     LLRS_HIP(hipGetLastError());                   \
     return LLRS_OK;                                \
   }
@@ -84,9 +97,9 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s, int thre
 #define SAME(A)                                          \
   if (ta == A && tb == A) {                              \
     if (args.bal)                                        \
-      launch_one<A, A, false, true>(args, grid, threads, lds, s); \
+      launch_one<A, A, false, true>(args, grid, threads, lds_exchange, lds, s); \
     else                                                 \
-      launch_one<A, A, false>(args, grid, threads, lds, s);       \
+      launch_one<A, A, false>(args, grid, threads, lds_exchange, lds, s);       \
     LLRS_HIP(hipGetLastError());                         \
     return LLRS_OK;                                      \
   }

@@ -724,7 +724,7 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
   if (which < 0 || which >= P_COUNT) return set_error(LLRS_E_INVALID, "unknown projection %d", which);
   if (use_fast(m, l, which)) {
     const FastGemvArgs a = projection_args(m, kv, l, which);
-    return launch_gemv_fast(a, fast_grid(m, a, which == P_GATE_UP), s);
+    return launch_gemv_fast(a, fast_grid(m, a, which == P_GATE_UP), s, 256, which == P_LM_HEAD);
   }
   if (which == P_LM_HEAD) {
     LLRS_TRY(launch_rmsnorm(kv->residual, m->norm, kv->hidden, H, eps, s));
