@@ -99,6 +99,9 @@ inline size_t fast_gemv_digits_size(size_t n) { return 2 * n + (n / 16) * 8; }
 // no SwiGLU, no balanced split.
 int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s, int threads = 256,
                      bool lds_exchange = false);
+// Whether rows of `cols` columns of `type` have at most 32 units of work, so
+// that each 32-lane half of a wave takes its own row group (packed rows).
+bool fast_gemv_packed(uint32_t type, int cols);
 // Workgroups for a launch over `rows` x `cols`, never more than the
 // partition units (`part` rows each; 0 = row pairs).
 int fast_gemv_grid(int cu_count, int rows, int cols, bool dual, int part);

@@ -112,6 +112,11 @@ int launch_gemv_fast(const FastGemvArgs &args, int grid, hipStream_t s, int thre
   return set_error(LLRS_E_UNSUPPORTED, "no tuned GEMV for %s + %s", type_name(ta), type_name(tb));
 }
 
+bool fast_gemv_packed(uint32_t type, int cols) {
+  const int per_unit = (type == LLRS_Q4_K || type == LLRS_Q5_K || type == LLRS_Q6_K) ? 64 : 32;
+  return cols / per_unit <= 32;
+}
+
 int fast_gemv_grid(int cu_count, int rows, int cols, bool dual, int part) {
   // Measured on the decode shapes: one workgroup per CU for rows of <= 8K
   // columns, two for longer rows (more loads in flight per row), three for the

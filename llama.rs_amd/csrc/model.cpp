@@ -724,7 +724,13 @@ static int launch_projection(llrs_model *m, llrs_kv *kv, size_t l, int which, hi
   if (which < 0 || which >= P_COUNT) return set_error(LLRS_E_INVALID, "unknown projection %d", which);
   if (use_fast(m, l, which)) {
     const FastGemvArgs a = projection_args(m, kv, l, which);
-    return launch_gemv_fast(a, fast_grid(m, a, which == P_GATE_UP), s, 256, which == P_LM_HEAD);
+    if (which == P_LM_HEAD) {
+      // Packed rows (1,536 columns of Q4_K, 896 of Q8_0): eight waves per
+      // workgroup; longer rows: four, with the row sums through ds_bpermute.
+      const bool packed = fast_gemv_packed(a.seg[0].type, a.cols);
+      return launch_gemv_fast(a, fast_grid(m, a), s, packed ? 512 : 256, !packed);
+    }
+    return launch_gemv_fast(a, fast_grid(m, a, which == P_GATE_UP), s);
   }
   if (which == P_LM_HEAD) {
     LLRS_TRY(launch_rmsnorm(kv->residual, m->norm, kv->hidden, H, eps, s));
