@@ -28,6 +28,7 @@
 #include <cstring>
 
 #include "common.h"
+#include "wave_dev.h"
 #include "prefill.h"
 #include "quant_dev.h"
 
@@ -556,7 +557,7 @@ __device__ __forceinline__ void swiglu_tile(const PrefillGemmArgs &g, const f32x
         for (int e = 0; e < 4; e++) {
           float v = xsum[q][e];
 #pragma unroll
-          for (int m = 8; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+          for (int b = 1; b < 16; b <<= 1) v += lane_partner(v, b);
           const int t = tb + 16 * i + 4 * (lane >> 4) + e, f = f0 + 32 * q;
           if ((lane & 15) == 0 && t < g.t && f < g.dual_rows)
             split_f16(v, g.xso[(size_t)t * g.ldxso + (f >> 5)], g.xso_lo[(size_t)t * g.ldxso + (f >> 5)]);
@@ -859,7 +860,7 @@ __global__ void embed_rows_kernel(const uint8_t *__restrict__ emb, uint32_t ty, 
 // columns 32 s ... 32 s + 31 (a 32-lane half-wave of one pass), as f16 pairs.
 __device__ __forceinline__ void half_wave_xsum(float v, int col, f16 *xs, f16 *xs_lo) {
 #pragma unroll
-  for (int m = 16; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  for (int b = 1; b < 32; b <<= 1) v += lane_partner(v, b);
   if ((threadIdx.x & 31) == 0) split_f16(v, xs[col >> 5], xs_lo[col >> 5]);
 }
 
@@ -888,8 +889,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_f16_kernel(const float *__re
   } else {
     for (int i = threadIdx.x; i < H; i += 256) s += xr[i] * xr[i];
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  s = wave_total(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
   __syncthreads();
   const float tot = red[0] + red[1] + red[2] + red[3];
@@ -1036,8 +1036,8 @@ __global__ __launch_bounds__(256, 3) void attention_tile_kernel(const float *__r
       sc[r] = key0 + 4 * g + r <= pq ? st[r] * scale : -INFINITY;
       mc = fmaxf(mc, sc[r]);
     }
-    mc = fmaxf(mc, __shfl_xor(mc, 16, 64));
-    mc = fmaxf(mc, __shfl_xor(mc, 32, 64));
+    mc = fmaxf(mc, lane_partner(mc, 16));
+    mc = fmaxf(mc, lane_partner(mc, 32));
     const float Mn = fmaxf(M, mc);
     const bool live = Mn != -INFINITY;
     const float alpha = live ? expf(M - Mn) : 1.f;
@@ -1057,8 +1057,8 @@ __global__ __launch_bounds__(256, 3) void attention_tile_kernel(const float *__r
     }
     if (b + 4 < nb) load_v(key0 + 64);
   }
-  L += __shfl_xor(L, 16, 64);
-  L += __shfl_xor(L, 32, 64);
+  L += lane_partner(L, 16);
+  L += lane_partner(L, 32);
   if (g == 0) {
     sm[wave][i] = M;
     sl[wave][i] = L;
@@ -1241,8 +1241,8 @@ __global__ __launch_bounds__(256, 3) void attention_f16_kernel(const float *__re
       sc[r] = key0 + 4 * g + r <= pq ? st[r] * scale : -INFINITY;
       mc = fmaxf(mc, sc[r]);
     }
-    mc = fmaxf(mc, __shfl_xor(mc, 16, 64));
-    mc = fmaxf(mc, __shfl_xor(mc, 32, 64));
+    mc = fmaxf(mc, lane_partner(mc, 16));
+    mc = fmaxf(mc, lane_partner(mc, 32));
     const float Mn = fmaxf(M, mc);
     const bool live = Mn != -INFINITY;
     const float alpha = live ? expf(M - Mn) : 1.f;
@@ -1268,8 +1268,8 @@ __global__ __launch_bounds__(256, 3) void attention_f16_kernel(const float *__re
     }
     if (b + 4 < nb) load_v(key0 + 64);
   }
-  L += __shfl_xor(L, 16, 64);
-  L += __shfl_xor(L, 32, 64);
+  L += lane_partner(L, 16);
+  L += lane_partner(L, 32);
   if (g == 0) {
     sm[wave][i] = M;
     sl[wave][i] = L;
