@@ -7,7 +7,7 @@
 // Layout: one wave64 per output row; lane l handles the 32-element units
 // l, l+64, ... of the row (a unit is a Q4_0..Q8_0 block, a K-quant sub-block,
 // or 32 consecutive F32/F16/BF16 elements), decodes them in registers and
-// accumulates in f32; a butterfly shuffle reduces the wave.  This path covers
+// accumulates in f32; DPP moves and permlane swaps reduce the wave.  This path covers
 // all types and shapes; the hot types of the decode step use the tuned
 // kernels in gemv_fast.hip.
 #include <hip/hip_runtime.h>
@@ -15,14 +15,11 @@
 #include "common.h"
 #include "gemv.h"
 #include "quant_dev.h"
+#include "wave_dev.h"
 
 namespace llrs {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave_total(v); }
 
 __device__ __forceinline__ float dot32(const float (&w)[32], const float *x) {
   const float4 *x4 = reinterpret_cast<const float4 *>(x);
