@@ -101,8 +101,10 @@ __device__ void bar_wait(unsigned *bar, unsigned *err, int nwg, unsigned k, bool
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const unsigned target = k * (unsigned)nwg;
-    const unsigned long long t0 = wall_clock64();
-    while (true) {
+    // The clock read is a scalar memory access of its own, so the 20 ms
+    // limit is checked every 16th poll, from the first check on.
+    unsigned long long t0 = 0;
+    for (unsigned it = 1;; it++) {
       unsigned v;
       if (scalar) {
         v = bar_sum_scalar(bar);
@@ -112,11 +114,16 @@ __device__ void bar_wait(unsigned *bar, unsigned *err, int nwg, unsigned k, bool
         for (int o = 1; o < kBarCounters; o <<= 1) v += __shfl_xor(v, o, 64);
       }
       if (__builtin_amdgcn_readfirstlane(v) >= target) break;
-      __builtin_amdgcn_s_sleep(1);
-      if (wall_clock64() - t0 > 2000000ull) {  // the 100 MHz wall clock: 20 ms
-        if (lane == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
+      if ((it & 15) == 0) {
+        const unsigned long long t = wall_clock64();  // the 100 MHz wall clock
+        if (!t0) {
+          t0 = t;
+        } else if (t - t0 > 2000000ull) {  // 20 ms
+          if (lane == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
       }
+      __builtin_amdgcn_s_sleep(1);
     }
   }
   __syncthreads();
